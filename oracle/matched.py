@@ -1,0 +1,194 @@
+"""Restatement of the reference's matched split-KV protocol (test infrastructure).
+
+Follows src/paged_decode/matched_splitkv.py of the reference repository:
+
+* ``normalized_partition`` restates ``_normalized_partition`` (matched_splitkv.py:52-98)
+  For each (b, kv head kh, split p): the partition is [p*T, min((p+1)*T, len)),
+  split into TILE-token tiles that are walked in REVERSE order (:71).  Per tile:
+  raw scores s = q . k (bf16 inputs, fp32 accumulation, unscaled, :77);
+  m' = max(m, rowmax s) (:78); alpha = exp2((m - m') * c) (:79);
+  p = exp2(fma(s, c, -m' * c)) with c = scale * log2(e) (:80);
+  four fp32 denominator lanes, scaled by alpha, then for each 8-column block
+  lane j adds column 8b+2j and then column 8b+2j+1 (:81-85);
+  acc = acc * alpha + bf16(p) @ v (:86).
+  Epilogue: denom = (s0 + s2) + (s1 + s3); partial = acc * (1 / denom) (denom
+  0 -> 1); lse = fma(m, scale, ln denom), or -inf for an empty partition (:92-98).
+* ``lse_merge`` restates ``_lse_merge`` (matched_splitkv.py:101-127)
+  M = max lse over lane-strided partial maxima (-inf -> 0); S = sum exp(lse - M)
+  over LANES partial sums then a tree sum; L = ln S + M (S == 0 -> +inf);
+  out = sum_p fma(exp(lse_p - L), partial_p, acc) sequentially in p order,
+  rounded to bf16.
+
+What pins it (tests/test_oracle_matched.py):
+* an independent float64 formulation that replaces the running maximum of the
+  reverse walk by per-tile suffix maxima (same mathematics, different order),
+  compared at one bf16 ulp; a forward walk or a dropped bf16(p) fails it;
+* the dense oracle (itself pinned to the reference's vectors) at the
+  reference's 2e-2 gate, and error magnitudes of the same order as the
+  reference's published D256 evidence (evidence/correctness.json: max-abs about
+  1.2e-3, RMSE about 1.5e-4 vs the fp32 gather on N(0,1) inputs);
+* invariants: one live partition -> the merge returns that normalized partial
+  exactly; an all-empty row -> exact zeros; x80 logits stay finite; the LSE
+  equals a float64 log-sum-exp of the partition's scaled scores within 1e-5.
+Parity unpinned: the exact float32 rounding of the reference's GPU
+instructions (ex2/lg2/rcp approximations, MMA accumulation order, the ptxas
+FMA contraction of the first denominator add, FlashAttention peer equality);
+those are below float32 noise and far below the bf16 output tolerance.
+"""
+import numpy as np
+
+from .numerics import (F32, LOG2E, bf16_round, exp2_32, exp32, fma32, ln32,
+                       next_pow2)
+
+PAGE_SIZE = 256
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile, scale=None):
+    """Returns (partials [B,Hq,S,D] f32, lse [B,Hq,S] f32)."""
+    q = np.asarray(q, dtype=F32)
+    B, Hq, D = q.shape
+    Hkv = k.shape[2]
+    G = Hq // Hkv
+    scale = D ** -0.5 if scale is None else float(scale)
+    s32 = F32(scale)
+    c = F32(scale * LOG2E)                  # SCALE_LOG2, matched_splitkv.py:363
+    T = int(tokens_per_split)
+    partials = np.zeros((B, Hq, splits, D), dtype=F32)
+    lse = np.full((B, Hq, splits), -np.inf, dtype=F32)
+    table = np.asarray(table)
+    for b in range(B):
+        length = int(lengths[b])
+        qb = q[b].reshape(Hkv, G, D)
+        for p in range(splits):
+            start = p * T
+            end = min((p + 1) * T, length)
+            count = max(_cdiv(end - start, tile), 0)
+            m = np.full((Hkv, G), -np.inf, dtype=F32)
+            lanes = np.zeros((Hkv, G, 4), dtype=F32)
+            acc = np.zeros((Hkv, G, D), dtype=F32)
+            for i in range(count):
+                t0 = start + (count - 1 - i) * tile          # reverse walk (:71)
+                nv = min(tile, end - t0)
+                pos = t0 + np.arange(nv)
+                pages = table[b, pos // PAGE_SIZE]
+                kt = k[pages, pos % PAGE_SIZE].astype(F32)   # [nv, Hkv, D]
+                vt = v[pages, pos % PAGE_SIZE].astype(F32)
+                s = np.full((Hkv, G, tile), -np.inf, dtype=F32)
+                s[..., :nv] = np.matmul(qb, kt.transpose(1, 2, 0))
+                with np.errstate(invalid="ignore"):
+                    m_next = np.maximum(m, s.max(axis=-1))
+                    alpha = exp2_32((m - m_next) * c)
+                    p_ = exp2_32(fma32(s, c, (-(m_next * c))[..., None]))
+                lanes = (lanes * alpha[..., None]).astype(F32)
+                for blk in range(tile // 8):
+                    lanes = (lanes + p_[..., 8 * blk:8 * blk + 8:2]).astype(F32)
+                    lanes = (lanes + p_[..., 8 * blk + 1:8 * blk + 8:2]).astype(F32)
+                pv = np.matmul(bf16_round(p_[..., :nv]), vt.transpose(1, 0, 2))
+                acc = (acc * alpha[..., None] + pv).astype(F32)
+                m = m_next
+            denom = ((lanes[..., 0] + lanes[..., 2]) + (lanes[..., 1] + lanes[..., 3])).astype(F32)
+            safe = np.where(denom > 0, denom, F32(1)).astype(F32)
+            partials[b, :, p] = (acc * (F32(1) / safe)[..., None]).reshape(Hq, D)
+            with np.errstate(invalid="ignore"):
+                lse_p = np.where(denom > 0, fma32(m, s32, ln32(safe)), F32(-np.inf))
+            lse[b, :, p] = lse_p.reshape(Hq)
+    return partials, lse
+
+
+def _tree_sum(x):
+    x = np.asarray(x, dtype=F32)
+    while x.shape[-1] > 1:
+        half = x.shape[-1] // 2
+        x = (x[..., :half] + x[..., half:]).astype(F32)
+    return x[..., 0]
+
+
+def lse_merge(partials, lse, lse_lanes):
+    """Returns the bf16-rounded output [B, Hq, D] as float32 values."""
+    B, Hq, S, D = partials.shape
+    pad = next_pow2(S)
+    lanes = int(lse_lanes)
+    vals = np.full((B, Hq, pad), -np.inf, dtype=F32)
+    vals[..., :S] = lse
+    local_max = np.full((B, Hq, lanes), -np.inf, dtype=F32)
+    for j in range(pad // lanes):
+        local_max = np.maximum(local_max, vals[..., j * lanes:(j + 1) * lanes])
+    mx = local_max.max(axis=-1)
+    mx = np.where(mx == -np.inf, F32(0), mx).astype(F32)
+    local_sum = np.zeros((B, Hq, lanes), dtype=F32)
+    for j in range(pad // lanes):
+        local_sum = (local_sum + exp32(vals[..., j * lanes:(j + 1) * lanes] - mx[..., None])).astype(F32)
+    total = _tree_sum(local_sum)
+    with np.errstate(invalid="ignore"):
+        logsum = np.where(total > 0, ln32(np.where(total > 0, total, F32(1))) + mx,
+                          F32(np.inf)).astype(F32)
+    acc = np.zeros((B, Hq, D), dtype=F32)
+    with np.errstate(invalid="ignore"):
+        for p in range(S):
+            w = exp32(lse[..., p] - logsum)
+            acc = fma32(w[..., None], partials[..., p, :], acc)
+    return bf16_round(acc)
+
+
+def matched_decode(q, k, v, table, lengths, splits, tokens_per_split, tile, lse_lanes, scale=None):
+    """Full matched operator: returns (out_bf16_as_f32, partials, lse)."""
+    partials, lse = normalized_partition(q, k, v, table, lengths, splits, tokens_per_split,
+                                         tile, scale)
+    return lse_merge(partials, lse, lse_lanes), partials, lse
+
+
+def suffix_max_decode(q, k, v, table, lengths, splits, tokens_per_split, tile, scale=None):
+    """Independent float64 formulation of the same protocol, used to pin the oracle.
+
+    Instead of a running maximum over a reverse tile walk, every tile i of a
+    partition takes M_i = max of the scores at positions >= the tile's start
+    (a suffix maximum at tile granularity).  p is computed in float64, rounded to
+    float32 and then to bf16 for the numerator; the denominator uses the
+    unrounded p.  All sums are float64, merged with a float64 log-sum-exp.
+    Returns the bf16-rounded output [B, Hq, D] as float32 values.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    B, Hq, D = q.shape
+    Hkv = k.shape[2]
+    G = Hq // Hkv
+    scale = D ** -0.5 if scale is None else float(scale)
+    c = scale * LOG2E
+    out = np.zeros((B, Hq, D), dtype=np.float64)
+    for b in range(B):
+        length = int(lengths[b])
+        num_parts, lse_parts = [], []
+        for p in range(splits):
+            start, end = p * tokens_per_split, min((p + 1) * tokens_per_split, length)
+            if end <= start:
+                continue
+            pos = np.arange(start, end)
+            pages = np.asarray(table)[b, pos // PAGE_SIZE]
+            kt = k[pages, pos % PAGE_SIZE].astype(np.float64)      # [n, Hkv, D]
+            vt = v[pages, pos % PAGE_SIZE].astype(np.float64)
+            kh = np.repeat(np.arange(Hkv), G)
+            s = np.einsum("hd,nhd->hn", q[b], kt[:, kh])           # [Hq, n]
+            tile_of = (pos - start) // tile
+            n_tiles = tile_of[-1] + 1
+            tile_max = np.stack([s[:, tile_of == t].max(axis=1) for t in range(n_tiles)], 1)
+            suffix = np.maximum.accumulate(tile_max[:, ::-1], axis=1)[:, ::-1]
+            m_tok = suffix[:, tile_of]                              # [Hq, n]
+            p64 = np.exp2(s * c - m_tok * c)
+            pb = bf16_round(p64.astype(np.float32)).astype(np.float64)
+            m_fin = suffix[:, 0]
+            w = np.exp2((m_tok - m_fin[:, None]) * c)               # rescale to the final max
+            num = np.einsum("hn,nhd->hd", pb * w, vt[:, kh])
+            den = (p64 * w).sum(axis=1)
+            num_parts.append(num / den[:, None])
+            lse_parts.append(m_fin * scale + np.log(den))
+        if not num_parts:
+            continue
+        lse_arr = np.stack(lse_parts, 1)                            # [Hq, P]
+        top = lse_arr.max(axis=1, keepdims=True)
+        logsum = np.log(np.exp(lse_arr - top).sum(axis=1, keepdims=True)) + top
+        weights = np.exp(lse_arr - logsum)
+        out[b] = np.einsum("hp,phd->hd", weights, np.stack(num_parts, 0))
+    return bf16_round(out.astype(np.float32))
