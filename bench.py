@@ -1,0 +1,315 @@
+"""Paged decode benchmark on one MI355X.
+
+Default workload: matched split-KV decode (partition + LSE merge), B=1, Hq=16,
+Hkv=4, D=256, page 256, context 2064 (table capacity 2112), bf16 N(0,1)
+synthetic Q/K/V, pages in a seeded random physical order, the planner's plan
+for the device's CU count.  A step is one operator call (both kernels); the
+K timed steps run as replays of a hipGraph that unrolls 128 calls, with the
+inputs resident in HBM.
+
+Printed: one JSON line with value = achieved algorithmic TB/s of the full call,
+a roofline object for the partition kernel (timed alone with HIP events on its
+launch stream), the CPU baseline (NumPy restatement of the reference CPU path
+on the host cores) and extra measurements (context 528, 1024-token partitions,
+the batch-64 bandwidth sweep over a 200 GB page pool).
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "paged-decode-lab_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_TBPS = 8.0            # MI355X HBM3E
+UNROLL = 128               # calls per captured graph (reference convention)
+PAGE = 256
+
+
+def algorithmic_bytes(lengths, batch, hq, hkv, dim, with_output=True):
+    """Bytes the operator must move: K+V rows, Q, output, live table entries, lengths."""
+    kv = sum(int(n) for n in lengths) * hkv * dim * 2 * 2
+    q = batch * hq * dim * 2
+    out = batch * hq * dim * 2 if with_output else 0
+    table = sum((int(n) + PAGE - 1) // PAGE for n in lengths) * 4
+    return kv + q + out + table + batch * 4
+
+
+def make_inputs(torch, batch, hq, hkv, dim, capacity, lengths, seed, pool_pages=None):
+    """Seeded synthetic inputs; pages scattered over a pool of ``pool_pages`` pages."""
+    dev = torch.device("cuda")
+    width = (capacity + PAGE - 1) // PAGE
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    live = [(int(n) + PAGE - 1) // PAGE for n in lengths]
+    pool = pool_pages or batch * width
+    physical = torch.randperm(pool, device=dev, generator=gen)[: sum(live)]
+    table = torch.full((batch, width), -1, dtype=torch.int32, device=dev)
+    offset = 0
+    for b, n in enumerate(live):
+        table[b, :n] = physical[offset:offset + n].to(torch.int32)
+        offset += n
+    k = torch.empty((pool, PAGE, hkv, dim), dtype=torch.bfloat16, device=dev)
+    v = torch.empty_like(k)
+    if pool_pages is None:
+        k.normal_(generator=gen)
+        v.normal_(generator=gen)
+    else:  # initialize only the live pages of a large pool
+        idx = physical.long()
+        for chunk in torch.split(idx, 1024):
+            k[chunk] = torch.randn((len(chunk), PAGE, hkv, dim), generator=gen, device=dev,
+                                   dtype=torch.bfloat16)
+            v[chunk] = torch.randn((len(chunk), PAGE, hkv, dim), generator=gen, device=dev,
+                                   dtype=torch.bfloat16)
+    q = torch.randn((batch, hq, dim), generator=gen, device=dev, dtype=torch.bfloat16)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    return q, k, v, table, lens
+
+
+def graph_time_us(torch, fn, calls, unroll=UNROLL, warmup=3):
+    """Microseconds per call for ``calls`` calls replayed from a graph of ``unroll`` calls."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    unroll = max(1, min(unroll, calls))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(unroll):
+            fn()
+    rest = calls % unroll
+    tail = None
+    if rest:
+        tail = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(tail):
+            for _ in range(rest):
+                fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(cur)
+    for _ in range(calls // unroll):
+        graph.replay()
+    if tail is not None:
+        tail.replay()
+    end.record(cur)
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / calls
+
+
+def reference_protocol_us(torch, fn, rounds=5, replays=20):
+    """Reference convention: 128-call graph, 20 replays, median of 5 rounds; t32 vs t128."""
+    from paged_decode.benchmark_protocol import convergence_delta
+    t128 = sorted(graph_time_us(torch, fn, replays * 128, 128) for _ in range(rounds))[rounds // 2]
+    t32 = sorted(graph_time_us(torch, fn, replays * 32, 32) for _ in range(rounds))[rounds // 2]
+    return t128, t32, convergence_delta(t32, t128)
+
+
+def matched_case(torch, batch, hq, hkv, dim, capacity, lengths, seed, num_splits=0,
+                 pool_pages=None):
+    from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
+    from paged_decode.spec import DecodeSpec
+    from paged_decode import _native
+    spec = DecodeSpec(batch, hq, hkv, dim, capacity)
+    res = allocate_matched_resources(spec, "cuda", num_splits=num_splits)
+    q, k, v, table, lens = make_inputs(torch, batch, hq, hkv, dim, capacity, lengths, seed,
+                                       pool_pages)
+    plan = res.plan
+    scale = dim ** -0.5
+
+    def full():
+        matched_decode(q, k, v, table, lens, resources=res)
+
+    def partition():
+        _native.partition(q, k, v, table, lens, res.partials, res.lse, hkv, plan.splits,
+                          plan.tokens_per_split, plan.tile_tokens, scale)
+
+    def merge():
+        _native.lse_merge(res.partials, res.lse, res.out, plan.lse_lanes)
+
+    return dict(spec=spec, plan=plan, full=full, partition=partition, merge=merge,
+                tensors=(q, k, v, table, lens), res=res)
+
+
+def fixed_partition_case(torch, case, part_tokens=1024):
+    """The same kernels with fixed ``part_tokens`` partitions (splits = ceil(cap / part))."""
+    from paged_decode import _native
+    q, k, v, table, lens = case["tensors"]
+    spec = case["spec"]
+    splits = -(-spec.table_width * PAGE // part_tokens)
+    partials = torch.empty((spec.max_batch, spec.num_heads, splits, spec.head_dim),
+                           device="cuda", dtype=torch.float32)
+    lse = torch.empty((spec.max_batch, spec.num_heads, splits), device="cuda",
+                      dtype=torch.float32)
+    out = torch.empty((spec.max_batch, spec.num_heads, spec.head_dim), device="cuda",
+                      dtype=torch.bfloat16)
+    lanes = min(1 << (splits - 1).bit_length(), 32 if spec.head_dim % 128 == 0 else 16)
+
+    def full():
+        _native.partition(q, k, v, table, lens, partials, lse, spec.num_kv_heads, splits,
+                          part_tokens, 16384 // spec.head_dim, spec.head_dim ** -0.5)
+        _native.lse_merge(partials, lse, out, lanes)
+    return full, splits
+
+
+CPU_SNIPPET = r"""
+import json, os, sys, time
+sys.path.insert(0, {root!r})
+import numpy as np
+from oracle import reference as R
+rng = np.random.default_rng(20261105)
+ctx, hq, hkv, dim, budget = {ctx}, 16, 4, 256, {budget}
+width = (ctx + 255) // 256
+table = rng.permutation(width).reshape(1, width).astype(np.int32)
+bf = lambda x: ((x.view(np.uint32).astype(np.uint64) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+k = bf(rng.normal(size=(width, 256, hkv, dim)).astype(np.float32))
+v = bf(rng.normal(size=k.shape).astype(np.float32))
+q = bf(rng.normal(size=(1, hq, dim)).astype(np.float32))
+lens = np.array([ctx], dtype=np.int32)
+R.streaming_reference(q, k, v, table, lens, split=True)          # warmup
+times, t_end = [], time.perf_counter() + budget
+while len(times) < 5 or time.perf_counter() < t_end:
+    t0 = time.perf_counter()
+    R.streaming_reference(q, k, v, table, lens, split=True)
+    times.append(time.perf_counter() - t0)
+times.sort()
+print(json.dumps(dict(us=times[len(times) // 2] * 1e6, calls=len(times))))
+"""
+
+
+def cpu_baseline(ctx, threads, budget):
+    env = dict(os.environ)
+    env["OPENBLAS_NUM_THREADS"] = str(threads)
+    env["OMP_NUM_THREADS"] = str(threads)
+    code = CPU_SNIPPET.format(root=ROOT, ctx=ctx, budget=budget)
+    res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=600)
+    if res.returncode:
+        raise RuntimeError(res.stderr[-2000:])
+    return json.loads(res.stdout.strip().splitlines()[-1])
+
+
+def bandwidth_sweep(torch, seed=64, calls=20):
+    """Batch 64, Hq 32, Hkv 8, D 128, lengths U[1, 32768], pages scattered over ~200 GB."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(1, 32769, size=64).tolist()
+    page_bytes = PAGE * 8 * 128 * 2
+    free, _ = torch.cuda.mem_get_info()
+    pool_pages = int(100e9 // page_bytes)          # 100 GB of K pages + 100 GB of V pages
+    if 2 * pool_pages * page_bytes > 0.9 * free:
+        pool_pages = int(0.4 * free // page_bytes)
+    case = matched_case(torch, 64, 32, 8, 128, 32768, lengths, seed, pool_pages=pool_pages)
+    us = graph_time_us(torch, case["full"], calls, unroll=4, warmup=2)
+    part_us = graph_time_us(torch, case["partition"], calls, unroll=4, warmup=1)
+    nbytes = algorithmic_bytes(lengths, 64, 32, 8, 128)
+    result = dict(workload="bandwidth sweep B=64 Hq=32 Hkv=8 D=128 len~U[1,32768]",
+                  pool_gb=round(2 * pool_pages * page_bytes / 1e9, 1),
+                  plan=f"{case['plan'].splits}x{case['plan'].tokens_per_split}",
+                  algorithmic_bytes=nbytes, us_per_call=round(us, 2),
+                  tbps=round(nbytes / us / 1e6, 3), pct_peak=round(100 * nbytes / us / 1e6 / PEAK_TBPS, 1),
+                  partition_us=round(part_us, 2),
+                  partition_tbps=round(algorithmic_bytes(lengths, 64, 32, 8, 128, False) / part_us / 1e6, 3))
+    del case
+    torch.cuda.empty_cache()
+    return result
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2560)
+    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--ctx", type=int, default=2064)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the extra measurements")
+    ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU run")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the operator has no multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from paged_decode import _native
+    _native.lib()
+
+    ctx, capacity = args.ctx, max(2112, args.ctx)
+    case = matched_case(torch, 1, 16, 4, 256, capacity, [ctx], 20261105)
+    plan = case["plan"]
+    for _ in range(args.warmup):
+        case["full"]()
+    torch.cuda.synchronize()
+    us = graph_time_us(torch, case["full"], args.steps)
+    part_us = graph_time_us(torch, case["partition"], args.steps)
+    merge_us = graph_time_us(torch, case["merge"], args.steps)
+    nbytes = algorithmic_bytes([ctx], 1, 16, 4, 256)
+    part_bytes = algorithmic_bytes([ctx], 1, 16, 4, 256, with_output=False)
+    tbps = nbytes / us / 1e6
+    part_tbps = part_bytes / part_us / 1e6
+
+    extra = {"us_per_call": round(us, 3), "pct_peak": round(100 * tbps / PEAK_TBPS, 2),
+             "partition_us": round(part_us, 3), "merge_us": round(merge_us, 3),
+             "algorithmic_bytes": nbytes,
+             "plan": f"{plan.splits} splits x {plan.tokens_per_split} tokens (sm_count {plan.sm_count})"}
+    if not args.no_sweep:
+        t128, t32, delta = reference_protocol_us(torch, case["full"])
+        extra["reference_protocol"] = {"us_per_call_unroll128_median5": round(t128, 3),
+                                       "us_per_call_unroll32_median5": round(t32, 3),
+                                       "convergence_delta": round(delta, 4)}
+        fixed, splits = fixed_partition_case(torch, case)
+        f_us = graph_time_us(torch, fixed, args.steps)
+        extra["partition_1024_tokens"] = {"splits": splits, "us_per_call": round(f_us, 3),
+                                          "tbps": round(nbytes / f_us / 1e6, 3)}
+        c528 = matched_case(torch, 1, 16, 4, 256, 528, [528], 20261105)
+        u528 = graph_time_us(torch, c528["full"], args.steps)
+        b528 = algorithmic_bytes([528], 1, 16, 4, 256)
+        extra["ctx_528"] = {"plan": f"{c528['plan'].splits}x{c528['plan'].tokens_per_split}",
+                            "us_per_call": round(u528, 3), "tbps": round(b528 / u528 / 1e6, 3)}
+        del c528
+        extra["bandwidth_sweep"] = bandwidth_sweep(torch)
+
+    cpu = None
+    if not args.no_cpu:
+        one = cpu_baseline(ctx, 1, args.cpu_budget)
+        allc = cpu_baseline(ctx, os.cpu_count() or 1, args.cpu_budget)
+        best = min((one, 1), (allc, os.cpu_count() or 1), key=lambda x: x[0]["us"])
+        cpu = {"value": round(nbytes / best[0]["us"] / 1e6, 6), "unit": "TB/s",
+               "cores": best[1], "kind": "port",
+               "us_per_call": round(best[0]["us"], 1),
+               "one_thread_us_per_call": round(one["us"], 1),
+               "all_threads_us_per_call": round(allc["us"], 1),
+               "host_cpus": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+               "sample": (f"NumPy restatement of the reference CPU path (streaming_reference, "
+                          f"1024-token partitions, 64-token tiles, FP32) on the same C2 shape, "
+                          f"median of {allc['calls']} calls in ~{args.cpu_budget:.0f} s")}
+
+    line = {
+        "metric": "paged-decode µs/call + achieved HBM TB/s (% peak), D256 GQA ctx 2064",
+        "value": round(tbps, 4), "unit": "TB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1000, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"matched split-KV decode B=1 Hq=16 Hkv=4 D=256 page=256 "
+                               f"ctx {ctx} (capacity {capacity}), planner plan, hot cache",
+                   "global_batch": 1, "seq_len": ctx, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(part_tbps * 1000, 1), "peak": PEAK_TBPS * 1000,
+                     "unit": "GB/s", "frac": round(part_tbps / PEAK_TBPS, 4), "traffic": None,
+                     "kernel": "matched_partition_kernel<256,4>", "bytes_per_launch": part_bytes,
+                     "us_per_launch": round(part_us, 3)},
+        "cpu_baseline": cpu,
+        **extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,131 @@
+/*
+ * paged_decode.h — C ABI of the MI355X (gfx950) paged decode operator.
+ *
+ * One query token per sequence attends over a paged KV cache:
+ *   Q       bf16 [batch, num_heads, head_dim], innermost dim contiguous,
+ *           rows 16-byte aligned (strides in elements are multiples of 8)
+ *   K, V    bf16 [num_pages, 256, num_kv_heads, head_dim], contiguous (NHD pages)
+ *   table   int32 [batch, width] block table, row stride table_stride_b;
+ *           logical token t of row b lives in page table[b, t / 256], slot t % 256
+ *   lengths int32 [batch], 0 <= lengths[b] <= width * 256
+ * Element offset of (page, slot, kv_head, d) is ((page*256+slot)*Hkv+kv_head)*D+d,
+ * computed in 64-bit.  Query head h reads kv head h / (num_heads / num_kv_heads).
+ *
+ * Conventions of every entry point:
+ *   - returns PD_OK (0) or a nonzero pd_status; pd_last_error() then holds a
+ *     message for the calling thread;
+ *   - pointers to tensors are device pointers; nothing is allocated, nothing
+ *     synchronizes, no device memory is read on the host, so every launch can
+ *     be recorded into a hipGraph on `stream` and replayed with new contents;
+ *   - tensor CONTENTS are trusted (live table entries must name valid pages);
+ *     use pd_validate_metadata on host copies to check them.
+ * `pd_stream_t` is the same type as hipStream_t.
+ */
+#ifndef PAGED_DECODE_H_
+#define PAGED_DECODE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* pd_stream_t;
+
+enum pd_status { PD_OK = 0, PD_EINVAL = 1, PD_ELAUNCH = 2 };
+
+#define PD_PAGE_SIZE 256      /* spec.py:6 */
+#define PD_PARTITION_SIZE 1024 /* spec.py:7 */
+#define PD_ABI_VERSION 1
+
+/* Split-KV plan; field meanings follow SplitKVPlan (splitkv_plan.py:15-23). */
+typedef struct pd_plan {
+  int32_t splits;
+  int32_t tile_tokens;
+  int32_t tokens_per_split;
+  int32_t table_capacity_tokens;
+  int32_t lse_lanes;
+  int32_t sm_count;
+  int32_t is_explicit; /* 1 = policy "explicit", 0 = "pinned_geometry" */
+} pd_plan;
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* pd_last_error(void);
+
+/* PD_ABI_VERSION of the built library. */
+int pd_abi_version(void);
+
+/* Replaces make_splitkv_plan (splitkv_plan.py:26-56), bit-exact including its
+ * float32 rounding points.  max_context_len gives the table capacity through
+ * ceil(max_context_len / 256) * 256 (spec.py:36-38).  num_splits = 0 selects
+ * the pinned-geometry heuristic, 1..128 an explicit count. */
+int pd_make_plan(int32_t max_batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                 int32_t max_context_len, int32_t sm_count, int32_t num_splits, pd_plan* out);
+
+/* Host-memory content check; replaces validate_metadata (reference.py:10-21)
+ * as used by validate_device_metadata (runtime.py:38-43): lengths within
+ * [0, max_context_len], live pages ceil(len/256) <= width, live entries within
+ * [0, num_pages).  `table` and `lengths` are HOST pointers. */
+int pd_validate_metadata(const int32_t* table, int64_t table_stride_b, int32_t width,
+                         const int32_t* lengths, int32_t batch, int64_t num_pages,
+                         int32_t max_context_len);
+
+/* Matched split-KV partition; replaces _normalized_partition
+ * (matched_splitkv.py:52-98) as launched by matched_decode (:142-146).
+ * Writes partials f32 [batch, num_heads, splits, head_dim] (normalized) and
+ * lse f32 [batch, num_heads, splits] (-inf for an empty partition).
+ * Partition p covers [p*tokens_per_split, min((p+1)*tokens_per_split, len)),
+ * walked in tile_tokens tiles from the last to the first.  Requires
+ * head_dim in {64,128,256}, tile_tokens == 16384/head_dim, tokens_per_split a
+ * multiple of tile_tokens, num_heads/num_kv_heads <= 16, splits in [1,128].
+ * scale is applied to the scores (exp2 argument uses f32(scale*log2(e))). */
+int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                 const void* k, const void* v,
+                 const int32_t* table, int64_t table_stride_b, const int32_t* lengths,
+                 float* partials, float* lse,
+                 int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                 int32_t splits, int32_t tokens_per_split, int32_t tile_tokens,
+                 double scale, pd_stream_t stream);
+
+/* Stable LSE merge; replaces _lse_merge (matched_splitkv.py:101-127) as
+ * launched by matched_decode (:147-149).  Writes out bf16 [batch, num_heads,
+ * head_dim].  lse_lanes is the plan's lane count (a power of two <= splits'
+ * next power of two); it only changes float32 summation order. */
+int pd_lse_merge(const float* partials, const float* lse, void* out,
+                 int32_t batch, int32_t num_heads, int32_t head_dim, int32_t splits,
+                 int32_t lse_lanes, pd_stream_t stream);
+
+/* Base decode: one workgroup per (sequence, query head), FP32 online softmax
+ * over the whole context, out = acc / denom (0 for an empty row).  Replaces
+ * _base (kernels.py:10-41) as launched by paged_decode (runtime.py:109).
+ * Writes out rows [0, batch). */
+int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+            const void* k, const void* v,
+            const int32_t* table, int64_t table_stride_b, const int32_t* lengths,
+            void* out, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+            int32_t head_dim, double scale, pd_stream_t stream);
+
+/* Fixed-size split-K partition: unnormalized (m, l, acc) per partition of
+ * partition_size tokens, m in scaled units.  Replaces _split (kernels.py:44-80)
+ * as launched by paged_decode (runtime.py:111-113).  maxima/denoms f32
+ * [batch, num_heads, partitions], accums f32 [batch, num_heads, partitions, D];
+ * the row stride of all three is `partitions`. */
+int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                   const void* k, const void* v,
+                   const int32_t* table, int64_t table_stride_b, const int32_t* lengths,
+                   float* maxima, float* denoms, float* accums,
+                   int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t partitions, int32_t partition_size, double scale,
+                   pd_stream_t stream);
+
+/* m/l/acc merge; replaces _merge (kernels.py:83-100) as launched by
+ * paged_decode (runtime.py:114-116).  Writes out rows [0, batch). */
+int pd_ml_merge(const float* maxima, const float* denoms, const float* accums, void* out,
+                int32_t batch, int32_t num_heads, int32_t head_dim, int32_t partitions,
+                pd_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGED_DECODE_H_ */

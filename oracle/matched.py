@@ -47,8 +47,36 @@ def _cdiv(a, b):
     return -(-a // b)
 
 
-def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile, scale=None):
-    """Returns (partials [B,Hq,S,D] f32, lse [B,Hq,S] f32)."""
+AMBIGUITY_ULPS = 128   # fp32 ulps around a bf16 rounding midpoint treated as ambiguous
+
+
+def _ambiguous_ulp(p):
+    """bf16 ulp of each float32 p whose bf16 rounding is ambiguous, else 0.
+
+    p is ambiguous when it lies within AMBIGUITY_ULPS float32 ulps of the
+    midpoint between two bf16 values, i.e. when an implementation that computes
+    the same p with different float32 rounding (another summation order for
+    the scores, another exp2 instruction) may round it to the other bf16
+    neighbour.  Rounding the other way changes bf16(p) by exactly one bf16 ulp.
+    """
+    bits = np.ascontiguousarray(p, dtype=F32).view(np.uint32)
+    low = (bits & 0xFFFF).astype(np.int64)
+    near = np.abs(low - 0x8000) <= AMBIGUITY_ULPS
+    exponent = ((bits >> 23) & 0xFF).astype(np.int64) - 127
+    ulp = np.ldexp(np.float32(1), (exponent - 7).clip(-149, 127)).astype(F32)
+    return np.where(near & (p > 0), ulp, F32(0)).astype(F32)
+
+
+def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile, scale=None,
+                         with_ambiguity=False):
+    """Returns (partials [B,Hq,S,D] f32, lse [B,Hq,S] f32[, ambiguity [B,Hq,S,D] f32]).
+
+    With ``with_ambiguity`` the third result bounds how far a faithful
+    implementation's normalized partial can move because of p values whose
+    bf16 rounding is ambiguous (see ``_ambiguous_ulp``): the sum over those
+    tokens of ulp_bf16(p) * |v|, rescaled by the same alpha factors as the
+    accumulator and divided by the denominator.
+    """
     q = np.asarray(q, dtype=F32)
     B, Hq, D = q.shape
     Hkv = k.shape[2]
@@ -59,6 +87,7 @@ def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile
     T = int(tokens_per_split)
     partials = np.zeros((B, Hq, splits, D), dtype=F32)
     lse = np.full((B, Hq, splits), -np.inf, dtype=F32)
+    ambiguity = np.zeros((B, Hq, splits, D), dtype=F32) if with_ambiguity else None
     table = np.asarray(table)
     for b in range(B):
         length = int(lengths[b])
@@ -70,6 +99,7 @@ def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile
             m = np.full((Hkv, G), -np.inf, dtype=F32)
             lanes = np.zeros((Hkv, G, 4), dtype=F32)
             acc = np.zeros((Hkv, G, D), dtype=F32)
+            amb = np.zeros((Hkv, G, D), dtype=F32)
             for i in range(count):
                 t0 = start + (count - 1 - i) * tile          # reverse walk (:71)
                 nv = min(tile, end - t0)
@@ -89,13 +119,20 @@ def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile
                     lanes = (lanes + p_[..., 8 * blk + 1:8 * blk + 8:2]).astype(F32)
                 pv = np.matmul(bf16_round(p_[..., :nv]), vt.transpose(1, 0, 2))
                 acc = (acc * alpha[..., None] + pv).astype(F32)
+                if with_ambiguity:
+                    flips = np.matmul(_ambiguous_ulp(p_[..., :nv]), np.abs(vt).transpose(1, 0, 2))
+                    amb = (amb * alpha[..., None] + flips).astype(F32)
                 m = m_next
             denom = ((lanes[..., 0] + lanes[..., 2]) + (lanes[..., 1] + lanes[..., 3])).astype(F32)
             safe = np.where(denom > 0, denom, F32(1)).astype(F32)
             partials[b, :, p] = (acc * (F32(1) / safe)[..., None]).reshape(Hq, D)
+            if with_ambiguity:
+                ambiguity[b, :, p] = (amb / safe[..., None]).reshape(Hq, D)
             with np.errstate(invalid="ignore"):
                 lse_p = np.where(denom > 0, fma32(m, s32, ln32(safe)), F32(-np.inf))
             lse[b, :, p] = lse_p.reshape(Hq)
+    if with_ambiguity:
+        return partials, lse, ambiguity
     return partials, lse
 
 
@@ -139,6 +176,30 @@ def matched_decode(q, k, v, table, lengths, splits, tokens_per_split, tile, lse_
     partials, lse = normalized_partition(q, k, v, table, lengths, splits, tokens_per_split,
                                          tile, scale)
     return lse_merge(partials, lse, lse_lanes), partials, lse
+
+
+def matched_decode_with_bounds(q, k, v, table, lengths, splits, tokens_per_split, tile,
+                               lse_lanes, scale=None):
+    """Returns (out, partials, lse, out_ambiguity, partial_ambiguity).
+
+    ``partial_ambiguity[b, h, p, d]`` bounds how far a faithful implementation's
+    normalized partial can move because of ambiguous bf16 roundings of p, and
+    ``out_ambiguity[b, h, d]`` bounds the change of the float32 output before
+    its final bf16 rounding: the merge-weighted (exp(lse_p - L)) sum of the
+    partial bounds.  Denominators and LSEs use the unrounded p, so they carry
+    no such term.
+    """
+    partials, lse, amb = normalized_partition(q, k, v, table, lengths, splits, tokens_per_split,
+                                              tile, scale, with_ambiguity=True)
+    out = lse_merge(partials, lse, lse_lanes)
+    with np.errstate(invalid="ignore", over="ignore"):
+        top = np.max(lse, axis=-1, keepdims=True)
+        top = np.where(np.isfinite(top), top, 0)
+        weights = np.exp(lse.astype(np.float64) - top)
+        total = weights.sum(axis=-1, keepdims=True)
+        weights = np.where(total > 0, weights / np.where(total > 0, total, 1), 0)
+    out_amb = (weights[..., None] * amb).sum(axis=-2).astype(F32)
+    return out, partials, lse, out_amb, amb
 
 
 def suffix_max_decode(q, k, v, table, lengths, splits, tokens_per_split, tile, scale=None):

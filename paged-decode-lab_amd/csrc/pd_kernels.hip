@@ -1,0 +1,761 @@
+// Paged decode attention kernels for MI355X (gfx950, CDNA4) and their C-ABI
+// launchers.  See include/paged_decode.h for the tensor contract.
+//
+// Kernels
+//   matched_partition  one 256-thread workgroup per (split, kv head, sequence):
+//                      QK^T on MFMA (v_mfma_f32_16x16x32_bf16), FP32 online
+//                      softmax over 16384/D-token tiles walked last-to-first,
+//                      PV on v_dot2_f32_bf16 with bf16(p) shared through LDS,
+//                      normalized FP32 partial + LSE out.
+//   lse_merge          one wavefront per (sequence, query head): stable
+//                      log-sum-exp merge of the split partials, bf16 out.
+//   online_decode      one 256-thread workgroup per (sequence, query head
+//                      [, fixed partition]): FP32 online softmax with fp32 p,
+//                      either normalized bf16 out (base) or (m, l, acc) state.
+//   ml_merge           one wavefront per (sequence, query head): merge of the
+//                      (m, l, acc) states.
+//
+// Every kernel reads the sequence length and block table on the device and
+// never needs host-side knowledge of tensor contents, so launches are
+// graph-capturable and replay correctly with new lengths, pages and KV.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "pd_internal.h"
+
+namespace {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;  // ln 2 rounded to float32
+constexpr int kThreads = 256;
+
+// ---------------------------------------------------------------- numerics
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// float32 -> bfloat16 bits, round to nearest even; NaN -> quiet NaN.
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Native gfx950 transcendental instructions (v_exp_f32 = 2^x, v_log_f32 =
+// log2 x, v_rcp_f32 = 1/x); ln and e^x by change of base.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+__device__ __forceinline__ float ln_fast(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
+__device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// a.lo*b.lo + a.hi*b.hi + c over bf16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+__device__ __forceinline__ u32x4_t load16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+// ------------------------------------------------------- matched partition
+//
+// Tile geometry: TILE = 16384 / D tokens (64/128/256 for D = 256/128/64), the
+// reference's tile_tokens (splitkv_plan.py:33), so a tile is always 32 KiB of K
+// and 32 KiB of V and never crosses a 256-token page.
+//
+// QK^T: wave w owns tokens [w*TILE/4, (w+1)*TILE/4) in groups of 16.  For the
+// MFMA, A = K rows (lane -> token lane%16, d = 32c + 8*(lane/16) .. +8) and
+// B = Q of the GQA group (lane -> head lane%16, same d), so the result lane
+// holds S[token 4*(lane/16)+r][head lane%16], r = 0..3.  Padded heads
+// (>= G) have zero Q and are never stored.
+//
+// PV: thread tid owns the 8-column slice d0 = 8*(tid % (D/8)) of row pairs
+// (j*TILE/4 + 2*rg, +1), rg = tid / (D/8), j = 0..3, so every V load is a
+// 16-byte piece of a row and a pair of rows packs into bf16x2 operands for
+// v_dot2_f32_bf16 together with the pair's bf16 probabilities from LDS.
+template <int D, int GP>
+struct Matched {
+  static constexpr int kTile = 16384 / D;
+  static constexpr int kTW = kTile / 4;   // tokens per wave in QK
+  static constexpr int kNG = kTW / 16;    // 16-token MFMA groups per wave
+  static constexpr int kCH = D / 32;      // MFMA k-chunks of 32 d
+  static constexpr int kLPR = D / 8;      // lanes per V row
+  static constexpr int kOut = GP * D;            // outputs of one GQA group
+  static constexpr int kE = kOut >= kThreads ? kOut / kThreads : 1;  // per thread
+  static_assert(kNG >= 1 && kCH >= 1, "geometry");
+};
+
+template <int D, int GP>
+struct TileRegs {
+  u32x4_t k[Matched<D, GP>::kNG][Matched<D, GP>::kCH];
+  u32x4_t v[4][2];
+};
+
+template <int D, int GP>
+__device__ __forceinline__ void matched_load(TileRegs<D, GP>& R, const uint16_t* __restrict__ k,
+                                             const uint16_t* __restrict__ v,
+                                             const int32_t* __restrict__ trow, int t0, int end,
+                                             int64_t RS, int kh, int lane, int w, int rg, int d0) {
+  using C = Matched<D, GP>;
+  const int64_t page = trow[t0 >> 8];
+  const int64_t base = (page * 256 + (t0 & 255)) * RS + int64_t(kh) * D;
+  const int nvalid = end - t0;
+  const int qh = lane & 15, qg = lane >> 4;
+#pragma unroll
+  for (int g = 0; g < C::kNG; ++g) {
+    const int row = w * C::kTW + 16 * g + qh;
+    const uint16_t* src = k + base + int64_t(row) * RS + 8 * qg;
+#pragma unroll
+    for (int c = 0; c < C::kCH; ++c)
+      R.k[g][c] = row < nvalid ? load16(src + 32 * c) : u32x4_t{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int row = j * (C::kTile / 4) + 2 * rg + par;
+      R.v[j][par] = row < nvalid ? load16(v + base + int64_t(row) * RS + d0)
+                                 : u32x4_t{0, 0, 0, 0};
+    }
+}
+
+template <int D, int GP>
+struct MatchedShared {
+  union alignas(16) {
+    uint16_t pbuf[GP][Matched<D, GP>::kTile];
+    float red[2][GP][D];
+  } u;
+  float wmax[4][16];
+  float lsum[4][16];
+  float mfin[16];
+};
+
+template <int D, int GP>
+__global__ void __launch_bounds__(kThreads, GP >= 16 ? 1 : 2)
+matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
+                         const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                         const int32_t* __restrict__ table, int64_t tsb,
+                         const int32_t* __restrict__ lengths, float* __restrict__ partials,
+                         float* __restrict__ lse_out, int Hq, int Hkv, int G, int splits, int T,
+                         float scale, float c) {
+  using C = Matched<D, GP>;
+  constexpr int TILE = C::kTile;
+  __shared__ MatchedShared<D, GP> sm;
+
+  const int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int qh = lane & 15, qg = lane >> 4;
+  const int rg = tid / C::kLPR, d0 = (tid % C::kLPR) * 8;
+  const int length = lengths[b];
+  const int start = p * T;
+  const int end = min(start + T, length);
+  const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+  const int64_t RS = int64_t(Hkv) * D;
+  const int32_t* trow = table + int64_t(b) * tsb;
+
+  // MFMA B operand: the GQA group's query rows.
+  bf16x8_t qf[C::kCH];
+  {
+    const bool live = qh < G;
+    const uint16_t* qrow =
+        q + int64_t(b) * qsb + int64_t(kh * G + (live ? qh : 0)) * qsh + 8 * qg;
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch)
+      qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
+  }
+
+  float M[GP];             // running max of raw scores, per head (uniform)
+  float acc[GP][8];        // PV accumulator for (head, d0 + e)
+#pragma unroll
+  for (int h = 0; h < GP; ++h) {
+    M[h] = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  }
+  float m_own = -INFINITY;  // running max of head qh (same value as M[qh])
+  float l_own = 0.f;        // this lane's share of head qh's denominator
+
+  auto process = [&](const TileRegs<D, GP>& R, int ti) __attribute__((always_inline)) {
+    const int t0 = start + ti * TILE;
+    const int nvalid = end - t0;
+    // ---- scores
+    floatx4_t s[C::kNG];
+#pragma unroll
+    for (int g = 0; g < C::kNG; ++g) {
+      s[g] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ch = 0; ch < C::kCH; ++ch)
+        s[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, R.k[g][ch]),
+                                                        qf[ch], s[g], 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = w * C::kTW + 16 * g + 4 * qg + r;
+        if (tok >= nvalid) s[g][r] = -INFINITY;
+        mx = fmaxf(mx, s[g][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (lane < 16) sm.wmax[w][lane] = mx;
+    __syncthreads();
+    // ---- running max update (reference order: m' = max(m, rowmax s))
+    float alpha[GP];
+#pragma unroll
+    for (int h = 0; h < GP; ++h) {
+      const float tm = fmaxf(fmaxf(sm.wmax[0][h], sm.wmax[1][h]), fmaxf(sm.wmax[2][h], sm.wmax[3][h]));
+      const float mn = fmaxf(M[h], tm);
+      alpha[h] = exp2_fast((M[h] - mn) * c);
+      M[h] = mn;
+    }
+    {
+      const float tm = fmaxf(fmaxf(sm.wmax[0][qh], sm.wmax[1][qh]), fmaxf(sm.wmax[2][qh], sm.wmax[3][qh]));
+      const float mn = fmaxf(m_own, tm);
+      const float a_own = exp2_fast((m_own - mn) * c);
+      m_own = mn;
+      const float neg_mc = -(mn * c);
+      float psum = 0.f;
+#pragma unroll
+      for (int g = 0; g < C::kNG; ++g) {
+        uint32_t bits[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = exp2_fast(fmaf(s[g][r], c, neg_mc));
+          psum += pr;
+          bits[r] = bf16_bits(pr);
+        }
+        if (qh < GP)
+          *reinterpret_cast<u32x2_t*>(&sm.u.pbuf[qh][w * C::kTW + 16 * g + 4 * qg]) =
+              u32x2_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+      }
+      l_own = l_own * a_own + psum;
+    }
+    __syncthreads();
+    // ---- PV
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row0 = j * (TILE / 4) + 2 * rg;
+      uint32_t pp[GP];
+#pragma unroll
+      for (int h = 0; h < GP; ++h) pp[h] = *reinterpret_cast<const uint32_t*>(&sm.u.pbuf[h][row0]);
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const uint32_t a = R.v[j][0][e4], bw = R.v[j][1][e4];
+        const uint32_t lo = (a & 0xffffu) | (bw << 16);
+        const uint32_t hi = (a >> 16) | (bw & 0xffff0000u);
+#pragma unroll
+        for (int h = 0; h < GP; ++h) {
+          acc[h][2 * e4] = dot2(lo, pp[h], acc[h][2 * e4]);
+          acc[h][2 * e4 + 1] = dot2(hi, pp[h], acc[h][2 * e4 + 1]);
+        }
+      }
+    }
+  };
+
+  // Reverse tile walk (matched_splitkv.py:71): last tile first.
+  for (int ti = count - 1; ti >= 0; --ti) {
+    TileRegs<D, GP> R;
+    matched_load<D, GP>(R, k, v, trow, start + ti * TILE, end, RS, kh, lane, w, rg, d0);
+    process(R, ti);
+  }
+
+  // ---- epilogue: combine the 4 waves' accumulators and denominators
+  float l = l_own;
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (lane < 16) sm.lsum[w][lane] = l;
+  if (tid < 16) sm.mfin[tid] = m_own;
+#pragma unroll
+  for (int msk = C::kLPR; msk < 64; msk <<= 1)
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], msk);
+  __syncthreads();  // pbuf (aliased by red) no longer read
+  if (lane < C::kLPR && w < 2)
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.u.red[w][h][d0 + e] = acc[h][e];
+  __syncthreads();
+  if (lane < C::kLPR && w >= 2)
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.u.red[w - 2][h][d0 + e] += acc[h][e];
+  __syncthreads();
+
+  const int idx0 = tid * C::kE;
+  const int h = idx0 / D, dd = idx0 % D;  // kE divides D, so one head per thread
+  if (idx0 < C::kOut && h < G) {
+    const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
+    const float safe = den > 0.f ? den : 1.f;
+    const float inv = rcp_fast(safe);
+    const int64_t orow = (int64_t(b) * Hq + kh * G + h) * splits + p;
+    float* dst = partials + orow * D + dd;
+#pragma unroll
+    for (int e = 0; e < C::kE; ++e) dst[e] = (sm.u.red[0][h][dd + e] + sm.u.red[1][h][dd + e]) * inv;
+    if (dd == 0) lse_out[orow] = den > 0.f ? fmaf(sm.mfin[h], scale, ln_fast(safe)) : -INFINITY;
+  }
+}
+
+// ------------------------------------------------------------- LSE merge
+// One wavefront per (b, h); lane owns VEC = D/64 consecutive columns.
+template <int VEC>
+__global__ void __launch_bounds__(64)
+lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ lse,
+                 uint16_t* __restrict__ out, int splits) {
+  constexpr int D = VEC * 64;
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* lrow = lse + int64_t(row) * splits;
+  const float v0 = lane < splits ? lrow[lane] : -INFINITY;
+  const float v1 = lane + 64 < splits ? lrow[lane + 64] : -INFINITY;
+  float mx = wave_max(fmaxf(v0, v1));
+  if (mx == -INFINITY) mx = 0.f;
+  const float total = wave_sum(exp_fast(v0 - mx) + exp_fast(v1 - mx));
+  const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
+  const float w0 = exp_fast(v0 - logsum);
+  const float w1 = exp_fast(v1 - logsum);
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  const float* prow = partials + int64_t(row) * splits * D + lane * VEC;
+#pragma unroll 4
+  for (int s = 0; s < splits; ++s) {
+    const float ws = s < 64 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w0), s))
+                            : __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w1), s - 64));
+    const float* src = prow + int64_t(s) * D;
+    float x[VEC];
+    if constexpr (VEC == 4) {
+      const floatx4_t t = *reinterpret_cast<const floatx4_t*>(src);
+      x[0] = t[0]; x[1] = t[1]; x[2] = t[2]; x[3] = t[3];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = src[e];
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = fmaf(ws, x[e], acc[e]);
+  }
+  uint16_t* dst = out + int64_t(row) * D + lane * VEC;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) dst[e] = uint16_t(bf16_bits(acc[e]));
+}
+
+// ------------------------------------------------- base / fixed-split kernel
+//
+// One 256-thread workgroup per (b, h[, partition]).  Each row of K/V is read
+// by D/8 lanes (16 bytes each); the 256/(D/8) row groups walk 16384/D-token
+// tiles (one page each), every row group keeping its own (m, l, acc) state
+// with fp32 p, merged across row groups and waves at the end.  With fp32
+// probabilities the result does not depend on the tile schedule beyond
+// float32 rounding.
+template <int D>
+struct Online {
+  static constexpr int kLPR = D / 8;
+  static constexpr int kRG = kThreads / kLPR;
+  static constexpr int kTile = 8 * kRG;  // 16384 / D
+};
+
+template <int D, bool kSplit>
+__global__ void __launch_bounds__(kThreads)
+online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
+                     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                     const int32_t* __restrict__ table, int64_t tsb,
+                     const int32_t* __restrict__ lengths, uint16_t* __restrict__ out,
+                     float* __restrict__ maxima, float* __restrict__ denoms,
+                     float* __restrict__ accums, int Hq, int Hkv, int G, int parts,
+                     int part_size, float scale) {
+  using C = Online<D>;
+  constexpr int TILE = C::kTile;
+  constexpr int LPR = C::kLPR;
+  __shared__ float wm[4], wl[4];
+  __shared__ float wacc[4][D];
+
+  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int rg = tid / LPR, d0 = (tid % LPR) * 8;
+  const int kh = h / G;
+  const int length = lengths[b];
+  const int start = kSplit ? part * part_size : 0;
+  const int end = kSplit ? min(start + part_size, length) : length;
+  const int64_t RS = int64_t(Hkv) * D;
+  const int32_t* trow = table + int64_t(b) * tsb;
+
+  const u32x4_t qv = load16(q + int64_t(b) * qsb + int64_t(h) * qsh + d0);
+
+  float m = -INFINITY, l = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+
+  for (int t0 = start; t0 < end; t0 += TILE) {
+    const int64_t page = trow[t0 >> 8];
+    const int64_t base = (page * 256 + (t0 & 255)) * RS + int64_t(kh) * D + d0;
+    const int nvalid = end - t0;
+    u32x4_t kr[8], vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = rg + i * C::kRG;
+      const bool ok = row < nvalid;
+      kr[i] = ok ? load16(k + base + int64_t(row) * RS) : u32x4_t{0, 0, 0, 0};
+      vr[i] = ok ? load16(v + base + int64_t(row) * RS) : u32x4_t{0, 0, 0, 0};
+    }
+    float s[8];
+    float smax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float x = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x = dot2(kr[i][e], qv[e], x);
+#pragma unroll
+      for (int msk = 1; msk < LPR; msk <<= 1) x += __shfl_xor(x, msk);
+      x *= scale;
+      s[i] = rg + i * C::kRG < nvalid ? x : -INFINITY;
+      smax = fmaxf(smax, s[i]);
+    }
+    const float mn = fmaxf(m, smax);
+    const float alpha = exp_fast(m - mn);
+    l *= alpha;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float pr = exp_fast(s[i] - mn);
+      l += pr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] = fmaf(pr, bf16_lo(vr[i][e]), acc[2 * e]);
+        acc[2 * e + 1] = fmaf(pr, bf16_hi(vr[i][e]), acc[2 * e + 1]);
+      }
+    }
+    m = mn;
+  }
+
+  // Merge row groups inside the wave (lanes sharing d0), then across waves.
+#pragma unroll
+  for (int msk = LPR; msk < 64; msk <<= 1) {
+    const float mo = __shfl_xor(m, msk);
+    const float lo = __shfl_xor(l, msk);
+    const float mn = fmaxf(m, mo);
+    const float fa = m == -INFINITY ? 0.f : exp_fast(m - mn);
+    const float fb = mo == -INFINITY ? 0.f : exp_fast(mo - mn);
+    l = l * fa + lo * fb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = acc[e] * fa + __shfl_xor(acc[e], msk) * fb;
+    m = mn;
+  }
+  if (lane == 0) {
+    wm[w] = m;
+    wl[w] = l;
+  }
+  if (lane < LPR)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wacc[w][d0 + e] = acc[e];
+  __syncthreads();
+  if (tid < D) {
+    float mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float f[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) f[x] = wm[x] == -INFINITY ? 0.f : exp_fast(wm[x] - mx);
+    const float tot = (wl[0] * f[0] + wl[1] * f[1]) + (wl[2] * f[2] + wl[3] * f[3]);
+    const float num = (wacc[0][tid] * f[0] + wacc[1][tid] * f[1]) +
+                      (wacc[2][tid] * f[2] + wacc[3][tid] * f[3]);
+    if constexpr (kSplit) {
+      const int64_t idx = (int64_t(b) * Hq + h) * parts + part;
+      accums[idx * D + tid] = num;
+      if (tid == 0) {
+        maxima[idx] = mx;
+        denoms[idx] = tot;
+      }
+    } else {
+      out[(int64_t(b) * Hq + h) * D + tid] = uint16_t(bf16_bits(num / (tot > 0.f ? tot : 1.f)));
+    }
+  }
+}
+
+// ------------------------------------------------------------ m/l/acc merge
+template <int VEC>
+__global__ void __launch_bounds__(64)
+ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
+                const float* __restrict__ accums, uint16_t* __restrict__ out, int parts) {
+  constexpr int D = VEC * 64;
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* mrow = maxima + int64_t(row) * parts;
+  const float* lrow = denoms + int64_t(row) * parts;
+  float mx = -INFINITY;
+  for (int p = lane; p < parts; p += 64) mx = fmaxf(mx, mrow[p]);
+  mx = wave_max(mx);
+  if (mx == -INFINITY) mx = 0.f;  // all partitions empty
+  float total = 0.f, acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  const float* arow = accums + int64_t(row) * parts * D + lane * VEC;
+  for (int p = 0; p < parts; ++p) {
+    const float f = exp_fast(mrow[p] - mx);
+    total += lrow[p] * f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = fmaf(arow[int64_t(p) * D + e], f, acc[e]);
+  }
+  const float inv = 1.f / (total > 0.f ? total : 1.f);
+  uint16_t* dst = out + int64_t(row) * D + lane * VEC;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) dst[e] = uint16_t(bf16_bits(acc[e] * inv));
+}
+
+// --------------------------------------------------------------- launchers
+
+int launch_status(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return pd::fail(PD_ELAUNCH, "%s launch failed: %s", what, hipGetErrorString(err));
+  return PD_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_qkv(const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
+              const int32_t* table, const int32_t* lengths, int32_t batch, int32_t num_heads,
+              int32_t num_kv_heads, int32_t head_dim) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0)
+    return pd::fail(PD_EINVAL, "batch and head counts must be positive");
+  if (!pd::valid_head_dim(head_dim))
+    return pd::fail(PD_EINVAL, "custom decode supports head_dim 64, 128, or 256");
+  if (num_heads % num_kv_heads)
+    return pd::fail(PD_EINVAL, "query heads must be divisible by KV heads");
+  if (!q || !k || !v || !table || !lengths) return pd::fail(PD_EINVAL, "null tensor pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (qsb & 7) || (qsh & 7) || qsb < 0 ||
+      qsh < 0)
+    return pd::fail(PD_EINVAL,
+                    "Q/K/V rows must be 16-byte aligned (strides multiples of 8 elements)");
+  return PD_OK;
+}
+
+template <int D>
+int launch_partition_d(int gp, dim3 grid, hipStream_t stream, const uint16_t* q, int64_t qsb,
+                       int64_t qsh, const uint16_t* k, const uint16_t* v, const int32_t* table,
+                       int64_t tsb, const int32_t* lengths, float* partials, float* lse, int Hq,
+                       int Hkv, int G, int splits, int T, float scale, float c) {
+#define PD_LAUNCH_GP(GPV)                                                                    \
+  hipLaunchKernelGGL((matched_partition_kernel<D, GPV>), grid, dim3(kThreads), 0, stream, q, \
+                     qsb, qsh, k, v, table, tsb, lengths, partials, lse, Hq, Hkv, G, splits, \
+                     T, scale, c)
+  switch (gp) {
+    case 1: PD_LAUNCH_GP(1); break;
+    case 2: PD_LAUNCH_GP(2); break;
+    case 4: PD_LAUNCH_GP(4); break;
+    case 8: PD_LAUNCH_GP(8); break;
+    default: PD_LAUNCH_GP(16); break;
+  }
+#undef PD_LAUNCH_GP
+  return launch_status("pd_partition");
+}
+
+int padded_group(int g) {
+  int gp = 1;
+  while (gp < g) gp <<= 1;
+  return gp;
+}
+
+}  // namespace
+
+extern "C" int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                            const void* k, const void* v, const int32_t* table,
+                            int64_t table_stride_b, const int32_t* lengths, float* partials,
+                            float* lse, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t splits, int32_t tokens_per_split,
+                            int32_t tile_tokens, double scale, pd_stream_t stream) {
+  pd::clear_error();
+  if (int st = check_qkv(q, q_stride_b, q_stride_h, k, v, table, lengths, batch, num_heads,
+                         num_kv_heads, head_dim))
+    return st;
+  const int G = num_heads / num_kv_heads;
+  if (G > 16)
+    return pd::fail(PD_EINVAL, "matched split-KV requires at most 16 query heads per KV head");
+  if (splits < 1 || splits > 128) return pd::fail(PD_EINVAL, "splits must be in [1,128]");
+  if (tile_tokens != 16384 / head_dim)
+    return pd::fail(PD_EINVAL, "tile_tokens must be %d for head_dim %d", 16384 / head_dim,
+                    head_dim);
+  if (tokens_per_split <= 0 || tokens_per_split % tile_tokens)
+    return pd::fail(PD_EINVAL, "tokens_per_split must be a positive multiple of tile_tokens");
+  if (!partials || !lse) return pd::fail(PD_EINVAL, "invalid matched workspace");
+  if (!(scale > 0.0) || !std::isfinite(scale))
+    return pd::fail(PD_EINVAL, "positive finite scale required");
+  if (batch > 65535 || num_kv_heads > 65535)
+    return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
+  const float s32 = float(scale);
+  const float c = float(scale * 1.4426950408889634);  // SCALE_LOG2 (matched_splitkv.py:363)
+  const dim3 grid(splits, num_kv_heads, batch);
+  const auto* qq = static_cast<const uint16_t*>(q);
+  const auto* kk = static_cast<const uint16_t*>(k);
+  const auto* vv = static_cast<const uint16_t*>(v);
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int gp = padded_group(G);
+  switch (head_dim) {
+    case 64:
+      return launch_partition_d<64>(gp, grid, st, qq, q_stride_b, q_stride_h, kk, vv, table,
+                                    table_stride_b, lengths, partials, lse, num_heads,
+                                    num_kv_heads, G, splits, tokens_per_split, s32, c);
+    case 128:
+      return launch_partition_d<128>(gp, grid, st, qq, q_stride_b, q_stride_h, kk, vv, table,
+                                     table_stride_b, lengths, partials, lse, num_heads,
+                                     num_kv_heads, G, splits, tokens_per_split, s32, c);
+    default:
+      return launch_partition_d<256>(gp, grid, st, qq, q_stride_b, q_stride_h, kk, vv, table,
+                                     table_stride_b, lengths, partials, lse, num_heads,
+                                     num_kv_heads, G, splits, tokens_per_split, s32, c);
+  }
+}
+
+extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, int32_t batch,
+                            int32_t num_heads, int32_t head_dim, int32_t splits,
+                            int32_t lse_lanes, pd_stream_t stream) {
+  pd::clear_error();
+  if (batch <= 0 || num_heads <= 0) return pd::fail(PD_EINVAL, "batch and heads must be positive");
+  if (!pd::valid_head_dim(head_dim))
+    return pd::fail(PD_EINVAL, "custom decode supports head_dim 64, 128, or 256");
+  if (splits < 1 || splits > 128) return pd::fail(PD_EINVAL, "splits must be in [1,128]");
+  if (lse_lanes < 1 || (lse_lanes & (lse_lanes - 1)))
+    return pd::fail(PD_EINVAL, "lse_lanes must be a power of two");
+  if (!partials || !lse || !out) return pd::fail(PD_EINVAL, "null tensor pointer");
+  if (!aligned16(partials)) return pd::fail(PD_EINVAL, "partials must be 16-byte aligned");
+  const int64_t rows = int64_t(batch) * num_heads;
+  if (rows > 0x7fffffff) return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto* o = static_cast<uint16_t*>(out);
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL(lse_merge_kernel<1>, dim3(rows), dim3(64), 0, st, partials, lse, o, splits);
+      break;
+    case 128:
+      hipLaunchKernelGGL(lse_merge_kernel<2>, dim3(rows), dim3(64), 0, st, partials, lse, o, splits);
+      break;
+    default:
+      hipLaunchKernelGGL(lse_merge_kernel<4>, dim3(rows), dim3(64), 0, st, partials, lse, o, splits);
+      break;
+  }
+  return launch_status("pd_lse_merge");
+}
+
+namespace {
+
+template <bool kSplit>
+int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
+                  const int32_t* table, int64_t tsb, const int32_t* lengths, void* out,
+                  float* maxima, float* denoms, float* accums, int32_t batch, int32_t num_heads,
+                  int32_t num_kv_heads, int32_t head_dim, int32_t parts, int32_t part_size,
+                  double scale, pd_stream_t stream, const char* what) {
+  if (int st = check_qkv(q, qsb, qsh, k, v, table, lengths, batch, num_heads, num_kv_heads,
+                         head_dim))
+    return st;
+  if (!std::isfinite(scale)) return pd::fail(PD_EINVAL, "scale must be finite");
+  if (batch > 65535 || num_heads > 65535)
+    return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
+  if (kSplit) {
+    if (parts < 1) return pd::fail(PD_EINVAL, "partitions must be positive");
+    if (part_size <= 0 || part_size % (16384 / head_dim))
+      return pd::fail(PD_EINVAL, "partition_size must be a positive multiple of %d",
+                      16384 / head_dim);
+    if (!maxima || !denoms || !accums)
+      return pd::fail(PD_EINVAL, "invalid or missing preallocated split-K workspace");
+  } else if (!out) {
+    return pd::fail(PD_EINVAL, "invalid output buffer");
+  }
+  const int G = num_heads / num_kv_heads;
+  const dim3 grid(kSplit ? parts : 1, num_heads, batch);
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const auto* qq = static_cast<const uint16_t*>(q);
+  const auto* kk = static_cast<const uint16_t*>(k);
+  const auto* vv = static_cast<const uint16_t*>(v);
+  auto* o = static_cast<uint16_t*>(out);
+  const float s32 = float(scale);
+#define PD_LAUNCH_ONLINE(DV)                                                                  \
+  hipLaunchKernelGGL((online_decode_kernel<DV, kSplit>), grid, dim3(kThreads), 0, st, qq, qsb, \
+                     qsh, kk, vv, table, tsb, lengths, o, maxima, denoms, accums, num_heads,  \
+                     num_kv_heads, G, parts, part_size, s32)
+  switch (head_dim) {
+    case 64: PD_LAUNCH_ONLINE(64); break;
+    case 128: PD_LAUNCH_ONLINE(128); break;
+    default: PD_LAUNCH_ONLINE(256); break;
+  }
+#undef PD_LAUNCH_ONLINE
+  return launch_status(what);
+}
+
+}  // namespace
+
+extern "C" int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                       const void* v, const int32_t* table, int64_t table_stride_b,
+                       const int32_t* lengths, void* out, int32_t batch, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, double scale, pd_stream_t stream) {
+  pd::clear_error();
+  return launch_online<false>(q, q_stride_b, q_stride_h, k, v, table, table_stride_b, lengths,
+                              out, nullptr, nullptr, nullptr, batch, num_heads, num_kv_heads,
+                              head_dim, 1, 0, scale, stream, "pd_base");
+}
+
+extern "C" int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                              const void* k, const void* v, const int32_t* table,
+                              int64_t table_stride_b, const int32_t* lengths, float* maxima,
+                              float* denoms, float* accums, int32_t batch, int32_t num_heads,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t partitions,
+                              int32_t partition_size, double scale, pd_stream_t stream) {
+  pd::clear_error();
+  return launch_online<true>(q, q_stride_b, q_stride_h, k, v, table, table_stride_b, lengths,
+                             nullptr, maxima, denoms, accums, batch, num_heads, num_kv_heads,
+                             head_dim, partitions, partition_size, scale, stream,
+                             "pd_split_fixed");
+}
+
+extern "C" int pd_ml_merge(const float* maxima, const float* denoms, const float* accums,
+                           void* out, int32_t batch, int32_t num_heads, int32_t head_dim,
+                           int32_t partitions, pd_stream_t stream) {
+  pd::clear_error();
+  if (batch <= 0 || num_heads <= 0) return pd::fail(PD_EINVAL, "batch and heads must be positive");
+  if (!pd::valid_head_dim(head_dim))
+    return pd::fail(PD_EINVAL, "custom decode supports head_dim 64, 128, or 256");
+  if (partitions < 1) return pd::fail(PD_EINVAL, "partitions must be positive");
+  if (!maxima || !denoms || !accums || !out)
+    return pd::fail(PD_EINVAL, "invalid or missing preallocated split-K workspace");
+  const int64_t rows = int64_t(batch) * num_heads;
+  if (rows > 0x7fffffff) return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto* o = static_cast<uint16_t*>(out);
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL(ml_merge_kernel<1>, dim3(rows), dim3(64), 0, st, maxima, denoms, accums, o, partitions);
+      break;
+    case 128:
+      hipLaunchKernelGGL(ml_merge_kernel<2>, dim3(rows), dim3(64), 0, st, maxima, denoms, accums, o, partitions);
+      break;
+    default:
+      hipLaunchKernelGGL(ml_merge_kernel<4>, dim3(rows), dim3(64), 0, st, maxima, denoms, accums, o, partitions);
+      break;
+  }
+  return launch_status("pd_ml_merge");
+}

@@ -1,0 +1,125 @@
+"""ctypes binding of libpaged_decode.so (declared in include/paged_decode.h).
+
+torch is imported before the library is opened so that the library's
+``libamdhip64.so.7`` dependency resolves to the HIP runtime torch already
+loaded: streams, graphs and device pointers are then shared with torch.
+
+There is no fallback: if the library is missing, every entry point raises.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpaged_decode.so")
+
+PD_OK, PD_EINVAL, PD_ELAUNCH = 0, 1, 2
+
+_i32, _i64, _dbl, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_double, ctypes.c_void_p
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("splits", _i32), ("tile_tokens", _i32), ("tokens_per_split", _i32),
+                ("table_capacity_tokens", _i32), ("lse_lanes", _i32), ("sm_count", _i32),
+                ("is_explicit", _i32)]
+
+
+# Exported symbol -> argtypes.  Kept in the order of include/paged_decode.h.
+SIGNATURES = {
+    "pd_last_error": [],
+    "pd_abi_version": [],
+    "pd_make_plan": [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(Plan)],
+    "pd_validate_metadata": [_vp, _i64, _i32, _vp, _i32, _i64, _i32],
+    "pd_partition": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                     _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
+    "pd_lse_merge": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
+    "pd_base": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _dbl, _vp],
+    "pd_split_fixed": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                       _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
+    "pd_ml_merge": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises RuntimeError when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built: run `make -C paged-decode-lab_amd/csrc` "
+                "(or __graft_entry__.build()); there is no fallback implementation")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_char_p if name == "pd_last_error" else ctypes.c_int
+        _lib = handle
+    return _lib
+
+
+def check(status):
+    if status == PD_OK:
+        return
+    message = lib().pd_last_error().decode()
+    if status == PD_EINVAL:
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def make_plan(max_batch, num_heads, num_kv_heads, head_dim, max_context_len, sm_count,
+              num_splits):
+    plan = Plan()
+    check(lib().pd_make_plan(max_batch, num_heads, num_kv_heads, head_dim, max_context_len,
+                             sm_count, num_splits, ctypes.byref(plan)))
+    return plan
+
+
+def validate_metadata(table, lengths, num_pages, max_context_len):
+    """``table``/``lengths``: contiguous int32 CPU tensors."""
+    check(lib().pd_validate_metadata(table.data_ptr(), table.stride(0) if table.dim() else 0,
+                                     table.shape[1], lengths.data_ptr(), lengths.shape[0],
+                                     num_pages, max_context_len))
+
+
+def stream_handle(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def partition(q, k, v, tables, lengths, partials, lse, num_kv_heads, splits, tokens_per_split,
+              tile_tokens, scale):
+    b, h, d = q.shape
+    check(lib().pd_partition(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                             tables.data_ptr(), tables.stride(0), lengths.data_ptr(),
+                             partials.data_ptr(), lse.data_ptr(), b, h, num_kv_heads, d, splits,
+                             tokens_per_split, tile_tokens, scale, stream_handle(q.device)))
+
+
+def lse_merge(partials, lse, out, lse_lanes):
+    b, h, splits, d = partials.shape
+    check(lib().pd_lse_merge(partials.data_ptr(), lse.data_ptr(), out.data_ptr(), b, h, d, splits,
+                             lse_lanes, stream_handle(partials.device)))
+
+
+def base(q, k, v, tables, lengths, out, num_kv_heads, scale):
+    b, h, d = q.shape
+    check(lib().pd_base(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                        tables.data_ptr(), tables.stride(0), lengths.data_ptr(), out.data_ptr(),
+                        b, h, num_kv_heads, d, scale, stream_handle(q.device)))
+
+
+def split_fixed(q, k, v, tables, lengths, maxima, denoms, accums, num_kv_heads, partitions,
+                partition_size, scale):
+    b, h, d = q.shape
+    check(lib().pd_split_fixed(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                               tables.data_ptr(), tables.stride(0), lengths.data_ptr(),
+                               maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(), b, h,
+                               num_kv_heads, d, partitions, partition_size, scale,
+                               stream_handle(q.device)))
+
+
+def ml_merge(maxima, denoms, accums, out, batch):
+    _, h, parts, d = accums.shape
+    check(lib().pd_ml_merge(maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(),
+                            out.data_ptr(), batch, h, d, parts, stream_handle(out.device)))

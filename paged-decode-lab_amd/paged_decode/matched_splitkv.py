@@ -1,0 +1,67 @@
+"""Capacity-aligned split-KV with normalized FP32 partials + LSE.
+
+Mirrors matched_splitkv.py of the reference (src/paged_decode/matched_splitkv.py:15-150):
+``MatchedResources``, ``allocate_matched_resources`` and ``matched_decode``,
+with the same plan, workspace shapes, contract checks and error messages.
+The two launches are the HIP kernels pd_partition and pd_lse_merge
+(include/paged_decode.h).
+"""
+from dataclasses import dataclass
+import math
+
+import torch
+
+from . import _native
+from .runtime import _validate
+from .splitkv_plan import make_splitkv_plan
+
+
+@dataclass
+class MatchedResources:
+    spec: object
+    plan: object
+    out: torch.Tensor
+    partials: torch.Tensor
+    lse: torch.Tensor
+
+
+def allocate_matched_resources(spec, device, *, num_splits=0):
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("matched resources require CUDA")
+    plan = make_splitkv_plan(spec, torch.cuda.get_device_properties(device).multi_processor_count,
+                             num_splits=num_splits)
+    shape = (spec.max_batch, spec.num_heads, plan.splits)
+    return MatchedResources(
+        spec, plan,
+        torch.empty((spec.max_batch, spec.num_heads, spec.head_dim), device=device,
+                    dtype=torch.bfloat16),
+        torch.empty((*shape, spec.head_dim), device=device, dtype=torch.float32),
+        torch.empty(shape, device=device, dtype=torch.float32))
+
+
+def _check_matched(q, tables, resources, scale):
+    if scale <= 0 or not math.isfinite(scale):
+        raise ValueError("positive finite scale required")
+    spec, plan = resources.spec, resources.plan
+    if q.shape[0] != spec.max_batch or tables.shape[1] != spec.table_width:
+        raise ValueError("matched plan requires its fixed batch and table capacity")
+    shape = (spec.max_batch, spec.num_heads, plan.splits)
+    for tensor, geometry in ((resources.lse, shape),
+                             (resources.partials, (*shape, spec.head_dim))):
+        if (tensor.shape != geometry or tensor.device != q.device
+                or tensor.dtype != torch.float32 or not tensor.is_contiguous()):
+            raise ValueError("invalid matched workspace")
+
+
+def matched_decode(q, k, v, tables, lengths, *, resources, scale=None):
+    """Return the borrowed [max_batch, Hq, D] bf16 output (overwritten by the next call)."""
+    scale = q.shape[-1] ** -.5 if scale is None else float(scale)
+    _validate(q, k, v, tables, lengths, resources, "hip_base", scale)
+    _check_matched(q, tables, resources, scale)
+    spec, plan = resources.spec, resources.plan
+    _native.partition(q, k, v, tables, lengths, resources.partials, resources.lse,
+                      spec.num_kv_heads, plan.splits, plan.tokens_per_split, plan.tile_tokens,
+                      scale)
+    _native.lse_merge(resources.partials, resources.lse, resources.out, plan.lse_lanes)
+    return resources.out

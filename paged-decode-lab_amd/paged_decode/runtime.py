@@ -1,0 +1,127 @@
+"""Validated launches and reusable output / split workspace.
+
+Mirrors runtime.py of the reference (src/paged_decode/runtime.py:15-117):
+``Resources``, ``allocate_resources``, ``validate_device_metadata``,
+``paged_decode`` and the host-only ``_validate`` contract with the same error
+messages.  Kernels are the HIP ones in libpaged_decode.so.
+
+Tensor CONTENTS are trusted on the hot path.  Call validate_device_metadata
+once for externally supplied tables; the engine's scheduler owns its metadata.
+A call allocates nothing, never synchronizes and never reads device memory on
+the host, so it can be captured into a hipGraph (torch.cuda.graph) after the
+resources are allocated and replayed with new lengths, pages and KV contents.
+"""
+from dataclasses import dataclass
+import math
+
+import torch
+
+from . import _native
+from .spec import DecodeSpec, PARTITION_SIZE, canonical_backend
+
+
+@dataclass
+class Resources:
+    spec: DecodeSpec
+    out: torch.Tensor
+    maxima: torch.Tensor | None = None
+    denoms: torch.Tensor | None = None
+    accums: torch.Tensor | None = None
+
+
+def allocate_resources(spec, device, backend="hip_splitk"):
+    try:
+        backend = canonical_backend(backend)
+    except ValueError:
+        raise ValueError("resources require a custom backend") from None
+    out = torch.empty((spec.max_batch, spec.num_heads, spec.head_dim),
+                      dtype=torch.bfloat16, device=device)
+    result = Resources(spec, out)
+    if backend == "hip_splitk":
+        shape = (spec.max_batch, spec.num_heads, spec.partitions)
+        result.maxima = torch.empty(shape, device=device, dtype=torch.float32)
+        result.denoms = torch.empty(shape, device=device, dtype=torch.float32)
+        result.accums = torch.empty((*shape, spec.head_dim), device=device, dtype=torch.float32)
+    return result
+
+
+def validate_device_metadata(table, lengths, num_pages, max_context_len):
+    """Debug check: deliberately synchronizes; NEVER call in capture/hot path."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("metadata content validation cannot run during graph capture")
+    table = table.detach().to("cpu", torch.int32).contiguous()
+    lengths = lengths.detach().to("cpu", torch.int32).contiguous()
+    if table.dim() != 2 or lengths.dim() != 1 or table.shape[0] != lengths.shape[0]:
+        raise ValueError("metadata batch dimensions differ")
+    _native.validate_metadata(table, lengths, int(num_pages), int(max_context_len))
+
+
+def _aligned(t):
+    return t.data_ptr() % 16 == 0
+
+
+def _validate(q, k, v, tables, lengths, resources, backend, scale):
+    if backend not in ("hip_base", "hip_splitk"):
+        raise ValueError("unknown custom backend")
+    spec = resources.spec
+    tensors = (q, k, v, tables, lengths, resources.out)
+    if not all(t.is_cuda and t.device == q.device for t in tensors):
+        raise ValueError("all tensors must be on the same CUDA device")
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("custom decode supports BF16 Q/K/V only")
+    if q.ndim != 3 or q.shape[1:] != (spec.num_heads, spec.head_dim):
+        raise ValueError("Q must have shape [batch, query_heads, head_dim]")
+    batch = q.shape[0]
+    if not 0 < batch <= spec.max_batch or q.stride(-1) != 1:
+        raise ValueError("Q batch exceeds capacity or innermost dimension is not contiguous")
+    if q.stride(0) % 8 or q.stride(1) % 8 or not _aligned(q):
+        raise ValueError("Q rows must be 16-byte aligned (strides multiples of 8 elements)")
+    if k.ndim != 4 or k.shape[1:] != (256, spec.num_kv_heads, spec.head_dim):
+        raise ValueError("KV must use NHD pages [pages,256,kv_heads,head_dim]")
+    if k.shape != v.shape or not k.is_contiguous() or not v.is_contiguous() or k.shape[0] == 0:
+        raise ValueError("K/V must have matching nonempty contiguous storage")
+    if not (_aligned(k) and _aligned(v)):
+        raise ValueError("K/V storage must be 16-byte aligned")
+    if tables.ndim != 2 or tables.shape[0] != batch or tables.stride(1) != 1:
+        raise ValueError("block table must have shape [batch,capacity] and contiguous rows")
+    # During eager execution the scheduler provides only the live table width.
+    if not 0 < tables.shape[1] <= spec.table_width:
+        raise ValueError("block table width outside configured capacity")
+    if lengths.shape != (batch,) or not lengths.is_contiguous():
+        raise ValueError("context lengths must be a contiguous [batch] tensor")
+    if tables.dtype != torch.int32 or lengths.dtype != torch.int32:
+        raise ValueError("block tables and context lengths must be int32")
+    if not math.isfinite(scale):
+        raise ValueError("scale must be finite")
+    if (resources.out.shape != (spec.max_batch, spec.num_heads, spec.head_dim)
+            or resources.out.dtype != q.dtype or not resources.out.is_contiguous()):
+        raise ValueError("invalid output buffer")
+    if backend == "hip_splitk":
+        shape = (spec.max_batch, spec.num_heads, spec.partitions)
+        for tensor, expected in ((resources.maxima, shape), (resources.denoms, shape),
+                                 (resources.accums, (*shape, spec.head_dim))):
+            if (tensor is None or tensor.shape != expected or tensor.device != q.device
+                    or tensor.dtype != torch.float32 or not tensor.is_contiguous()):
+                raise ValueError("invalid or missing preallocated split-K workspace")
+
+
+def paged_decode(q, k, v, tables, lengths, *, resources, backend="hip_base", scale=None):
+    """Return borrowed [B,H,D] output. Next launch using resources overwrites it.
+
+    Resources must not overlap live inputs or be used concurrently across streams.
+    Live table entries must be valid pages; 0 <= lengths <= max_context_len and
+    ceil(length/256) <= table width. Padding table entries may contain -1.
+    """
+    scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
+    backend = canonical_backend(backend)
+    _validate(q, k, v, tables, lengths, resources, backend, scale)
+    spec = resources.spec
+    b = q.shape[0]
+    if backend == "hip_base":
+        _native.base(q, k, v, tables, lengths, resources.out, spec.num_kv_heads, scale)
+    else:
+        _native.split_fixed(q, k, v, tables, lengths, resources.maxima, resources.denoms,
+                            resources.accums, spec.num_kv_heads, spec.partitions,
+                            PARTITION_SIZE, scale)
+        _native.ml_merge(resources.maxima, resources.denoms, resources.accums, resources.out, b)
+    return resources.out[:b]

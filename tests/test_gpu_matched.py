@@ -1,0 +1,201 @@
+"""GPU parity of the matched split-KV operator (pd_partition + pd_lse_merge).
+
+Outputs are compared with the CPU oracle (oracle/matched.py) at one bf16 ulp
+and with the dense fp32 reference at the reference's 2e-2 gate.  Cases follow
+the reference's tests/test_matched_splitkv.py and the benchmark geometries.
+"""
+import numpy as np
+import pytest
+import torch
+
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X GPU", allow_module_level=True)
+
+from cases import make_case, poison_tails
+from gpu_cases import (assert_close_dense, assert_within_one_ulp, to_gpu, to_np,
+                       torch_dense)
+from oracle import matched as OM
+from paged_decode import _native
+from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
+from paged_decode.spec import DecodeSpec
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_for(case, plan, scale=None):
+    """(out, partials, lse, rounding-ambiguity bound of out) from the oracle."""
+    return OM.matched_decode_with_bounds(*case, plan.splits, plan.tokens_per_split,
+                                         plan.tile_tokens, plan.lse_lanes, scale)
+
+
+def run(case, spec, num_splits=0, scale=None):
+    g = to_gpu(case)
+    res = allocate_matched_resources(spec, "cuda", num_splits=num_splits)
+    out = matched_decode(*g, resources=res, scale=scale)
+    torch.cuda.synchronize()
+    return g, res, out
+
+
+def assert_partials(actual, expected, bound):
+    """fp32 partials: within the oracle's rounding-ambiguity bound plus fp32 noise."""
+    diff = np.abs(to_np(actual) - expected)
+    allowed = bound + 2e-5 + 2e-5 * np.abs(expected)
+    assert (diff <= allowed).all(), f"partials off by up to {diff.max():.3g}"
+
+
+def check_all(case, g, res, out, scale=None, where=""):
+    expected, partials, lse, bound, partial_bound = oracle_for(case, res.plan, scale)
+    frac = assert_within_one_ulp(out, expected, where, bound)
+    np.testing.assert_allclose(to_np(res.lse), lse, atol=2e-5, rtol=1e-6)
+    assert_partials(res.partials, partials, partial_bound)
+    assert_close_dense(out, torch_dense(*g, scale=scale))
+    return frac
+
+
+@pytest.mark.parametrize("ctx,cap", [(528, 528), (2064, 2112), (2064, 2064), (2112, 2112),
+                                     (1, 2112), (2063, 2304)])
+def test_d256_gqa_single_sequence(ctx, cap):
+    case = make_case([ctx], 16, 4, 256, seed=20261105, capacity=cap)
+    g, res, out = run(case, DecodeSpec(1, 16, 4, 256, cap))
+    frac = check_all(case, g, res, out, where=f"ctx {ctx}")
+    print(f"plan {res.plan.splits}x{res.plan.tokens_per_split} sm {res.plan.sm_count}: "
+          f"{frac:.2e} of outputs one ulp off")
+
+
+def test_d256_fixed_1024_token_partitions():
+    """Same kernels with 1024-token partitions (the fixed-partition geometry)."""
+    case = make_case([2064], 16, 4, 256, seed=20261105, capacity=2112)
+    g = to_gpu(case)
+    partials = torch.empty((1, 16, 3, 256), device="cuda", dtype=torch.float32)
+    lse = torch.empty((1, 16, 3), device="cuda", dtype=torch.float32)
+    out = torch.empty((1, 16, 256), device="cuda", dtype=torch.bfloat16)
+    _native.partition(*g, partials, lse, 4, 3, 1024, 64, 256 ** -0.5)
+    _native.lse_merge(partials, lse, out, 4)
+    torch.cuda.synchronize()
+    expected, _, exp_lse, bound, _ = OM.matched_decode_with_bounds(*case, 3, 1024, 64, 4)
+    assert_within_one_ulp(out, expected, "1024-token partitions", bound)
+    np.testing.assert_allclose(to_np(lse), exp_lse, atol=2e-5, rtol=1e-6)
+
+
+@pytest.mark.parametrize("splits", [3, 6])
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (128, 4, 2), (256, 8, 2)])
+def test_explicit_cross_page_boundaries(splits, dim, hq, hkv):
+    # reference tests/test_matched_splitkv.py:20-36, with NaN tails and -1 padding.
+    lengths = [0, 1, 255, 256, 257, 1023, 1024, 2051]
+    q, k, v, table, lens = make_case(lengths, hq, hkv, dim, capacity=2051)
+    poison_tails(k, v, table, lens)
+    case = (q, k, v, table, lens)
+    g, res, out = run(case, DecodeSpec(8, hq, hkv, dim, 2051), num_splits=splits)
+    check_all(case, g, res, out)
+    assert torch.count_nonzero(out[0]) == 0
+
+
+def test_graph_replay_and_empty_partitions():
+    # reference tests/test_matched_splitkv.py:39-57: capture after warmup, then
+    # replay with new lengths, pages and KV; replay == eager bit-exactly.
+    case = make_case([255, 1023, 0], 8, 2, 256, capacity=2051)
+    q, k, v, table, lengths = g = to_gpu(case)
+    res = allocate_matched_resources(DecodeSpec(3, 8, 2, 256, 2051), "cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            matched_decode(*g, resources=res)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = matched_decode(*g, resources=res)
+    for values in ([257, 1025, 0], [2051, 1, 0], [0, 0, 0], [2051, 2051, 2051]):
+        lengths.copy_(torch.tensor(values, dtype=torch.int32, device="cuda"))
+        q.normal_()
+        k.normal_()
+        v.normal_()
+        table.copy_(table.flip(1))
+        graph.replay()
+        captured = out.clone()
+        torch.cuda.synchronize()
+        host = (to_np(q), to_np(k), to_np(v), table.cpu().numpy(), lengths.cpu().numpy())
+        expected, _, _, bound, _ = oracle_for(host, res.plan)
+        assert_within_one_ulp(captured, expected, f"replay {values}", bound)
+        assert_close_dense(captured, torch_dense(*g))
+        eager = matched_decode(*g, resources=res)
+        torch.testing.assert_close(captured, eager, atol=0, rtol=0)
+        if not any(values):
+            assert torch.count_nonzero(captured) == 0
+
+
+def test_fixed_plan_contract():
+    # reference tests/test_matched_splitkv.py:60-69.
+    g = to_gpu(make_case([1, 2, 0], 8, 2, 256, capacity=2051))
+    res = allocate_matched_resources(DecodeSpec(3, 8, 2, 256, 2051), "cuda")
+    q, k, v, table, lengths = g
+    with pytest.raises(ValueError, match="fixed batch"):
+        matched_decode(q[:1], k, v, table[:1], lengths[:1], resources=res)
+    with pytest.raises(ValueError, match="fixed batch"):
+        matched_decode(q, k, v, table[:, :8], lengths, resources=res)
+    with pytest.raises(ValueError, match="positive"):
+        matched_decode(*g, resources=res, scale=0)
+    with pytest.raises(ValueError, match="BF16"):
+        matched_decode(q.float(), k, v, table, lengths, resources=res)
+    bad = allocate_matched_resources(DecodeSpec(3, 8, 2, 256, 2051), "cuda", num_splits=2)
+    bad.lse = bad.lse[:, :, :1]
+    with pytest.raises(ValueError, match="workspace"):
+        matched_decode(*g, resources=bad)
+
+
+def test_cpu_reference_config_c1():
+    # B=4, Hq=8, Hkv=2, D=128, lengths {0,1,257,1000}.
+    case = make_case([0, 1, 257, 1000], 8, 2, 128, seed=1, capacity=1000)
+    g, res, out = run(case, DecodeSpec(4, 8, 2, 128, 1000))
+    check_all(case, g, res, out)
+    assert torch.count_nonzero(out[0]) == 0
+
+
+def _edge_lengths(rng, batch, maximum):
+    lengths = rng.integers(1, maximum + 1, size=batch)
+    lengths[rng.permutation(batch)[: batch // 4]] = 0
+    special = [255, 256, 257, 511, 512, 513, 1023, 1024, 1025, 2047, 2048, 2049, maximum]
+    lengths[batch // 4: batch // 4 + len(special)] = special
+    return lengths.astype(np.int32)
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 16, 16), (256, 32, 4)])
+@pytest.mark.parametrize("splits", [0, 3, 6])
+def test_edge_coverage_config_c4(dim, hq, hkv, splits):
+    rng = np.random.default_rng(404)
+    lengths = _edge_lengths(rng, 128, 4096)
+    case = make_case(list(lengths), hq, hkv, dim, seed=5, capacity=4096)
+    g, res, out = run(case, DecodeSpec(128, hq, hkv, dim, 4096), num_splits=splits)
+    check_all(case, g, res, out, where=f"D{dim} {hq}/{hkv} splits {res.plan.splits}")
+    zero_rows = torch.from_numpy(lengths == 0).cuda()
+    assert torch.count_nonzero(out[zero_rows]) == 0
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+@pytest.mark.parametrize("group", [1, 2, 3, 5, 6, 8, 12, 16])
+def test_gqa_group_sizes(dim, group):
+    hkv = 2
+    case = make_case([0, 1, 300, 1025], hkv * group, hkv, dim, seed=group, capacity=1500)
+    for splits in (0, 3):
+        g, res, out = run(case, DecodeSpec(4, hkv * group, hkv, dim, 1500), num_splits=splits)
+        check_all(case, g, res, out, where=f"G{group} D{dim} splits {splits}")
+
+
+def test_custom_scale_and_strided_query():
+    case = make_case([700, 1, 2000], 8, 2, 128, seed=11, capacity=2048)
+    q, k, v, table, lengths = to_gpu(case)
+    wide = torch.zeros((3, 10, 128), device="cuda", dtype=torch.bfloat16)
+    wide[:, 1:9] = q
+    strided = wide[:, 1:9]            # stride(0) = 1280, stride(1) = 128
+    assert not strided.is_contiguous()
+    res = allocate_matched_resources(DecodeSpec(3, 8, 2, 128, 2048), "cuda")
+    out = matched_decode(strided, k, v, table, lengths, resources=res, scale=0.0625)
+    torch.cuda.synchronize()
+    check_all(case, (q, k, v, table, lengths), res, out, scale=0.0625)
+
+
+def test_long_single_split_reverse_walk():
+    # One split over up to 32768 tokens: 256 tiles walked last-to-first.
+    case = make_case([32768, 20000], 32, 8, 128, seed=3, capacity=32768)
+    g, res, out = run(case, DecodeSpec(2, 32, 8, 128, 32768), num_splits=1)
+    check_all(case, g, res, out)

@@ -1,0 +1,138 @@
+"""GPU parity of paged_decode backends hip_base and hip_splitk (and their aliases).
+
+Restates the reference's tests/test_gpu.py:51-128 and adds oracle parity at one
+bf16 ulp against oracle/splitk.py (the reference kernels.py restated).
+"""
+import numpy as np
+import pytest
+import torch
+
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X GPU", allow_module_level=True)
+
+from cases import make_case, poison_tails
+from gpu_cases import assert_close_dense, assert_within_one_ulp, to_gpu, to_np, torch_dense
+from oracle import splitk as OS
+from paged_decode.runtime import allocate_resources, paged_decode, validate_device_metadata
+from paged_decode.spec import DecodeSpec, canonical_backend
+
+pytestmark = pytest.mark.gpu
+
+BACKENDS = ["hip_base", "hip_splitk", "triton_base", "triton_splitk"]
+
+
+def oracle_for(case, backend, spec, scale=None):
+    if canonical_backend(backend) == "hip_base":
+        return OS.base_decode(*case, scale=scale)
+    return OS.ml_merge(*OS.split_partitions(*case, spec.partitions, scale=scale))
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (128, 4, 2), (64, 2, 2), (256, 8, 2)])
+def test_boundaries_gqa_and_padding(backend, dim, hq, hkv):
+    lengths = [0, 1, 255, 256, 257, 1023, 1024, 1025]
+    q, k, v, table, lens = make_case(lengths, hq, hkv, dim, seed=19, capacity=1025)
+    poison_tails(k, v, table, lens)
+    case = (q, k, v, table, lens)
+    g = to_gpu(case)
+    validate_device_metadata(g[3], g[4], len(k), 1025)
+    spec = DecodeSpec(len(lengths), hq, hkv, dim, 1025)
+    res = allocate_resources(spec, "cuda", backend)
+    actual = paged_decode(*g, resources=res, backend=backend).clone()
+    torch.cuda.synchronize()
+    assert_close_dense(actual, torch_dense(*g))
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec), backend)
+    assert torch.count_nonzero(actual[0]) == 0
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+@pytest.mark.parametrize("dim", [64, 256])
+def test_graph_replay_changes_lengths_pages_and_kv(backend, dim):
+    case = make_case([255, 1023, 0], 4, 1, dim, seed=19, capacity=2048)
+    g = to_gpu(case)
+    q, k, v, table, lens = g
+    spec = DecodeSpec(3, 4, 1, dim, 2048)
+    res = allocate_resources(spec, "cuda", backend)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            paged_decode(*g, resources=res, backend=backend)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        output = paged_decode(*g, resources=res, backend=backend)
+    for lengths in ([256, 1024, 0], [257, 1025, 1], [1, 0, 1025], [0, 0, 0], [2048, 2047, 1]):
+        lens.copy_(torch.tensor(lengths, device="cuda", dtype=torch.int32))
+        q.normal_()
+        k.normal_()
+        v.normal_()
+        table.copy_(table.flip(1))
+        graph.replay()
+        captured = output.clone()
+        torch.cuda.synchronize()
+        host = (to_np(q), to_np(k), to_np(v), table.cpu().numpy(), lens.cpu().numpy())
+        assert_close_dense(captured, torch_dense(*g))
+        assert_within_one_ulp(captured, oracle_for(host, backend, spec), f"replay {lengths}")
+        eager = paged_decode(*g, resources=res, backend=backend).clone()
+        torch.testing.assert_close(captured, eager, atol=0, rtol=0)
+
+
+def test_public_contract_rejects_bad_dtype_and_missing_workspace():
+    g = to_gpu(make_case([2], 4, 1, 64, capacity=2048))
+    r = allocate_resources(DecodeSpec(1, 4, 1, 64, 2048), "cuda", "hip_base")
+    for backend in ("hip_splitk", "triton_splitk"):
+        with pytest.raises(ValueError, match="workspace"):
+            paged_decode(*g, resources=r, backend=backend)
+    with pytest.raises(ValueError, match="BF16"):
+        paged_decode(g[0].float(), *g[1:], resources=r)
+    with pytest.raises(ValueError, match="unknown decode_backend"):
+        paged_decode(*g, resources=r, backend="triton_tc")
+    with pytest.raises(ValueError, match="resources require a custom backend"):
+        allocate_resources(DecodeSpec(1, 4, 1, 64, 2048), "cuda", "flash_attn")
+
+
+@pytest.mark.parametrize("backend", ["hip_splitk"])
+@pytest.mark.parametrize("dim", [64, 256])
+def test_non_power_of_two_split_count(dim, backend):
+    # Three real partitions (reference tests/test_gpu.py:121-128).
+    case = make_case([0, 2051, 2049, 1025], 4, 1, dim, seed=19, capacity=2051)
+    g = to_gpu(case)
+    spec = DecodeSpec(4, 4, 1, dim, 2051)
+    res = allocate_resources(spec, "cuda", backend)
+    actual = paged_decode(*g, resources=res, backend=backend)
+    torch.cuda.synchronize()
+    assert_close_dense(actual, torch_dense(*g))
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec))
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+def test_eager_partial_batch_and_live_table_width(backend):
+    # The scheduler may pass fewer rows than max_batch and only the live width.
+    case = make_case([300, 5, 511], 8, 2, 128, seed=7, capacity=512)
+    g = to_gpu(case)
+    spec = DecodeSpec(6, 8, 2, 128, 4096)
+    res = allocate_resources(spec, "cuda", backend)
+    actual = paged_decode(*g, resources=res, backend=backend, scale=0.1)
+    torch.cuda.synchronize()
+    assert actual.shape == (3, 8, 128)
+    assert_close_dense(actual, torch_dense(*g, scale=0.1))
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec, scale=0.1))
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 16, 16), (256, 32, 4)])
+def test_edge_coverage_config_c4(backend, dim, hq, hkv):
+    rng = np.random.default_rng(404)
+    lengths = rng.integers(1, 4097, size=32)
+    lengths[:8] = 0
+    lengths[8:20] = [255, 256, 257, 511, 512, 513, 1023, 1024, 1025, 2047, 2048, 4096]
+    case = make_case(list(lengths.astype(np.int32)), hq, hkv, dim, seed=5, capacity=4096)
+    g = to_gpu(case)
+    spec = DecodeSpec(32, hq, hkv, dim, 4096)
+    res = allocate_resources(spec, "cuda", backend)
+    actual = paged_decode(*g, resources=res, backend=backend)
+    torch.cuda.synchronize()
+    assert_close_dense(actual, torch_dense(*g))
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec))
+    assert torch.count_nonzero(actual[:8]) == 0

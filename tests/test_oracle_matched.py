@@ -144,6 +144,51 @@ def test_planted_oracle_mistakes_are_caught(old, new):
         assert not within_one_ulp(out, independent).all()
 
 
+@pytest.mark.parametrize("old,new", [
+    ("t0 = start + (count - 1 - i) * tile", "t0 = start + i * tile"),
+    ("np.matmul(bf16_round(p_[..., :nv])", "np.matmul((p_[..., :nv])"),
+])
+@pytest.mark.parametrize("lengths,hq,hkv,dim,cap,splits", [
+    ([3000, 700], 8, 2, 128, 4096, 1), ([4096, 1000], 32, 4, 256, 4096, 1),
+    ([1000, 2051], 8, 2, 128, 2051, 3)])
+def test_parity_gate_rejects_protocol_mistakes(old, new, lengths, hq, hkv, dim, cap, splits):
+    """The GPU parity gate (tests/parity.py) must fail a planted protocol mistake."""
+    from parity import assert_parity
+    mutant = _mutant(old, new)
+    case = make_case(lengths, hq, hkv, dim, capacity=cap)
+    plan = P.make_plan(len(lengths), hq, hkv, dim, cap, 256, num_splits=splits)
+    args = (plan["splits"], plan["tokens_per_split"], plan["tile_tokens"], plan["lse_lanes"])
+    wrong, _, _ = mutant.matched_decode(*case, *args)
+    right, _, _, bound, _ = M.matched_decode_with_bounds(*case, *args)
+    assert_parity(right, right, ambiguity=bound)
+    with pytest.raises(AssertionError):
+        assert_parity(wrong, right, ambiguity=bound)
+
+
+@pytest.mark.parametrize("old,new", [
+    # scores summed in float64 and rounded once (another summation order)
+    ("s[..., :nv] = np.matmul(qb, kt.transpose(1, 2, 0))",
+     "s[..., :nv] = np.matmul(qb.astype(np.float64), "
+     "kt.transpose(1, 2, 0).astype(np.float64)).astype(F32)"),
+    # exp2 evaluated in float64 and rounded once (another exp2 instruction)
+    ("p_ = exp2_32(fma32(s, c, (-(m_next * c))[..., None]))",
+     "p_ = np.exp2(fma32(s, c, (-(m_next * c))[..., None]).astype(np.float64)).astype(F32)"),
+])
+@pytest.mark.parametrize("seed", [1, 2])
+def test_ambiguity_bound_covers_fp32_rounding_differences(old, new, seed):
+    """Faithful implementations that only differ in fp32 rounding pass the gate,
+    although individual near-zero outputs move by many bf16 ulps."""
+    from parity import assert_parity
+    variant = _mutant(old, new)
+    case = make_case([4096, 4000, 1000, 2000, 3000, 256], 32, 4, 256, seed=seed, capacity=4096)
+    plan = P.make_plan(6, 32, 4, 256, 4096, 256, num_splits=1)
+    args = (plan["splits"], plan["tokens_per_split"], plan["tile_tokens"], plan["lse_lanes"])
+    other, other_partials, _ = variant.matched_decode(*case, *args)
+    right, partials, _, bound, partial_bound = M.matched_decode_with_bounds(*case, *args)
+    assert_parity(other, right, ambiguity=bound)
+    assert (np.abs(other_partials - partials) <= partial_bound + 2e-5 + 2e-5 * np.abs(partials)).all()
+
+
 def test_scale_log2_constant():
     # SCALE_LOG2 = scale * 1.4426950408889634 in double, used as float32.
     assert LOG2E == 1.4426950408889634
