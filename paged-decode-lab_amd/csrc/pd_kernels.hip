@@ -439,13 +439,16 @@ online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
       smax = fmaxf(smax, s[i]);
     }
     const float mn = fmaxf(m, smax);
-    const float alpha = exp_fast(m - mn);
+    // A row group with no valid row so far keeps m = -inf; subtract 0 instead
+    // of -inf so that exp(-inf - -inf) never turns the empty state into NaN.
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = exp_fast(m - mref);
     l *= alpha;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float pr = exp_fast(s[i] - mn);
+      const float pr = exp_fast(s[i] - mref);
       l += pr;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
