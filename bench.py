@@ -1,6 +1,7 @@
 """Paged decode benchmark on one MI355X.
 
-Default workload: matched split-KV decode (partition + LSE merge), B=1, Hq=16,
+Default workload: matched split-KV decode (partition + LSE merge, the two
+launches of matched_decode), B=1, Hq=16,
 Hkv=4, D=256, page 256, context 2064 (table capacity 2112), bf16 N(0,1)
 synthetic Q/K/V, pages in a seeded random physical order, the planner's plan
 for the device's CU count.  A step is one operator call (both kernels); the
@@ -120,14 +121,19 @@ def matched_case(torch, batch, hq, hkv, dim, capacity, lengths, seed, num_splits
     from paged_decode.spec import DecodeSpec
     from paged_decode import _native
     spec = DecodeSpec(batch, hq, hkv, dim, capacity)
-    res = allocate_matched_resources(spec, "cuda", num_splits=num_splits)
+    res = allocate_matched_resources(spec, "cuda", num_splits=num_splits, fused=True)
     q, k, v, table, lens = make_inputs(torch, batch, hq, hkv, dim, capacity, lengths, seed,
                                        pool_pages)
     plan = res.plan
     scale = dim ** -0.5
 
-    def full():
+    def fused():
         matched_decode(q, k, v, table, lens, resources=res)
+
+    def full():
+        _native.partition(q, k, v, table, lens, res.partials, res.lse, hkv, plan.splits,
+                          plan.tokens_per_split, plan.tile_tokens, scale)
+        _native.lse_merge(res.partials, res.lse, res.out, plan.lse_lanes)
 
     def partition():
         _native.partition(q, k, v, table, lens, res.partials, res.lse, hkv, plan.splits,
@@ -136,8 +142,8 @@ def matched_case(torch, batch, hq, hkv, dim, capacity, lengths, seed, num_splits
     def merge():
         _native.lse_merge(res.partials, res.lse, res.out, plan.lse_lanes)
 
-    return dict(spec=spec, plan=plan, full=full, partition=partition, merge=merge,
-                tensors=(q, k, v, table, lens), res=res)
+    return dict(spec=spec, plan=plan, full=full, fused=fused, partition=partition,
+                merge=merge, tensors=(q, k, v, table, lens), res=res)
 
 
 def fixed_partition_case(torch, case, part_tokens=1024):
@@ -250,6 +256,7 @@ def main():
         case["full"]()
     torch.cuda.synchronize()
     us = graph_time_us(torch, case["full"], args.steps)
+    fused_us = graph_time_us(torch, case["fused"], args.steps)
     part_us = graph_time_us(torch, case["partition"], args.steps)
     merge_us = graph_time_us(torch, case["merge"], args.steps)
     nbytes = algorithmic_bytes([ctx], 1, 16, 4, 256)
@@ -258,6 +265,7 @@ def main():
     part_tbps = part_bytes / part_us / 1e6
 
     extra = {"us_per_call": round(us, 3), "pct_peak": round(100 * tbps / PEAK_TBPS, 2),
+             "fused_single_launch_us_per_call": round(fused_us, 3),
              "partition_us": round(part_us, 3), "merge_us": round(merge_us, 3),
              "algorithmic_bytes": nbytes,
              "plan": f"{plan.splits} splits x {plan.tokens_per_split} tokens (sm_count {plan.sm_count})"}

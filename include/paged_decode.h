@@ -95,6 +95,23 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
                  int32_t batch, int32_t num_heads, int32_t head_dim, int32_t splits,
                  int32_t lse_lanes, pd_stream_t stream);
 
+/* Matched split-KV decode in one launch: the partition of pd_partition plus,
+ * in the last workgroup to finish each (sequence, kv head), the LSE merge of
+ * pd_lse_merge for that GQA group (bit-identical to pd_partition followed by
+ * pd_lse_merge).  Replaces the two launches of matched_decode
+ * (matched_splitkv.py:142-149).  `counters` is int32 [batch * num_kv_heads],
+ * all zero before the first call; every completed call leaves it all zero
+ * again, so the launch can be replayed from a graph without a reset.  Calls
+ * that share `counters` must not run concurrently.  Writes partials, lse and
+ * out bf16 [batch, num_heads, head_dim]. */
+int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                      const void* k, const void* v,
+                      const int32_t* table, int64_t table_stride_b, const int32_t* lengths,
+                      float* partials, float* lse, int32_t* counters, void* out,
+                      int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t splits, int32_t tokens_per_split, int32_t tile_tokens,
+                      double scale, pd_stream_t stream);
+
 /* Base decode: one workgroup per (sequence, query head), FP32 online softmax
  * over the whole context, out = acc / denom (0 for an empty row).  Replaces
  * _base (kernels.py:10-41) as launched by paged_decode (runtime.py:109).

@@ -30,6 +30,7 @@ namespace {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef float floatx2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -76,6 +77,98 @@ __device__ __forceinline__ u32x4_t load16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
 
+// Coherent (device-scope) float load: bypasses a possibly stale L2 line of
+// another XCD (global_load sc1) without invalidating the whole cache.
+template <bool kCoherent>
+__device__ __forceinline__ float load_f32(const float* p) {
+  if constexpr (kCoherent) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *p;
+}
+
+// ------------------------------------------------------ LSE merge arithmetic
+// Shared by the standalone merge kernel and the fused decode so that both give
+// bit-identical outputs.
+//
+// Merge weights of one (b, h) row, computed by one full wavefront: lane owns
+// splits `lane` and `lane + 64` (splits <= 128).  M = max lse (-inf -> 0),
+// S = sum exp(lse - M), L = ln S + M (+inf when S == 0), w_p = exp(lse_p - L)
+// (matched_splitkv.py:107-120; an all-empty row gets w = 0 everywhere).
+template <bool kCoherent>
+__device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lane,
+                                            float& w0, float& w1) {
+  const float v0 = lane < splits ? load_f32<kCoherent>(lrow + lane) : -INFINITY;
+  const float v1 = lane + 64 < splits ? load_f32<kCoherent>(lrow + lane + 64) : -INFINITY;
+  float mx = wave_max(fmaxf(v0, v1));
+  if (mx == -INFINITY) mx = 0.f;
+  const float total = wave_sum(exp_fast(v0 - mx) + exp_fast(v1 - mx));
+  const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
+  w0 = exp_fast(v0 - logsum);
+  w1 = exp_fast(v1 - logsum);
+}
+
+// Buffer resource (V#) over `bytes` bytes at `base`; word 3 is the gfx9-family
+// raw-buffer format.  Loads at or past `bytes` return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// E consecutive floats at byte offset `off`; kCoherent sets the sc1 cache
+// policy bit (device-scope coherent, so a line another XCD wrote is re-read).
+// The builtins' results are bit-cast as whole vectors to float vectors before
+// any element is read: reading elements of their integer vector results
+// directly made this compiler emit a single dword load for the whole vector.
+template <int E, bool kCoherent>
+__device__ __forceinline__ void buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, int off,
+                                                float (&x)[E]) {
+  constexpr int aux = kCoherent ? 16 : 0;
+  if constexpr (E == 1) {
+    x[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, aux));
+  } else if constexpr (E == 2) {
+    const u32x2_t t = __builtin_amdgcn_raw_buffer_load_b64(rsrc, off, 0, aux);
+    const floatx2_t f = __builtin_bit_cast(floatx2_t, t);
+    x[0] = f.x;
+    x[1] = f.y;
+  } else {
+    static_assert(E % 4 == 0, "vector width");
+#pragma unroll
+    for (int i = 0; i < E; i += 4) {
+      const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 4 * i, 0, aux);
+      const floatx4_t f = __builtin_bit_cast(floatx4_t, t);
+      x[i] = f.x;
+      x[i + 1] = f.y;
+      x[i + 2] = f.z;
+      x[i + 3] = f.w;
+    }
+  }
+}
+
+// acc[e] = fma(w_p, partial_p[e], acc[e]) for p = 0, 1, ..., splits-1 in order
+// (matched_splitkv.py:121-126).  `row` is the (b, h) row of partials
+// [splits][D]; this thread owns elements dd .. dd+E-1.  Splits are processed
+// kBatch at a time as straight-line vector loads followed by the FMA chain, so
+// 36 splits cost two memory round trips.  Past the last split the loads return
+// zero and `weight` must return zero, so the padding steps are fma(0, 0, acc)
+// and leave acc unchanged (a -0 accumulator becomes +0).
+template <int E, bool kCoherent, typename WeightFn>
+__device__ __forceinline__ void weighted_sum(const float* __restrict__ row, int D, int dd,
+                                             int splits, WeightFn weight, float (&acc)[E]) {
+  constexpr int kBatch = 128 / E < 32 ? 128 / E : 32;  // about 128 floats in flight
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(row, splits * D * 4);
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += kBatch) {
+    float x[kBatch][E];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) buffer_load_f32<E, kCoherent>(rsrc, ((s0 + j) * D + dd) * 4, x[j]);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const float wj = weight(s0 + j);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = fmaf(wj, x[j][e], acc[e]);
+    }
+  }
+}
+
 // ------------------------------------------------------- matched partition
 //
 // Tile geometry: TILE = 16384 / D tokens (64/128/256 for D = 256/128/64), the
@@ -110,32 +203,50 @@ struct TileRegs {
   u32x4_t v[4][2];
 };
 
+// 16 bytes at byte offset `off` of a buffer (zero past its end).
+__device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int off) {
+  const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+  return t;
+}
+
+// The K and V rows of one tile as buffers that end after row nvalid - 1, so
+// rows past the sequence end read as zero without being fetched (NaN-poisoned
+// slots and dead pages are never touched) and every load is unconditional.
+// Byte sizes fit 32 bits: nvalid <= 256 and Hkv*D*512 < 2^31 (launcher check).
+struct TileBuffers {
+  __amdgpu_buffer_rsrc_t k, v;
+};
+
+__device__ __forceinline__ TileBuffers tile_buffers(const uint16_t* __restrict__ k,
+                                                    const uint16_t* __restrict__ v,
+                                                    const int32_t* __restrict__ trow, int t0,
+                                                    int end, int64_t RS, int kh, int D) {
+  const int64_t page = trow[t0 >> 8];
+  const int64_t base = (page * 256 + (t0 & 255)) * RS + int64_t(kh) * D;
+  const int bytes = (end - t0 < 256 ? end - t0 : 256) * int(RS) * 2;
+  return {buffer_rsrc(k + base, bytes), buffer_rsrc(v + base, bytes)};
+}
+
 template <int D, int GP>
 __device__ __forceinline__ void matched_load(TileRegs<D, GP>& R, const uint16_t* __restrict__ k,
                                              const uint16_t* __restrict__ v,
                                              const int32_t* __restrict__ trow, int t0, int end,
                                              int64_t RS, int kh, int lane, int w, int rg, int d0) {
   using C = Matched<D, GP>;
-  const int64_t page = trow[t0 >> 8];
-  const int64_t base = (page * 256 + (t0 & 255)) * RS + int64_t(kh) * D;
-  const int nvalid = end - t0;
+  const TileBuffers buf = tile_buffers(k, v, trow, t0, end, RS, kh, D);
   const int qh = lane & 15, qg = lane >> 4;
 #pragma unroll
   for (int g = 0; g < C::kNG; ++g) {
-    const int row = w * C::kTW + 16 * g + qh;
-    const uint16_t* src = k + base + int64_t(row) * RS + 8 * qg;
+    const int off = ((w * C::kTW + 16 * g + qh) * int(RS) + 8 * qg) * 2;
 #pragma unroll
-    for (int c = 0; c < C::kCH; ++c)
-      R.k[g][c] = row < nvalid ? load16(src + 32 * c) : u32x4_t{0, 0, 0, 0};
+    for (int c = 0; c < C::kCH; ++c) R.k[g][c] = buffer_load16(buf.k, off + 64 * c);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int par = 0; par < 2; ++par) {
-      const int row = j * (C::kTile / 4) + 2 * rg + par;
-      R.v[j][par] = row < nvalid ? load16(v + base + int64_t(row) * RS + d0)
-                                 : u32x4_t{0, 0, 0, 0};
-    }
+    for (int par = 0; par < 2; ++par)
+      R.v[j][par] =
+          buffer_load16(buf.v, ((j * (C::kTile / 4) + 2 * rg + par) * int(RS) + d0) * 2);
 }
 
 template <int D, int GP>
@@ -143,19 +254,28 @@ struct MatchedShared {
   union alignas(16) {
     uint16_t pbuf[GP][Matched<D, GP>::kTile];
     float red[2][GP][D];
+    float wts[GP][128];
   } u;
   float wmax[4][16];
   float lsum[4][16];
   float mfin[16];
+  int last;
 };
 
-template <int D, int GP>
+// kFused = false: the partition alone (pd_partition).
+// kFused = true: after writing its partial, each workgroup releases it at
+// device scope and increments counters[b, kh]; the workgroup that completes
+// the count acquires, merges all splits of its GQA group into `out` with the
+// same arithmetic as lse_merge_kernel, and resets the counter to 0, so the
+// counters are zero again when the kernel ends (graph replays need no reset).
+template <int D, int GP, bool kFused>
 __global__ void __launch_bounds__(kThreads, GP >= 16 ? 1 : 2)
 matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
                          const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                          const int32_t* __restrict__ table, int64_t tsb,
                          const int32_t* __restrict__ lengths, float* __restrict__ partials,
-                         float* __restrict__ lse_out, int Hq, int Hkv, int G, int splits, int T,
+                         float* __restrict__ lse_out, int* __restrict__ counters,
+                         uint16_t* __restrict__ out, int Hq, int Hkv, int G, int splits, int T,
                          float scale, float c) {
   using C = Matched<D, GP>;
   constexpr int TILE = C::kTile;
@@ -277,11 +397,29 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
     }
   };
 
-  // Reverse tile walk (matched_splitkv.py:71): last tile first.
-  for (int ti = count - 1; ti >= 0; --ti) {
-    TileRegs<D, GP> R;
-    matched_load<D, GP>(R, k, v, trow, start + ti * TILE, end, RS, kh, lane, w, rg, d0);
-    process(R, ti);
+  // Reverse tile walk (matched_splitkv.py:71): last tile first.  Up to GQA
+  // groups of 4 the registers hold a second tile, so the loads of the next tile
+  // are in flight while the current one is computed.
+  if constexpr (GP <= 4) {
+    if (count > 0) {
+      TileRegs<D, GP> R;
+      matched_load<D, GP>(R, k, v, trow, start + (count - 1) * TILE, end, RS, kh, lane, w, rg,
+                          d0);
+      for (int ti = count - 1; ti >= 0; --ti) {
+        TileRegs<D, GP> N;
+        if (ti > 0)
+          matched_load<D, GP>(N, k, v, trow, start + (ti - 1) * TILE, end, RS, kh, lane, w, rg,
+                              d0);
+        process(R, ti);
+        R = N;
+      }
+    }
+  } else {
+    for (int ti = count - 1; ti >= 0; --ti) {
+      TileRegs<D, GP> R;
+      matched_load<D, GP>(R, k, v, trow, start + ti * TILE, end, RS, kh, lane, w, rg, d0);
+      process(R, ti);
+    }
   }
 
   // ---- epilogue: combine the 4 waves' accumulators and denominators
@@ -318,9 +456,55 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
     const float inv = rcp_fast(safe);
     const int64_t orow = (int64_t(b) * Hq + kh * G + h) * splits + p;
     float* dst = partials + orow * D + dd;
+    const float lv = den > 0.f ? fmaf(sm.mfin[h], scale, ln_fast(safe)) : -INFINITY;
+    if constexpr (kFused) {
+      // Device-scope stores (global_store sc1): written through to the
+      // coherence point, so another XCD can read them without any L2 flush.
 #pragma unroll
-    for (int e = 0; e < C::kE; ++e) dst[e] = (sm.u.red[0][h][dd + e] + sm.u.red[1][h][dd + e]) * inv;
-    if (dd == 0) lse_out[orow] = den > 0.f ? fmaf(sm.mfin[h], scale, ln_fast(safe)) : -INFINITY;
+      for (int e = 0; e < C::kE; ++e)
+        __hip_atomic_store(dst + e, (sm.u.red[0][h][dd + e] + sm.u.red[1][h][dd + e]) * inv,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (dd == 0) __hip_atomic_store(lse_out + orow, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+#pragma unroll
+      for (int e = 0; e < C::kE; ++e) dst[e] = (sm.u.red[0][h][dd + e] + sm.u.red[1][h][dd + e]) * inv;
+      if (dd == 0) lse_out[orow] = lv;
+    }
+  }
+
+  if constexpr (kFused) {
+    // Split-completion count.  Every partial and LSE value exchanged between
+    // workgroups is written and read with device-scope (sc1) accesses.  The
+    // barrier waits until this workgroup's stores have completed before thread
+    // 0 increments the counter, and the last workgroup issues its loads only
+    // after its increment returned splits - 1, i.e. after every other
+    // workgroup's stores completed.  No cache-wide writeback or invalidate is
+    // needed, so the KV tiles other calls keep in L2 stay resident.
+    int* counter = counters + int64_t(b) * Hkv + kh;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (tid == 0)
+      sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                splits - 1;
+    __syncthreads();
+    if (!sm.last) return;
+    const int64_t row0 = int64_t(b) * Hq + kh * G;  // first query head of the group
+    for (int hh = w; hh < G; hh += 4) {
+      float w0, w1;
+      lse_weights<true>(lse_out + (row0 + hh) * splits, splits, lane, w0, w1);
+      sm.u.wts[hh][lane] = w0;        // zero for lanes past the last split
+      sm.u.wts[hh][lane + 64] = w1;
+    }
+    __syncthreads();
+    if (idx0 < C::kOut && h < G) {
+      float acc[C::kE];
+      weighted_sum<C::kE, true>(partials + (row0 + h) * splits * D, D, dd, splits,
+                                [&](int s) { return sm.u.wts[h][s]; }, acc);
+      uint16_t* dst = out + (row0 + h) * D + dd;
+#pragma unroll
+      for (int e = 0; e < C::kE; ++e) dst[e] = uint16_t(bf16_bits(acc[e]));
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -333,35 +517,15 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
   constexpr int D = VEC * 64;
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
-  const float* lrow = lse + int64_t(row) * splits;
-  const float v0 = lane < splits ? lrow[lane] : -INFINITY;
-  const float v1 = lane + 64 < splits ? lrow[lane + 64] : -INFINITY;
-  float mx = wave_max(fmaxf(v0, v1));
-  if (mx == -INFINITY) mx = 0.f;
-  const float total = wave_sum(exp_fast(v0 - mx) + exp_fast(v1 - mx));
-  const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
-  const float w0 = exp_fast(v0 - logsum);
-  const float w1 = exp_fast(v1 - logsum);
+  float w0, w1;
+  lse_weights<false>(lse + int64_t(row) * splits, splits, lane, w0, w1);
+  auto weight = [&](int s) {  // w of lanes past the last split is exp(-inf) = 0
+    const int src = s < 64 ? __builtin_bit_cast(int, w0) : __builtin_bit_cast(int, w1);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(src, s & 63));
+  };
   float acc[VEC];
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
-  const float* prow = partials + int64_t(row) * splits * D + lane * VEC;
-#pragma unroll 4
-  for (int s = 0; s < splits; ++s) {
-    const float ws = s < 64 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w0), s))
-                            : __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w1), s - 64));
-    const float* src = prow + int64_t(s) * D;
-    float x[VEC];
-    if constexpr (VEC == 4) {
-      const floatx4_t t = *reinterpret_cast<const floatx4_t*>(src);
-      x[0] = t[0]; x[1] = t[1]; x[2] = t[2]; x[3] = t[3];
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) x[e] = src[e];
-    }
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] = fmaf(ws, x[e], acc[e]);
-  }
+  weighted_sum<VEC, false>(partials + int64_t(row) * splits * D, D, lane * VEC, splits, weight,
+                           acc);
   uint16_t* dst = out + int64_t(row) * D + lane * VEC;
 #pragma unroll
   for (int e = 0; e < VEC; ++e) dst[e] = uint16_t(bf16_bits(acc[e]));
@@ -414,16 +578,14 @@ online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 
   for (int t0 = start; t0 < end; t0 += TILE) {
-    const int64_t page = trow[t0 >> 8];
-    const int64_t base = (page * 256 + (t0 & 255)) * RS + int64_t(kh) * D + d0;
+    const TileBuffers buf = tile_buffers(k, v, trow, t0, end, RS, kh, D);
     const int nvalid = end - t0;
     u32x4_t kr[8], vr[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int row = rg + i * C::kRG;
-      const bool ok = row < nvalid;
-      kr[i] = ok ? load16(k + base + int64_t(row) * RS) : u32x4_t{0, 0, 0, 0};
-      vr[i] = ok ? load16(v + base + int64_t(row) * RS) : u32x4_t{0, 0, 0, 0};
+      const int off = ((rg + i * C::kRG) * int(RS) + d0) * 2;
+      kr[i] = buffer_load16(buf.k, off);
+      vr[i] = buffer_load16(buf.v, off);
     }
     float s[8];
     float smax = -INFINITY;
@@ -556,18 +718,34 @@ int check_qkv(const void* q, int64_t qsb, int64_t qsh, const void* k, const void
       qsh < 0)
     return pd::fail(PD_EINVAL,
                     "Q/K/V rows must be 16-byte aligned (strides multiples of 8 elements)");
+  if (int64_t(num_kv_heads) * head_dim * 512 >= (int64_t(1) << 31))
+    return pd::fail(PD_EINVAL, "a 256-slot page of one KV tensor must stay below 2 GiB");
   return PD_OK;
 }
 
-template <int D>
-int launch_partition_d(int gp, dim3 grid, hipStream_t stream, const uint16_t* q, int64_t qsb,
-                       int64_t qsh, const uint16_t* k, const uint16_t* v, const int32_t* table,
-                       int64_t tsb, const int32_t* lengths, float* partials, float* lse, int Hq,
-                       int Hkv, int G, int splits, int T, float scale, float c) {
-#define PD_LAUNCH_GP(GPV)                                                                    \
-  hipLaunchKernelGGL((matched_partition_kernel<D, GPV>), grid, dim3(kThreads), 0, stream, q, \
-                     qsb, qsh, k, v, table, tsb, lengths, partials, lse, Hq, Hkv, G, splits, \
-                     T, scale, c)
+struct PartitionArgs {
+  const uint16_t* q;
+  int64_t qsb, qsh;
+  const uint16_t* k;
+  const uint16_t* v;
+  const int32_t* table;
+  int64_t tsb;
+  const int32_t* lengths;
+  float* partials;
+  float* lse;
+  int* counters;
+  uint16_t* out;
+  int Hq, Hkv, G, splits, T;
+  float scale, c;
+};
+
+template <int D, bool kFused>
+void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
+#define PD_LAUNCH_GP(GPV)                                                                     \
+  hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused>), grid, dim3(kThreads), 0,     \
+                     stream, a.q, a.qsb, a.qsh, a.k, a.v, a.table, a.tsb, a.lengths,          \
+                     a.partials, a.lse, a.counters, a.out, a.Hq, a.Hkv, a.G, a.splits, a.T,   \
+                     a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_GP(1); break;
     case 2: PD_LAUNCH_GP(2); break;
@@ -576,7 +754,6 @@ int launch_partition_d(int gp, dim3 grid, hipStream_t stream, const uint16_t* q,
     default: PD_LAUNCH_GP(16); break;
   }
 #undef PD_LAUNCH_GP
-  return launch_status("pd_partition");
 }
 
 int padded_group(int g) {
@@ -585,17 +762,17 @@ int padded_group(int g) {
   return gp;
 }
 
-}  // namespace
-
-extern "C" int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                            const void* k, const void* v, const int32_t* table,
-                            int64_t table_stride_b, const int32_t* lengths, float* partials,
-                            float* lse, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
-                            int32_t head_dim, int32_t splits, int32_t tokens_per_split,
-                            int32_t tile_tokens, double scale, pd_stream_t stream) {
+// Validation and dispatch shared by pd_partition (fused = false) and
+// pd_matched_decode (fused = true).
+int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, int64_t qsh,
+                    const void* k, const void* v, const int32_t* table, int64_t tsb,
+                    const int32_t* lengths, float* partials, float* lse, int32_t* counters,
+                    void* out, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t splits, int32_t tokens_per_split,
+                    int32_t tile_tokens, double scale, pd_stream_t stream) {
   pd::clear_error();
-  if (int st = check_qkv(q, q_stride_b, q_stride_h, k, v, table, lengths, batch, num_heads,
-                         num_kv_heads, head_dim))
+  if (int st = check_qkv(q, qsb, qsh, k, v, table, lengths, batch, num_heads, num_kv_heads,
+                         head_dim))
     return st;
   const int G = num_heads / num_kv_heads;
   if (G > 16)
@@ -606,33 +783,56 @@ extern "C" int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_
                     head_dim);
   if (tokens_per_split <= 0 || tokens_per_split % tile_tokens)
     return pd::fail(PD_EINVAL, "tokens_per_split must be a positive multiple of tile_tokens");
-  if (!partials || !lse) return pd::fail(PD_EINVAL, "invalid matched workspace");
+  if (!partials || !lse || (fused && (!counters || !out)))
+    return pd::fail(PD_EINVAL, "invalid matched workspace");
   if (!(scale > 0.0) || !std::isfinite(scale))
     return pd::fail(PD_EINVAL, "positive finite scale required");
   if (batch > 65535 || num_kv_heads > 65535)
     return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
-  const float s32 = float(scale);
-  const float c = float(scale * 1.4426950408889634);  // SCALE_LOG2 (matched_splitkv.py:363)
+  PartitionArgs a{static_cast<const uint16_t*>(q), qsb, qsh, static_cast<const uint16_t*>(k),
+                  static_cast<const uint16_t*>(v), table, tsb, lengths, partials, lse,
+                  counters, static_cast<uint16_t*>(out), num_heads, num_kv_heads, G, splits,
+                  tokens_per_split, float(scale),
+                  float(scale * 1.4426950408889634)};  // SCALE_LOG2 (matched_splitkv.py:363)
   const dim3 grid(splits, num_kv_heads, batch);
-  const auto* qq = static_cast<const uint16_t*>(q);
-  const auto* kk = static_cast<const uint16_t*>(k);
-  const auto* vv = static_cast<const uint16_t*>(v);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int gp = padded_group(G);
-  switch (head_dim) {
-    case 64:
-      return launch_partition_d<64>(gp, grid, st, qq, q_stride_b, q_stride_h, kk, vv, table,
-                                    table_stride_b, lengths, partials, lse, num_heads,
-                                    num_kv_heads, G, splits, tokens_per_split, s32, c);
-    case 128:
-      return launch_partition_d<128>(gp, grid, st, qq, q_stride_b, q_stride_h, kk, vv, table,
-                                     table_stride_b, lengths, partials, lse, num_heads,
-                                     num_kv_heads, G, splits, tokens_per_split, s32, c);
-    default:
-      return launch_partition_d<256>(gp, grid, st, qq, q_stride_b, q_stride_h, kk, vv, table,
-                                     table_stride_b, lengths, partials, lse, num_heads,
-                                     num_kv_heads, G, splits, tokens_per_split, s32, c);
+  switch (head_dim * 2 + (fused ? 1 : 0)) {
+    case 128: launch_partition_d<64, false>(gp, grid, st, a); break;
+    case 129: launch_partition_d<64, true>(gp, grid, st, a); break;
+    case 256: launch_partition_d<128, false>(gp, grid, st, a); break;
+    case 257: launch_partition_d<128, true>(gp, grid, st, a); break;
+    case 512: launch_partition_d<256, false>(gp, grid, st, a); break;
+    default: launch_partition_d<256, true>(gp, grid, st, a); break;
   }
+  return launch_status(what);
+}
+
+}  // namespace
+
+extern "C" int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                            const void* k, const void* v, const int32_t* table,
+                            int64_t table_stride_b, const int32_t* lengths, float* partials,
+                            float* lse, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t splits, int32_t tokens_per_split,
+                            int32_t tile_tokens, double scale, pd_stream_t stream) {
+  return partition_entry("pd_partition", false, q, q_stride_b, q_stride_h, k, v, table,
+                         table_stride_b, lengths, partials, lse, nullptr, nullptr, batch,
+                         num_heads, num_kv_heads, head_dim, splits, tokens_per_split,
+                         tile_tokens, scale, stream);
+}
+
+extern "C" int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                 const void* k, const void* v, const int32_t* table,
+                                 int64_t table_stride_b, const int32_t* lengths,
+                                 float* partials, float* lse, int32_t* counters, void* out,
+                                 int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, int32_t splits, int32_t tokens_per_split,
+                                 int32_t tile_tokens, double scale, pd_stream_t stream) {
+  return partition_entry("pd_matched_decode", true, q, q_stride_b, q_stride_h, k, v, table,
+                         table_stride_b, lengths, partials, lse, counters, out, batch,
+                         num_heads, num_kv_heads, head_dim, splits, tokens_per_split,
+                         tile_tokens, scale, stream);
 }
 
 extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, int32_t batch,

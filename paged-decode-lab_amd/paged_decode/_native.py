@@ -33,6 +33,8 @@ SIGNATURES = {
     "pd_partition": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
                      _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_lse_merge": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
+    "pd_matched_decode": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+                          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_base": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_split_fixed": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
                        _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
@@ -94,6 +96,17 @@ def partition(q, k, v, tables, lengths, partials, lse, num_kv_heads, splits, tok
                              tables.data_ptr(), tables.stride(0), lengths.data_ptr(),
                              partials.data_ptr(), lse.data_ptr(), b, h, num_kv_heads, d, splits,
                              tokens_per_split, tile_tokens, scale, stream_handle(q.device)))
+
+
+def matched_decode(q, k, v, tables, lengths, partials, lse, counters, out, num_kv_heads, splits,
+                   tokens_per_split, tile_tokens, scale):
+    b, h, d = q.shape
+    check(lib().pd_matched_decode(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                                  v.data_ptr(), tables.data_ptr(), tables.stride(0),
+                                  lengths.data_ptr(), partials.data_ptr(), lse.data_ptr(),
+                                  counters.data_ptr(), out.data_ptr(), b, h, num_kv_heads, d,
+                                  splits, tokens_per_split, tile_tokens, scale,
+                                  stream_handle(q.device)))
 
 
 def lse_merge(partials, lse, out, lse_lanes):

@@ -3,8 +3,15 @@
 Mirrors matched_splitkv.py of the reference (src/paged_decode/matched_splitkv.py:15-150):
 ``MatchedResources``, ``allocate_matched_resources`` and ``matched_decode``,
 with the same plan, workspace shapes, contract checks and error messages.
-The two launches are the HIP kernels pd_partition and pd_lse_merge
-(include/paged_decode.h).
+
+By default ``matched_decode`` launches the partition and the LSE merge as two
+kernels (pd_partition, pd_lse_merge), like the reference.  Resources
+allocated with ``fused=True`` carry a zeroed int32 counter per (sequence, kv
+head) and run both in one launch instead (pd_matched_decode: the last
+workgroup of each GQA group merges it).  Both give bit-identical outputs; the
+two-launch path is faster on MI355X at the benchmark shapes, because the
+single launch exchanges the partials between XCDs through device-coherent
+memory inside the kernel.
 """
 from dataclasses import dataclass
 import math
@@ -23,9 +30,10 @@ class MatchedResources:
     out: torch.Tensor
     partials: torch.Tensor
     lse: torch.Tensor
+    counters: torch.Tensor | None = None
 
 
-def allocate_matched_resources(spec, device, *, num_splits=0):
+def allocate_matched_resources(spec, device, *, num_splits=0, fused=False):
     device = torch.device(device)
     if device.type != "cuda":
         raise ValueError("matched resources require CUDA")
@@ -37,7 +45,9 @@ def allocate_matched_resources(spec, device, *, num_splits=0):
         torch.empty((spec.max_batch, spec.num_heads, spec.head_dim), device=device,
                     dtype=torch.bfloat16),
         torch.empty((*shape, spec.head_dim), device=device, dtype=torch.float32),
-        torch.empty(shape, device=device, dtype=torch.float32))
+        torch.empty(shape, device=device, dtype=torch.float32),
+        torch.zeros((spec.max_batch * spec.num_kv_heads,), device=device, dtype=torch.int32)
+        if fused else None)
 
 
 def _check_matched(q, tables, resources, scale):
@@ -52,6 +62,11 @@ def _check_matched(q, tables, resources, scale):
         if (tensor.shape != geometry or tensor.device != q.device
                 or tensor.dtype != torch.float32 or not tensor.is_contiguous()):
             raise ValueError("invalid matched workspace")
+    counters = resources.counters
+    if counters is not None and (
+            counters.shape != (spec.max_batch * spec.num_kv_heads,) or counters.device != q.device
+            or counters.dtype != torch.int32 or not counters.is_contiguous()):
+        raise ValueError("invalid matched workspace")
 
 
 def matched_decode(q, k, v, tables, lengths, *, resources, scale=None):
@@ -60,6 +75,11 @@ def matched_decode(q, k, v, tables, lengths, *, resources, scale=None):
     _validate(q, k, v, tables, lengths, resources, "hip_base", scale)
     _check_matched(q, tables, resources, scale)
     spec, plan = resources.spec, resources.plan
+    if resources.counters is not None:
+        _native.matched_decode(q, k, v, tables, lengths, resources.partials, resources.lse,
+                               resources.counters, resources.out, spec.num_kv_heads, plan.splits,
+                               plan.tokens_per_split, plan.tile_tokens, scale)
+        return resources.out
     _native.partition(q, k, v, tables, lengths, resources.partials, resources.lse,
                       spec.num_kv_heads, plan.splits, plan.tokens_per_split, plan.tile_tokens,
                       scale)

@@ -124,6 +124,58 @@ def test_graph_replay_and_empty_partitions():
             assert torch.count_nonzero(captured) == 0
 
 
+def _two_kernel_resources(res):
+    from paged_decode.matched_splitkv import MatchedResources
+    return MatchedResources(res.spec, res.plan, torch.empty_like(res.out),
+                            torch.empty_like(res.partials), torch.empty_like(res.lse))
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32)
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,dim,cap,splits", [
+    ([2064], 16, 4, 256, 2112, 0), ([528], 16, 4, 256, 528, 0),
+    ([0, 1, 257, 1000], 8, 2, 128, 1000, 0), ([0, 0, 0], 8, 2, 64, 2051, 0),
+    ([2051, 1, 0, 1025], 32, 4, 256, 4096, 1), ([2051, 1, 0, 1025], 32, 2, 128, 4096, 6),
+    ([3000, 17], 12, 4, 64, 4096, 0), ([4096] * 3, 16, 1, 256, 4096, 0)])
+def test_fused_decode_is_bit_identical_to_two_launches(lengths, hq, hkv, dim, cap, splits):
+    g = to_gpu(make_case(lengths, hq, hkv, dim, seed=31, capacity=cap))
+    res = allocate_matched_resources(DecodeSpec(len(lengths), hq, hkv, dim, cap), "cuda",
+                                     num_splits=splits, fused=True)
+    two = _two_kernel_resources(res)
+    for _ in range(3):
+        fused = matched_decode(*g, resources=res).clone()
+        split = matched_decode(*g, resources=two).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(fused), _bits(split))
+        assert torch.equal(_bits(res.partials), _bits(two.partials))
+        assert torch.equal(_bits(res.lse), _bits(two.lse))
+        assert torch.count_nonzero(res.counters) == 0
+
+
+def test_fused_counters_return_to_zero_across_graph_replays():
+    case = make_case([2064], 16, 4, 256, seed=3, capacity=2112)
+    g = to_gpu(case)
+    res = allocate_matched_resources(DecodeSpec(1, 16, 4, 256, 2112), "cuda", fused=True)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            matched_decode(*g, resources=res)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(8):
+            out = matched_decode(*g, resources=res)
+    expected = matched_decode(*g, resources=_two_kernel_resources(res)).clone()
+    for _ in range(5):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(res.counters) == 0
+        assert torch.equal(_bits(out), _bits(expected))
+
+
 def test_fixed_plan_contract():
     # reference tests/test_matched_splitkv.py:60-69.
     g = to_gpu(make_case([1, 2, 0], 8, 2, 256, capacity=2051))
