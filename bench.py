@@ -117,7 +117,8 @@ def reference_protocol_us(torch, fn, rounds=5, replays=20):
 
 def matched_case(torch, batch, hq, hkv, dim, capacity, lengths, seed, num_splits=0,
                  pool_pages=None):
-    from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
+    from paged_decode.matched_splitkv import (MatchedResources, allocate_matched_resources,
+                                              matched_decode)
     from paged_decode.spec import DecodeSpec
     from paged_decode import _native
     spec = DecodeSpec(batch, hq, hkv, dim, capacity)
@@ -127,13 +128,14 @@ def matched_case(torch, batch, hq, hkv, dim, capacity, lengths, seed, num_splits
     plan = res.plan
     scale = dim ** -0.5
 
+    # Default resources (no counters): matched_decode's two launches.
+    two_launch = MatchedResources(spec, plan, res.out, res.partials, res.lse)
+
     def fused():
         matched_decode(q, k, v, table, lens, resources=res)
 
     def full():
-        _native.partition(q, k, v, table, lens, res.partials, res.lse, hkv, plan.splits,
-                          plan.tokens_per_split, plan.tile_tokens, scale)
-        _native.lse_merge(res.partials, res.lse, res.out, plan.lse_lanes)
+        matched_decode(q, k, v, table, lens, resources=two_launch)
 
     def partition():
         _native.partition(q, k, v, table, lens, res.partials, res.lse, hkv, plan.splits,
@@ -230,6 +232,51 @@ def bandwidth_sweep(torch, seed=64, calls=20):
     return result
 
 
+def committed_traffic(key):
+    """HBM bytes per dispatch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)[key]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def profile_launches(torch, which, calls=50):
+    """Eager launches for rocprofv3 (kernel trace / PMC counters).
+
+    calibrate: a 256 MiB device copy (known bytes: 256 MiB read + 256 MiB
+    written), used to scale FETCH_SIZE / WRITE_SIZE.  headline: partition and
+    merge at the headline shape.  sweep: partition and merge of the bandwidth sweep.
+    """
+    import numpy as np
+    src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device="cuda")
+    src.normal_()
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    if "headline" in which:
+        case = matched_case(torch, 1, 16, 4, 256, 2112, [2064], 20261105)
+        for _ in range(calls):
+            case["partition"]()
+            case["merge"]()
+        torch.cuda.synchronize()
+        del case
+    if "sweep" in which:
+        rng = np.random.default_rng(64)
+        lengths = rng.integers(1, 32769, size=64).tolist()
+        pool = int(100e9 // (PAGE * 8 * 128 * 2))
+        case = matched_case(torch, 64, 32, 8, 128, 32768, lengths, 64, pool_pages=pool)
+        for _ in range(3):
+            case["partition"]()
+            case["merge"]()
+        torch.cuda.synchronize()
+        del case
+    torch.cuda.empty_cache()
+    print(json.dumps({"profiled": which}))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -239,6 +286,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the extra measurements")
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU run")
+    ap.add_argument("--profile", default=None, metavar="headline,sweep",
+                    help="only make eager launches for rocprofv3 (calibration copy + cases)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -248,6 +297,9 @@ def main():
     import torch
     from paged_decode import _native
     _native.lib()
+    if args.profile:
+        profile_launches(torch, args.profile)
+        return
 
     ctx, capacity = args.ctx, max(2112, args.ctx)
     case = matched_case(torch, 1, 16, 4, 256, capacity, [ctx], 20261105)
@@ -298,7 +350,7 @@ def main():
                "all_threads_us_per_call": round(allc["us"], 1),
                "host_cpus": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
                "sample": (f"NumPy restatement of the reference CPU path (streaming_reference, "
-                          f"1024-token partitions, 64-token tiles, FP32) on the same C2 shape, "
+                          f"1024-token partitions, 64-token tiles, FP32) on the same B=1 Hq=16 Hkv=4 D=256 shape, "
                           f"median of {allc['calls']} calls in ~{args.cpu_budget:.0f} s")}
 
     line = {
@@ -310,7 +362,10 @@ def main():
                                f"ctx {ctx} (capacity {capacity}), planner plan, hot cache",
                    "global_batch": 1, "seq_len": ctx, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(part_tbps * 1000, 1), "peak": PEAK_TBPS * 1000,
-                     "unit": "GB/s", "frac": round(part_tbps / PEAK_TBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(part_tbps / PEAK_TBPS, 4),
+                     "traffic": committed_traffic(
+                         "matched_partition_kernel<256,4,false> d256 gqa4 ctx2064"),
+                     "traffic_source": "profiles/traffic.json (2.0 x FETCH_SIZE + WRITE_SIZE)",
                      "kernel": "matched_partition_kernel<256,4>", "bytes_per_launch": part_bytes,
                      "us_per_launch": round(part_us, 3)},
         "cpu_baseline": cpu,

@@ -37,17 +37,17 @@ def test_reference_bad_group():
 
 @pytest.mark.parametrize("args,expected", [
     # Hand derivations at sm_count=256 (virtual SMs 512).
-    # C2: B=1, Hkv=4, D=256, width 9 -> 36 blocks of 64; eff(n) = 4n/512 is
+    # B=1, Hkv=4, D=256, width 9 -> 36 blocks of 64; eff(n) = 4n/512 is
     # maximal at n=36 and the first eligible n reaching .85 of it is 36.
     ((1, 16, 4, 256, 2064, 256), (36, 64, 32)),
     ((1, 16, 4, 256, 2112, 256), (36, 64, 32)),
     # ctx 528 -> width 3, 12 blocks; eff maximal at the last eligible n=12.
     ((1, 16, 4, 256, 528, 256), (12, 64, 16)),
-    # C1: B=4, Hkv=2, D=128 (tile 128), width 4 -> 8 blocks -> 8 splits of 128.
+    # B=4, Hkv=2, D=128 (tile 128), width 4 -> 8 blocks -> 8 splits of 128.
     ((4, 8, 2, 128, 1000, 256), (8, 128, 8)),
-    # C3: work = 64*8 = 512 >= f32(.8*512) -> 1 split.
+    # B=64, Hkv=8: work = 64*8 = 512 >= f32(.8*512) -> 1 split.
     ((64, 32, 8, 128, 32768, 256), (1, 32768, 1)),
-    # C4: work 128*16 and 128*4 are >= 409.6 -> 1 split.
+    # B=128 with Hkv 16 or 4: work 128*16 and 128*4 are >= 409.6 -> 1 split.
     ((128, 16, 16, 64, 4096, 256), (1, 4096, 1)),
     ((128, 32, 4, 256, 4096, 256), (1, 4096, 1)),
     # Rounding point: sm_count=5 -> vsm=10; f32(f32(.8)*10) == 8.0 exactly, so
