@@ -5,8 +5,11 @@
  *   Q       bf16 [batch, num_heads, head_dim], innermost dim contiguous,
  *           rows 16-byte aligned (strides in elements are multiples of 8)
  *   K, V    bf16 [num_pages, 256, num_kv_heads, head_dim], contiguous (NHD pages)
- *   table   int32 [batch, width] block table, row stride table_stride_b;
- *           logical token t of row b lives in page table[b, t / 256], slot t % 256
+ *   table   int32 [batch, width] block table, row stride table_stride_b,
+ *           width = table_width (1 <= width < 2^22); logical token t of row b
+ *           lives in page table[b, t / 256], slot t % 256.  Entries are read
+ *           only inside the row's width: a length beyond width * 256 reads
+ *           page 0 for the missing entries, never memory outside the table.
  *   lengths int32 [batch], 0 <= lengths[b] <= width * 256
  * Element offset of (page, slot, kv_head, d) is ((page*256+slot)*Hkv+kv_head)*D+d,
  * computed in 64-bit.  Query head h reads kv head h / (num_heads / num_kv_heads).
@@ -36,7 +39,7 @@ enum pd_status { PD_OK = 0, PD_EINVAL = 1, PD_ELAUNCH = 2 };
 
 #define PD_PAGE_SIZE 256      /* spec.py:6 */
 #define PD_PARTITION_SIZE 1024 /* spec.py:7 */
-#define PD_ABI_VERSION 1
+#define PD_ABI_VERSION 2
 
 /* Split-KV plan; field meanings follow SplitKVPlan (splitkv_plan.py:15-23). */
 typedef struct pd_plan {
@@ -78,10 +81,12 @@ int pd_validate_metadata(const int32_t* table, int64_t table_stride_b, int32_t w
  * walked in tile_tokens tiles from the last to the first.  Requires
  * head_dim in {64,128,256}, tile_tokens == 16384/head_dim, tokens_per_split a
  * multiple of tile_tokens, num_heads/num_kv_heads <= 16, splits in [1,128].
+ * splits * tokens_per_split < 2^31.
  * scale is applied to the scores (exp2 argument uses f32(scale*log2(e))). */
 int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                  const void* k, const void* v,
-                 const int32_t* table, int64_t table_stride_b, const int32_t* lengths,
+                 const int32_t* table, int64_t table_stride_b, int32_t table_width,
+                 const int32_t* lengths,
                  float* partials, float* lse,
                  int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                  int32_t splits, int32_t tokens_per_split, int32_t tile_tokens,
@@ -106,7 +111,8 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
  * out bf16 [batch, num_heads, head_dim]. */
 int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                       const void* k, const void* v,
-                      const int32_t* table, int64_t table_stride_b, const int32_t* lengths,
+                      const int32_t* table, int64_t table_stride_b, int32_t table_width,
+                      const int32_t* lengths,
                       float* partials, float* lse, int32_t* counters, void* out,
                       int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                       int32_t splits, int32_t tokens_per_split, int32_t tile_tokens,
@@ -118,7 +124,8 @@ int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * Writes out rows [0, batch). */
 int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h,
             const void* k, const void* v,
-            const int32_t* table, int64_t table_stride_b, const int32_t* lengths,
+            const int32_t* table, int64_t table_stride_b, int32_t table_width,
+            const int32_t* lengths,
             void* out, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
             int32_t head_dim, double scale, pd_stream_t stream);
 
@@ -126,10 +133,12 @@ int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * partition_size tokens, m in scaled units.  Replaces _split (kernels.py:44-80)
  * as launched by paged_decode (runtime.py:111-113).  maxima/denoms f32
  * [batch, num_heads, partitions], accums f32 [batch, num_heads, partitions, D];
- * the row stride of all three is `partitions`. */
+ * the row stride of all three is `partitions`; partitions * partition_size
+ * < 2^31. */
 int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                    const void* k, const void* v,
-                   const int32_t* table, int64_t table_stride_b, const int32_t* lengths,
+                   const int32_t* table, int64_t table_stride_b, int32_t table_width,
+                   const int32_t* lengths,
                    float* maxima, float* denoms, float* accums,
                    int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                    int32_t partitions, int32_t partition_size, double scale,

@@ -7,8 +7,8 @@
 //                      softmax over 16384/D-token tiles walked last-to-first,
 //                      PV on v_dot2_f32_bf16 with bf16(p) shared through LDS,
 //                      normalized FP32 partial + LSE out.
-//   lse_merge          one wavefront per (sequence, query head): stable
-//                      log-sum-exp merge of the split partials, bf16 out.
+//   lse_merge          one D-thread workgroup per (sequence, query head):
+//                      stable log-sum-exp merge of the split partials, bf16 out.
 //   online_decode      one 256-thread workgroup per (sequence, query head
 //                      [, fixed partition]): FP32 online softmax with fp32 p,
 //                      either normalized bf16 out (base) or (m, l, acc) state.
@@ -77,35 +77,6 @@ __device__ __forceinline__ u32x4_t load16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
 
-// Coherent (device-scope) float load: bypasses a possibly stale L2 line of
-// another XCD (global_load sc1) without invalidating the whole cache.
-template <bool kCoherent>
-__device__ __forceinline__ float load_f32(const float* p) {
-  if constexpr (kCoherent) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else return *p;
-}
-
-// ------------------------------------------------------ LSE merge arithmetic
-// Shared by the standalone merge kernel and the fused decode so that both give
-// bit-identical outputs.
-//
-// Merge weights of one (b, h) row, computed by one full wavefront: lane owns
-// splits `lane` and `lane + 64` (splits <= 128).  M = max lse (-inf -> 0),
-// S = sum exp(lse - M), L = ln S + M (+inf when S == 0), w_p = exp(lse_p - L)
-// (matched_splitkv.py:107-120; an all-empty row gets w = 0 everywhere).
-template <bool kCoherent>
-__device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lane,
-                                            float& w0, float& w1) {
-  const float v0 = lane < splits ? load_f32<kCoherent>(lrow + lane) : -INFINITY;
-  const float v1 = lane + 64 < splits ? load_f32<kCoherent>(lrow + lane + 64) : -INFINITY;
-  float mx = wave_max(fmaxf(v0, v1));
-  if (mx == -INFINITY) mx = 0.f;
-  const float total = wave_sum(exp_fast(v0 - mx) + exp_fast(v1 - mx));
-  const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
-  w0 = exp_fast(v0 - logsum);
-  w1 = exp_fast(v1 - logsum);
-}
-
 // Buffer resource (V#) over `bytes` bytes at `base`; word 3 is the gfx9-family
 // raw-buffer format.  Loads at or past `bytes` return zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
@@ -142,30 +113,87 @@ __device__ __forceinline__ void buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, int
   }
 }
 
+// ------------------------------------------------------ LSE merge arithmetic
+// Shared by the standalone merge kernel and the fused decode so that both give
+// bit-identical outputs.
+//
+// Merge weights of one (b, h) row, computed by one full wavefront: lane owns
+// splits `lane` and `lane + 64` (splits <= 128).  M = max lse (-inf -> 0),
+// S = sum exp(lse - M), L = ln S + M (+inf when S == 0), w_p = exp(lse_p - L)
+// (matched_splitkv.py:107-120; an all-empty row gets w = 0 everywhere).  The
+// two loads are unconditional buffer loads (zero past the row, replaced by
+// -inf), so they issue without a branch and queue behind earlier loads.
+template <bool kCoherent>
+__device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lane,
+                                            float& w0, float& w1) {
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(lrow, splits * 4);
+  float a[1], c[1];
+  buffer_load_f32<1, kCoherent>(rsrc, lane * 4, a);
+  buffer_load_f32<1, kCoherent>(rsrc, (lane + 64) * 4, c);
+  const float v0 = lane < splits ? a[0] : -INFINITY;
+  const float v1 = lane + 64 < splits ? c[0] : -INFINITY;
+  float mx = wave_max(fmaxf(v0, v1));
+  if (mx == -INFINITY) mx = 0.f;
+  const float total = wave_sum(exp_fast(v0 - mx) + exp_fast(v1 - mx));
+  const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
+  w0 = exp_fast(v0 - logsum);
+  w1 = exp_fast(v1 - logsum);
+}
+
 // acc[e] = fma(w_p, partial_p[e], acc[e]) for p = 0, 1, ..., splits-1 in order
 // (matched_splitkv.py:121-126).  `row` is the (b, h) row of partials
-// [splits][D]; this thread owns elements dd .. dd+E-1.  Splits are processed
-// kBatch at a time as straight-line vector loads followed by the FMA chain, so
-// 36 splits cost two memory round trips.  Past the last split the loads return
-// zero and `weight` must return zero, so the padding steps are fma(0, 0, acc)
-// and leave acc unchanged (a -0 accumulator becomes +0).
-template <int E, bool kCoherent, typename WeightFn>
-__device__ __forceinline__ void weighted_sum(const float* __restrict__ row, int D, int dd,
-                                             int splits, WeightFn weight, float (&acc)[E]) {
-  constexpr int kBatch = 128 / E < 32 ? 128 / E : 32;  // about 128 floats in flight
+// [splits][D]; this thread owns elements dd .. dd+E-1.  Splits are loaded kBatch
+// at a time as straight-line vector loads; the first batch is issued before
+// `prepare()` (which computes the weights), so the partial loads overlap the
+// LSE loads and reductions (a scheduling barrier keeps them issued first).
+// weight(s0, j) returns w_{s0+j}; it must be 0 for splits <= s0+j < 128 and
+// finite for every index.  Past the last split the loads return zero, so the
+// padding steps are fma(w, 0, acc) with w >= 0 finite and leave acc unchanged
+// (acc is never -0: it starts at +0 and a round-to-nearest sum is -0 only if
+// both addends are), so the batch size does not change the result's bits.
+// w_s of a row whose weights lane l holds as w0 = w_l and w1 = w_{l+64}
+// (lse_weights).  For s >= 128 it returns w_{s-64}, a finite value that only
+// multiplies the zero a load past the row returns.
+__device__ __forceinline__ float wave_weight(float w0, float w1, int s) {
+  const float src = s < 64 ? w0 : w1;
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src), s & 63));
+}
+
+template <int E>
+struct MergeBatch {
+  static constexpr int value = E == 1 ? 64 : (E == 2 ? 48 : (E == 4 ? 40 : (E == 8 ? 16 : 8)));
+};
+
+template <int E, bool kCoherent, typename PrepareFn, typename WeightFn>
+__device__ __forceinline__ void merge_splits(const float* __restrict__ row, int D, int dd,
+                                             int splits, PrepareFn prepare, WeightFn weight,
+                                             float (&acc)[E]) {
+  constexpr int kBatch = MergeBatch<E>::value;
+  // `row` must be wavefront-uniform: the resource lives in scalar registers.
   const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(row, splits * D * 4);
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  for (int s0 = 0; s0 < splits; s0 += kBatch) {
-    float x[kBatch][E];
+  float x[kBatch][E];
+  auto load = [&](int s0) {
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) buffer_load_f32<E, kCoherent>(rsrc, ((s0 + j) * D + dd) * 4, x[j]);
+    for (int j = 0; j < kBatch; ++j)
+      buffer_load_f32<E, kCoherent>(rsrc, ((s0 + j) * D + dd) * 4, x[j]);
+  };
+  auto accumulate = [&](int s0) {
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
-      const float wj = weight(s0 + j);
+      const float wj = weight(s0, j);
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[e] = fmaf(wj, x[j][e], acc[e]);
     }
+  };
+  load(0);
+  __builtin_amdgcn_sched_barrier(0);
+  prepare();
+  accumulate(0);
+  for (int s0 = kBatch; s0 < splits; s0 += kBatch) {
+    load(s0);
+    accumulate(s0);
   }
 }
 
@@ -209,6 +237,46 @@ __device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t rsrc, in
   return t;
 }
 
+// Block-table window of one sequence: lane `lane` holds in e[r] the entry of
+// page first + 64 r + lane (r < kRegs), loaded unconditionally through a
+// buffer over the row's `width` entries (zero past the row), so the loads
+// issue at kernel entry in the same round trip as the sequence length.
+// page(t0) of a tile inside the window is a readlane; past the window it is
+// a load of the entry (zero past the row, so a length beyond width * 256 reads
+// page 0 instead of memory outside the table).
+template <int kRegs>
+struct PageWindow {
+  const int32_t* row;
+  int width, first;
+  int32_t e[kRegs];
+
+  __device__ __forceinline__ void load(const int32_t* __restrict__ trow, int width_, int first_,
+                                       int lane) {
+    row = trow;
+    width = width_;
+    first = first_;
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(trow, width_ * 4);
+#pragma unroll
+    for (int r = 0; r < kRegs; ++r)
+      e[r] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, (first_ + 64 * r + lane) * 4, 0, 0);
+  }
+
+  // Page of logical token t0 (t0 >= first * 256, wavefront-uniform).
+  __device__ __forceinline__ int page(int t0) const {
+    const int idx = (t0 >> 8) - first;
+    if (idx < 64 * kRegs) {
+      int pg = __builtin_amdgcn_readlane(e[0], idx & 63);
+#pragma unroll
+      for (int r = 1; r < kRegs; ++r) {
+        const int x = __builtin_amdgcn_readlane(e[r], idx & 63);
+        pg = (idx >> 6) == r ? x : pg;
+      }
+      return pg;
+    }
+    return (t0 >> 8) < width ? row[t0 >> 8] : 0;
+  }
+};
+
 // The K and V rows of one tile as buffers that end after row nvalid - 1, so
 // rows past the sequence end read as zero without being fetched (NaN-poisoned
 // slots and dead pages are never touched) and every load is unconditional.
@@ -218,22 +286,20 @@ struct TileBuffers {
 };
 
 __device__ __forceinline__ TileBuffers tile_buffers(const uint16_t* __restrict__ k,
-                                                    const uint16_t* __restrict__ v,
-                                                    const int32_t* __restrict__ trow, int t0,
-                                                    int end, int64_t RS, int kh, int D) {
-  const int64_t page = trow[t0 >> 8];
-  const int64_t base = (page * 256 + (t0 & 255)) * RS + int64_t(kh) * D;
+                                                    const uint16_t* __restrict__ v, int page,
+                                                    int t0, int end, int64_t RS, int kh, int D) {
+  const int64_t base = (int64_t(page) * 256 + (t0 & 255)) * RS + int64_t(kh) * D;
   const int bytes = (end - t0 < 256 ? end - t0 : 256) * int(RS) * 2;
   return {buffer_rsrc(k + base, bytes), buffer_rsrc(v + base, bytes)};
 }
 
 template <int D, int GP>
 __device__ __forceinline__ void matched_load(TileRegs<D, GP>& R, const uint16_t* __restrict__ k,
-                                             const uint16_t* __restrict__ v,
-                                             const int32_t* __restrict__ trow, int t0, int end,
-                                             int64_t RS, int kh, int lane, int w, int rg, int d0) {
+                                             const uint16_t* __restrict__ v, int page, int t0,
+                                             int end, int64_t RS, int kh, int lane, int w, int rg,
+                                             int d0) {
   using C = Matched<D, GP>;
-  const TileBuffers buf = tile_buffers(k, v, trow, t0, end, RS, kh, D);
+  const TileBuffers buf = tile_buffers(k, v, page, t0, end, RS, kh, D);
   const int qh = lane & 15, qg = lane >> 4;
 #pragma unroll
   for (int g = 0; g < C::kNG; ++g) {
@@ -254,7 +320,6 @@ struct MatchedShared {
   union alignas(16) {
     uint16_t pbuf[GP][Matched<D, GP>::kTile];
     float red[2][GP][D];
-    float wts[GP][128];
   } u;
   float wmax[4][16];
   float lsum[4][16];
@@ -272,7 +337,7 @@ template <int D, int GP, bool kFused>
 __global__ void __launch_bounds__(kThreads, GP >= 16 ? 1 : 2)
 matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
                          const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                         const int32_t* __restrict__ table, int64_t tsb,
+                         const int32_t* __restrict__ table, int64_t tsb, int width,
                          const int32_t* __restrict__ lengths, float* __restrict__ partials,
                          float* __restrict__ lse_out, int* __restrict__ counters,
                          uint16_t* __restrict__ out, int Hq, int Hkv, int G, int splits, int T,
@@ -285,12 +350,15 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int qh = lane & 15, qg = lane >> 4;
   const int rg = tid / C::kLPR, d0 = (tid % C::kLPR) * 8;
-  const int length = lengths[b];
   const int start = p * T;
+  // The partition's table entries do not depend on the length: fetch them
+  // together with it, so the first KV loads wait for one round trip.
+  PageWindow<2> pw;
+  pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
+  const int length = lengths[b];
   const int end = min(start + T, length);
   const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
   const int64_t RS = int64_t(Hkv) * D;
-  const int32_t* trow = table + int64_t(b) * tsb;
 
   // MFMA B operand: the GQA group's query rows.
   bf16x8_t qf[C::kCH];
@@ -403,13 +471,14 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   if constexpr (GP <= 4) {
     if (count > 0) {
       TileRegs<D, GP> R;
-      matched_load<D, GP>(R, k, v, trow, start + (count - 1) * TILE, end, RS, kh, lane, w, rg,
-                          d0);
+      const int tl = start + (count - 1) * TILE;
+      matched_load<D, GP>(R, k, v, pw.page(tl), tl, end, RS, kh, lane, w, rg, d0);
       for (int ti = count - 1; ti >= 0; --ti) {
         TileRegs<D, GP> N;
-        if (ti > 0)
-          matched_load<D, GP>(N, k, v, trow, start + (ti - 1) * TILE, end, RS, kh, lane, w, rg,
-                              d0);
+        if (ti > 0) {
+          const int tn = start + (ti - 1) * TILE;
+          matched_load<D, GP>(N, k, v, pw.page(tn), tn, end, RS, kh, lane, w, rg, d0);
+        }
         process(R, ti);
         R = N;
       }
@@ -417,7 +486,8 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   } else {
     for (int ti = count - 1; ti >= 0; --ti) {
       TileRegs<D, GP> R;
-      matched_load<D, GP>(R, k, v, trow, start + ti * TILE, end, RS, kh, lane, w, rg, d0);
+      const int t0 = start + ti * TILE;
+      matched_load<D, GP>(R, k, v, pw.page(t0), t0, end, RS, kh, lane, w, rg, d0);
       process(R, ti);
     }
   }
@@ -488,47 +558,41 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
                 splits - 1;
     __syncthreads();
     if (!sm.last) return;
+    // Wavefront w merges query heads w, w + 4, ... of the group; lane owns
+    // D/64 consecutive columns, as in lse_merge_kernel's wavefronts.
     const int64_t row0 = int64_t(b) * Hq + kh * G;  // first query head of the group
-    for (int hh = w; hh < G; hh += 4) {
-      float w0, w1;
-      lse_weights<true>(lse_out + (row0 + hh) * splits, splits, lane, w0, w1);
-      sm.u.wts[hh][lane] = w0;        // zero for lanes past the last split
-      sm.u.wts[hh][lane + 64] = w1;
-    }
-    __syncthreads();
-    if (idx0 < C::kOut && h < G) {
-      float acc[C::kE];
-      weighted_sum<C::kE, true>(partials + (row0 + h) * splits * D, D, dd, splits,
-                                [&](int s) { return sm.u.wts[h][s]; }, acc);
-      uint16_t* dst = out + (row0 + h) * D + dd;
+    constexpr int kV = D / 64;
+    for (int hh = __builtin_amdgcn_readfirstlane(w); hh < G; hh += 4) {
+      float w0 = 0.f, w1 = 0.f, acc[kV];
+      merge_splits<kV, true>(
+          partials + (row0 + hh) * splits * D, D, lane * kV, splits,
+          [&] { lse_weights<true>(lse_out + (row0 + hh) * splits, splits, lane, w0, w1); },
+          [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
+      uint16_t* dst = out + (row0 + hh) * D + lane * kV;
 #pragma unroll
-      for (int e = 0; e < C::kE; ++e) dst[e] = uint16_t(bf16_bits(acc[e]));
+      for (int e = 0; e < kV; ++e) dst[e] = uint16_t(bf16_bits(acc[e]));
     }
     if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 // ------------------------------------------------------------- LSE merge
-// One wavefront per (b, h); lane owns VEC = D/64 consecutive columns.
-template <int VEC>
-__global__ void __launch_bounds__(64)
+// One workgroup of D threads per (b, h) row, one output element per thread.
+// Every wavefront computes the row's weights itself (the same arithmetic, so
+// the same bits) and broadcasts them with readlane: no LDS, no barrier.
+template <int D>
+__global__ void __launch_bounds__(D)
 lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ lse,
                  uint16_t* __restrict__ out, int splits) {
-  constexpr int D = VEC * 64;
-  const int row = blockIdx.x;
-  const int lane = threadIdx.x;
-  float w0, w1;
-  lse_weights<false>(lse + int64_t(row) * splits, splits, lane, w0, w1);
-  auto weight = [&](int s) {  // w of lanes past the last split is exp(-inf) = 0
-    const int src = s < 64 ? __builtin_bit_cast(int, w0) : __builtin_bit_cast(int, w1);
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(src, s & 63));
-  };
-  float acc[VEC];
-  weighted_sum<VEC, false>(partials + int64_t(row) * splits * D, D, lane * VEC, splits, weight,
-                           acc);
-  uint16_t* dst = out + int64_t(row) * D + lane * VEC;
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) dst[e] = uint16_t(bf16_bits(acc[e]));
+  const int64_t row = blockIdx.x;
+  const int dd = threadIdx.x;
+  const int lane = dd & 63;
+  float w0 = 0.f, w1 = 0.f, acc[1];
+  merge_splits<1, false>(
+      partials + row * splits * D, D, dd, splits,
+      [&] { lse_weights<false>(lse + row * splits, splits, lane, w0, w1); },
+      [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
+  out[row * D + dd] = uint16_t(bf16_bits(acc[0]));
 }
 
 // ------------------------------------------------- base / fixed-split kernel
@@ -550,7 +614,7 @@ template <int D, bool kSplit>
 __global__ void __launch_bounds__(kThreads)
 online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
                      const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                     const int32_t* __restrict__ table, int64_t tsb,
+                     const int32_t* __restrict__ table, int64_t tsb, int width,
                      const int32_t* __restrict__ lengths, uint16_t* __restrict__ out,
                      float* __restrict__ maxima, float* __restrict__ denoms,
                      float* __restrict__ accums, int Hq, int Hkv, int G, int parts,
@@ -565,11 +629,12 @@ online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int rg = tid / LPR, d0 = (tid % LPR) * 8;
   const int kh = h / G;
-  const int length = lengths[b];
   const int start = kSplit ? part * part_size : 0;
+  PageWindow<1> pw;  // fetched with the length, as in the matched partition
+  pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
+  const int length = lengths[b];
   const int end = kSplit ? min(start + part_size, length) : length;
   const int64_t RS = int64_t(Hkv) * D;
-  const int32_t* trow = table + int64_t(b) * tsb;
 
   const u32x4_t qv = load16(q + int64_t(b) * qsb + int64_t(h) * qsh + d0);
 
@@ -578,7 +643,7 @@ online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 
   for (int t0 = start; t0 < end; t0 += TILE) {
-    const TileBuffers buf = tile_buffers(k, v, trow, t0, end, RS, kh, D);
+    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
     const int nvalid = end - t0;
     u32x4_t kr[8], vr[8];
 #pragma unroll
@@ -587,6 +652,7 @@ online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
       kr[i] = buffer_load16(buf.k, off);
       vr[i] = buffer_load16(buf.v, off);
     }
+    __builtin_amdgcn_sched_barrier(0);  // all 16 loads in flight before the first use
     float s[8];
     float smax = -INFINITY;
 #pragma unroll
@@ -705,8 +771,8 @@ int launch_status(const char* what) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_qkv(const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
-              const int32_t* table, const int32_t* lengths, int32_t batch, int32_t num_heads,
-              int32_t num_kv_heads, int32_t head_dim) {
+              const int32_t* table, int32_t width, const int32_t* lengths, int32_t batch,
+              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0)
     return pd::fail(PD_EINVAL, "batch and head counts must be positive");
   if (!pd::valid_head_dim(head_dim))
@@ -720,6 +786,8 @@ int check_qkv(const void* q, int64_t qsb, int64_t qsh, const void* k, const void
                     "Q/K/V rows must be 16-byte aligned (strides multiples of 8 elements)");
   if (int64_t(num_kv_heads) * head_dim * 512 >= (int64_t(1) << 31))
     return pd::fail(PD_EINVAL, "a 256-slot page of one KV tensor must stay below 2 GiB");
+  if (width < 1 || width >= (1 << 22))
+    return pd::fail(PD_EINVAL, "table width must be in [1, 2^22)");
   return PD_OK;
 }
 
@@ -730,6 +798,7 @@ struct PartitionArgs {
   const uint16_t* v;
   const int32_t* table;
   int64_t tsb;
+  int width;
   const int32_t* lengths;
   float* partials;
   float* lse;
@@ -743,9 +812,9 @@ template <int D, bool kFused>
 void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_GP(GPV)                                                                     \
   hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused>), grid, dim3(kThreads), 0,     \
-                     stream, a.q, a.qsb, a.qsh, a.k, a.v, a.table, a.tsb, a.lengths,          \
-                     a.partials, a.lse, a.counters, a.out, a.Hq, a.Hkv, a.G, a.splits, a.T,   \
-                     a.scale, a.c)
+                     stream, a.q, a.qsb, a.qsh, a.k, a.v, a.table, a.tsb, a.width,          \
+                     a.lengths, a.partials, a.lse, a.counters, a.out, a.Hq, a.Hkv, a.G,       \
+                     a.splits, a.T, a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_GP(1); break;
     case 2: PD_LAUNCH_GP(2); break;
@@ -766,13 +835,14 @@ int padded_group(int g) {
 // pd_matched_decode (fused = true).
 int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, int64_t qsh,
                     const void* k, const void* v, const int32_t* table, int64_t tsb,
-                    const int32_t* lengths, float* partials, float* lse, int32_t* counters,
+                    int32_t width, const int32_t* lengths, float* partials, float* lse,
+                    int32_t* counters,
                     void* out, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t splits, int32_t tokens_per_split,
                     int32_t tile_tokens, double scale, pd_stream_t stream) {
   pd::clear_error();
-  if (int st = check_qkv(q, qsb, qsh, k, v, table, lengths, batch, num_heads, num_kv_heads,
-                         head_dim))
+  if (int st = check_qkv(q, qsb, qsh, k, v, table, width, lengths, batch, num_heads,
+                         num_kv_heads, head_dim))
     return st;
   const int G = num_heads / num_kv_heads;
   if (G > 16)
@@ -783,6 +853,8 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
                     head_dim);
   if (tokens_per_split <= 0 || tokens_per_split % tile_tokens)
     return pd::fail(PD_EINVAL, "tokens_per_split must be a positive multiple of tile_tokens");
+  if (int64_t(splits) * tokens_per_split >= (int64_t(1) << 31))
+    return pd::fail(PD_EINVAL, "splits * tokens_per_split must stay below 2^31");
   if (!partials || !lse || (fused && (!counters || !out)))
     return pd::fail(PD_EINVAL, "invalid matched workspace");
   if (!(scale > 0.0) || !std::isfinite(scale))
@@ -790,7 +862,7 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
   if (batch > 65535 || num_kv_heads > 65535)
     return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
   PartitionArgs a{static_cast<const uint16_t*>(q), qsb, qsh, static_cast<const uint16_t*>(k),
-                  static_cast<const uint16_t*>(v), table, tsb, lengths, partials, lse,
+                  static_cast<const uint16_t*>(v), table, tsb, width, lengths, partials, lse,
                   counters, static_cast<uint16_t*>(out), num_heads, num_kv_heads, G, splits,
                   tokens_per_split, float(scale),
                   float(scale * 1.4426950408889634)};  // SCALE_LOG2 (matched_splitkv.py:363)
@@ -812,25 +884,29 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
 
 extern "C" int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                             const void* k, const void* v, const int32_t* table,
-                            int64_t table_stride_b, const int32_t* lengths, float* partials,
-                            float* lse, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
-                            int32_t head_dim, int32_t splits, int32_t tokens_per_split,
-                            int32_t tile_tokens, double scale, pd_stream_t stream) {
+                            int64_t table_stride_b, int32_t table_width, const int32_t* lengths,
+                            float* partials, float* lse, int32_t batch, int32_t num_heads,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t splits,
+                            int32_t tokens_per_split, int32_t tile_tokens, double scale,
+                            pd_stream_t stream) {
   return partition_entry("pd_partition", false, q, q_stride_b, q_stride_h, k, v, table,
-                         table_stride_b, lengths, partials, lse, nullptr, nullptr, batch,
+                         table_stride_b, table_width, lengths, partials, lse, nullptr, nullptr,
+                         batch,
                          num_heads, num_kv_heads, head_dim, splits, tokens_per_split,
                          tile_tokens, scale, stream);
 }
 
 extern "C" int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                  const void* k, const void* v, const int32_t* table,
-                                 int64_t table_stride_b, const int32_t* lengths,
-                                 float* partials, float* lse, int32_t* counters, void* out,
+                                 int64_t table_stride_b, int32_t table_width,
+                                 const int32_t* lengths, float* partials, float* lse,
+                                 int32_t* counters, void* out,
                                  int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                  int32_t head_dim, int32_t splits, int32_t tokens_per_split,
                                  int32_t tile_tokens, double scale, pd_stream_t stream) {
   return partition_entry("pd_matched_decode", true, q, q_stride_b, q_stride_h, k, v, table,
-                         table_stride_b, lengths, partials, lse, counters, out, batch,
+                         table_stride_b, table_width, lengths, partials, lse, counters, out,
+                         batch,
                          num_heads, num_kv_heads, head_dim, splits, tokens_per_split,
                          tile_tokens, scale, stream);
 }
@@ -853,13 +929,13 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
   auto* o = static_cast<uint16_t*>(out);
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(lse_merge_kernel<1>, dim3(rows), dim3(64), 0, st, partials, lse, o, splits);
+      hipLaunchKernelGGL(lse_merge_kernel<64>, dim3(rows), dim3(64), 0, st, partials, lse, o, splits);
       break;
     case 128:
-      hipLaunchKernelGGL(lse_merge_kernel<2>, dim3(rows), dim3(64), 0, st, partials, lse, o, splits);
+      hipLaunchKernelGGL(lse_merge_kernel<128>, dim3(rows), dim3(128), 0, st, partials, lse, o, splits);
       break;
     default:
-      hipLaunchKernelGGL(lse_merge_kernel<4>, dim3(rows), dim3(64), 0, st, partials, lse, o, splits);
+      hipLaunchKernelGGL(lse_merge_kernel<256>, dim3(rows), dim3(256), 0, st, partials, lse, o, splits);
       break;
   }
   return launch_status("pd_lse_merge");
@@ -869,12 +945,13 @@ namespace {
 
 template <bool kSplit>
 int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
-                  const int32_t* table, int64_t tsb, const int32_t* lengths, void* out,
+                  const int32_t* table, int64_t tsb, int32_t width, const int32_t* lengths,
+                  void* out,
                   float* maxima, float* denoms, float* accums, int32_t batch, int32_t num_heads,
                   int32_t num_kv_heads, int32_t head_dim, int32_t parts, int32_t part_size,
                   double scale, pd_stream_t stream, const char* what) {
-  if (int st = check_qkv(q, qsb, qsh, k, v, table, lengths, batch, num_heads, num_kv_heads,
-                         head_dim))
+  if (int st = check_qkv(q, qsb, qsh, k, v, table, width, lengths, batch, num_heads,
+                         num_kv_heads, head_dim))
     return st;
   if (!std::isfinite(scale)) return pd::fail(PD_EINVAL, "scale must be finite");
   if (batch > 65535 || num_heads > 65535)
@@ -884,6 +961,8 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
     if (part_size <= 0 || part_size % (16384 / head_dim))
       return pd::fail(PD_EINVAL, "partition_size must be a positive multiple of %d",
                       16384 / head_dim);
+    if (int64_t(parts) * part_size >= (int64_t(1) << 31))
+      return pd::fail(PD_EINVAL, "partitions * partition_size must stay below 2^31");
     if (!maxima || !denoms || !accums)
       return pd::fail(PD_EINVAL, "invalid or missing preallocated split-K workspace");
   } else if (!out) {
@@ -899,8 +978,8 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   const float s32 = float(scale);
 #define PD_LAUNCH_ONLINE(DV)                                                                  \
   hipLaunchKernelGGL((online_decode_kernel<DV, kSplit>), grid, dim3(kThreads), 0, st, qq, qsb, \
-                     qsh, kk, vv, table, tsb, lengths, o, maxima, denoms, accums, num_heads,  \
-                     num_kv_heads, G, parts, part_size, s32)
+                     qsh, kk, vv, table, tsb, width, lengths, o, maxima, denoms, accums,      \
+                     num_heads, num_kv_heads, G, parts, part_size, s32)
   switch (head_dim) {
     case 64: PD_LAUNCH_ONLINE(64); break;
     case 128: PD_LAUNCH_ONLINE(128); break;
@@ -914,22 +993,26 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
 
 extern "C" int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
                        const void* v, const int32_t* table, int64_t table_stride_b,
-                       const int32_t* lengths, void* out, int32_t batch, int32_t num_heads,
-                       int32_t num_kv_heads, int32_t head_dim, double scale, pd_stream_t stream) {
+                       int32_t table_width, const int32_t* lengths, void* out, int32_t batch,
+                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, double scale,
+                       pd_stream_t stream) {
   pd::clear_error();
-  return launch_online<false>(q, q_stride_b, q_stride_h, k, v, table, table_stride_b, lengths,
+  return launch_online<false>(q, q_stride_b, q_stride_h, k, v, table, table_stride_b,
+                              table_width, lengths,
                               out, nullptr, nullptr, nullptr, batch, num_heads, num_kv_heads,
                               head_dim, 1, 0, scale, stream, "pd_base");
 }
 
 extern "C" int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                               const void* k, const void* v, const int32_t* table,
-                              int64_t table_stride_b, const int32_t* lengths, float* maxima,
+                              int64_t table_stride_b, int32_t table_width,
+                              const int32_t* lengths, float* maxima,
                               float* denoms, float* accums, int32_t batch, int32_t num_heads,
                               int32_t num_kv_heads, int32_t head_dim, int32_t partitions,
                               int32_t partition_size, double scale, pd_stream_t stream) {
   pd::clear_error();
-  return launch_online<true>(q, q_stride_b, q_stride_h, k, v, table, table_stride_b, lengths,
+  return launch_online<true>(q, q_stride_b, q_stride_h, k, v, table, table_stride_b,
+                             table_width, lengths,
                              nullptr, maxima, denoms, accums, batch, num_heads, num_kv_heads,
                              head_dim, partitions, partition_size, scale, stream,
                              "pd_split_fixed");

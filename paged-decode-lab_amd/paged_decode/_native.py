@@ -30,13 +30,14 @@ SIGNATURES = {
     "pd_abi_version": [],
     "pd_make_plan": [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(Plan)],
     "pd_validate_metadata": [_vp, _i64, _i32, _vp, _i32, _i64, _i32],
-    "pd_partition": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+    "pd_partition": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
                      _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_lse_merge": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
-    "pd_matched_decode": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+    "pd_matched_decode": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                           _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
-    "pd_base": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _dbl, _vp],
-    "pd_split_fixed": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+    "pd_base": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i32,
+                _dbl, _vp],
+    "pd_split_fixed": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp,
                        _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_ml_merge": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
 }
@@ -93,8 +94,9 @@ def partition(q, k, v, tables, lengths, partials, lse, num_kv_heads, splits, tok
               tile_tokens, scale):
     b, h, d = q.shape
     check(lib().pd_partition(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
-                             tables.data_ptr(), tables.stride(0), lengths.data_ptr(),
-                             partials.data_ptr(), lse.data_ptr(), b, h, num_kv_heads, d, splits,
+                             tables.data_ptr(), tables.stride(0), tables.shape[1],
+                             lengths.data_ptr(), partials.data_ptr(), lse.data_ptr(), b, h,
+                             num_kv_heads, d, splits,
                              tokens_per_split, tile_tokens, scale, stream_handle(q.device)))
 
 
@@ -103,7 +105,8 @@ def matched_decode(q, k, v, tables, lengths, partials, lse, counters, out, num_k
     b, h, d = q.shape
     check(lib().pd_matched_decode(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
                                   v.data_ptr(), tables.data_ptr(), tables.stride(0),
-                                  lengths.data_ptr(), partials.data_ptr(), lse.data_ptr(),
+                                  tables.shape[1], lengths.data_ptr(), partials.data_ptr(),
+                                  lse.data_ptr(),
                                   counters.data_ptr(), out.data_ptr(), b, h, num_kv_heads, d,
                                   splits, tokens_per_split, tile_tokens, scale,
                                   stream_handle(q.device)))
@@ -118,7 +121,8 @@ def lse_merge(partials, lse, out, lse_lanes):
 def base(q, k, v, tables, lengths, out, num_kv_heads, scale):
     b, h, d = q.shape
     check(lib().pd_base(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
-                        tables.data_ptr(), tables.stride(0), lengths.data_ptr(), out.data_ptr(),
+                        tables.data_ptr(), tables.stride(0), tables.shape[1], lengths.data_ptr(),
+                        out.data_ptr(),
                         b, h, num_kv_heads, d, scale, stream_handle(q.device)))
 
 
@@ -126,8 +130,8 @@ def split_fixed(q, k, v, tables, lengths, maxima, denoms, accums, num_kv_heads, 
                 partition_size, scale):
     b, h, d = q.shape
     check(lib().pd_split_fixed(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
-                               tables.data_ptr(), tables.stride(0), lengths.data_ptr(),
-                               maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(), b, h,
+                               tables.data_ptr(), tables.stride(0), tables.shape[1],
+                               lengths.data_ptr(), maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(), b, h,
                                num_kv_heads, d, partitions, partition_size, scale,
                                stream_handle(q.device)))
 

@@ -28,26 +28,26 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert names == sorted(_native.SIGNATURES), names
     for name in names:
         assert getattr(lib, name) is not None
-    assert lib.pd_abi_version() == 1
+    assert lib.pd_abi_version() == 2
 
 
 def test_error_reporting_and_validation_without_launching():
     lib = _native.lib()
     null = ctypes.c_void_p(0)
     # head_dim 80 is rejected before any device call.
-    status = lib.pd_partition(null, 0, 0, null, null, null, 0, null, null, null,
+    status = lib.pd_partition(null, 0, 0, null, null, null, 0, 1, null, null, null,
                               1, 4, 1, 80, 1, 64, 64, 0.1, null)
     assert status == _native.PD_EINVAL
     assert b"head_dim" in lib.pd_last_error()
     status = lib.pd_lse_merge(null, null, null, 1, 4, 256, 0, 1, null)
     assert status == _native.PD_EINVAL and b"splits" in lib.pd_last_error()
-    status = lib.pd_base(null, 0, 0, null, null, null, 0, null, null, 1, 4, 3, 64, 0.1, null)
+    status = lib.pd_base(null, 0, 0, null, null, null, 0, 1, null, null, 1, 4, 3, 64, 0.1, null)
     assert status == _native.PD_EINVAL and b"divisible" in lib.pd_last_error()
     status = lib.pd_ml_merge(null, null, null, null, 1, 4, 64, 0, null)
     assert status == _native.PD_EINVAL and b"partitions" in lib.pd_last_error()
     with pytest.raises(ValueError, match="head_dim"):
-        _native.check(lib.pd_split_fixed(null, 0, 0, null, null, null, 0, null, null, null, null,
-                                         1, 4, 1, 96, 1, 1024, 0.1, null))
+        _native.check(lib.pd_split_fixed(null, 0, 0, null, null, null, 0, 1, null, null, null,
+                                         null, 1, 4, 1, 96, 1, 1024, 0.1, null))
 
 
 def test_metadata_validation_on_host_copies():

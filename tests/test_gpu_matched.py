@@ -251,3 +251,13 @@ def test_long_single_split_reverse_walk():
     case = make_case([32768, 20000], 32, 8, 128, seed=3, capacity=32768)
     g, res, out = run(case, DecodeSpec(2, 32, 8, 128, 32768), num_splits=1)
     check_all(case, g, res, out)
+
+
+def test_single_split_beyond_the_prefetched_table_window():
+    # 160 pages in one partition: the first 128 table entries are fetched at
+    # kernel entry, the rest are read as the reverse walk reaches them.
+    case = make_case([40000, 33000, 256], 4, 1, 64, seed=8, capacity=40960)
+    g, res, out = run(case, DecodeSpec(3, 4, 1, 64, 40960), num_splits=1)
+    assert res.plan.tokens_per_split == 40960
+    check_all(case, g, res, out)
+

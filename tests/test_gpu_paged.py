@@ -136,3 +136,17 @@ def test_edge_coverage_config_c4(backend, dim, hq, hkv):
     assert_close_dense(actual, torch_dense(*g))
     assert_within_one_ulp(actual, oracle_for(case, backend, spec))
     assert torch.count_nonzero(actual[:8]) == 0
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+def test_context_beyond_the_prefetched_table_window(backend):
+    # hip_base walks 80 pages in one workgroup, past its 64-entry table window.
+    case = make_case([20480, 17000, 3], 4, 1, 128, seed=9, capacity=20480)
+    g = to_gpu(case)
+    spec = DecodeSpec(3, 4, 1, 128, 20480)
+    res = allocate_resources(spec, "cuda", backend)
+    actual = paged_decode(*g, resources=res, backend=backend)
+    torch.cuda.synchronize()
+    assert_close_dense(actual, torch_dense(*g))
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec))
+
