@@ -201,40 +201,97 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
 //
 // Tile geometry: TILE = 16384 / D tokens (64/128/256 for D = 256/128/64), the
 // reference's tile_tokens (splitkv_plan.py:33), so a tile is always 32 KiB of K
-// and 32 KiB of V and never crosses a 256-token page.
+// and 32 KiB of V and never crosses a 256-token page.  Wavefront w owns tokens
+// [w*TILE/4, (w+1)*TILE/4) of every tile, in groups of 16, for both products.
 //
-// QK^T: wave w owns tokens [w*TILE/4, (w+1)*TILE/4) in groups of 16.  For the
-// MFMA, A = K rows (lane -> token lane%16, d = 32c + 8*(lane/16) .. +8) and
-// B = Q of the GQA group (lane -> head lane%16, same d), so the result lane
-// holds S[token 4*(lane/16)+r][head lane%16], r = 0..3.  Padded heads
-// (>= G) have zero Q and are never stored.
+// QK^T on v_mfma_f32_16x16x32_bf16: A = K rows (lane L -> token L%16, d = 32c +
+// 8*(L/16) .. +8, loaded straight into registers), B = Q of the GQA group
+// (lane -> head L%16), so lane L holds S[token 4*(L/16)+r][head L%16],
+// r = 0..3.  Padded heads (>= G) have zero Q and zero probabilities.
 //
-// PV: thread tid owns the 8-column slice d0 = 8*(tid % (D/8)) of row pairs
-// (j*TILE/4 + 2*rg, +1), rg = tid / (D/8), j = 0..3, so every V load is a
-// 16-byte piece of a row and a pair of rows packs into bf16x2 operands for
-// v_dot2_f32_bf16 together with the pair's bf16 probabilities from LDS.
+// PV on MFMA, with the bf16 probabilities as the A operand taken directly from
+// the QK result registers: lane L holds P[head L%16][tokens 4*(L/16) + r] of
+// each 16-token group, the A layout of v_mfma_f32_16x16x16_bf16 for one group
+// and, for two groups g, g+1 side by side, of v_mfma_f32_16x16x32_bf16
+// (k = 8*(L/16) + e <-> token 16g + 4*(L/16) + e for e < 4, 16(g+1) +
+// 4*(L/16) + e-4 above).  The B operand needs V columns (4 consecutive tokens
+// of one d per lane).  V rows therefore go to LDS by buffer_load ... lds (no
+// registers; lane l of a copy fills bytes 16l .. 16l+15 of its 1 KiB, and
+// reads past the buffer write zeros), each row padded by 16 bytes so that
+// the transposed reads hit distinct banks, and are read with
+// ds_read_b64_tr_b16: in each 16-lane group, when source lane 4c + b
+// addresses row c, columns 4b .. 4b+3 of a 4 x 16 block, lane n receives
+// column n of the block (rows 0..3).  Output lane L holds O[head 4*(L/16) + r]
+// [d = 16j + L%16] of column block j.
 template <int D, int GP>
 struct Matched {
   static constexpr int kTile = 16384 / D;
-  static constexpr int kTW = kTile / 4;   // tokens per wave in QK
-  static constexpr int kNG = kTW / 16;    // 16-token MFMA groups per wave
-  static constexpr int kCH = D / 32;      // MFMA k-chunks of 32 d
-  static constexpr int kLPR = D / 8;      // lanes per V row
-  static constexpr int kOut = GP * D;            // outputs of one GQA group
+  static constexpr int kTW = kTile / 4;                      // tokens per wavefront
+  static constexpr int kNG = kTW / 16;                       // 16-token groups per wavefront
+  static constexpr int kCH = D / 32;                         // 32-wide k-chunks of QK
+  static constexpr int kNB = D / 16;                         // 16-column blocks of PV
+  static constexpr int kPieces = D / 8 + 1;                  // 16-byte pieces per LDS row
+  static constexpr int kPitch = 16 * kPieces;                // bytes per V row in LDS
+  static constexpr int kDma = (kTW * kPitch + 1023) / 1024;  // 1 KiB copies per wavefront
+  static constexpr int kSlot = 1024 * kDma;                  // LDS bytes of a wavefront's rows
+  static constexpr int kOut = GP * D;                        // outputs of one GQA group
   static constexpr int kE = kOut >= kThreads ? kOut / kThreads : 1;  // per thread
-  static_assert(kNG >= 1 && kCH >= 1, "geometry");
+  static_assert(kNG >= 1 && kCH >= 1 && 2 * kOut * 4 <= 4 * kSlot, "geometry");
 };
 
 template <int D, int GP>
-struct TileRegs {
+struct KTile {
   u32x4_t k[Matched<D, GP>::kNG][Matched<D, GP>::kCH];
-  u32x4_t v[4][2];
 };
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // 16 bytes at byte offset `off` of a buffer (zero past its end).
 __device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int off) {
   const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
   return t;
+}
+
+// Four bf16 of one column, transposed out of LDS (see above).  `p` points
+// into a __shared__ array; the LDS address-space casts live in these helpers
+// so that kernel bodies only handle ordinary pointers.
+__device__ __forceinline__ short4_t lds_read_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(const_cast<char*>(p)));
+}
+
+// Copies 16 bytes at byte offset `off` of a buffer into LDS: lane l of the
+// wavefront writes bytes [dst + 16l, dst + 16l + 16); `dst` is wavefront-uniform.
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t rsrc, char* dst, int off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16,
+                                           off, 0, 0, 0);
+}
+
+// Workgroup barrier for LDS data written with ds_write only.  __syncthreads()
+// also waits for every outstanding vector-memory operation, including the
+// LDS copies of the next tile that are meant to stay in flight; this waits
+// for the LDS instructions only.  The memory clobber keeps the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Wait states between the last MFMA writing `x` and the first vector-ALU read
+// of it.  The hardware does not interlock this dependency, and this compiler
+// emitted none when a branch separated the MFMA from the read: rows 8-15 of
+// the 16x16 result were then read before the MFMA had written them.  24 wait
+// states cover the 8-pass MFMAs used here; the empty statements keep every
+// element's reads after them.
+template <int N>
+__device__ __forceinline__ void mfma_result_barrier(floatx4_t (&x)[N]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(x[N - 1]));
+#pragma unroll
+  for (int i = 0; i < N - 1; ++i) asm volatile("" : "+v"(x[i]));
+}
+
+// bf16 bits of (a, b), round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2_t{a, b}, bf16x2_t));
 }
 
 // Block-table window of one sequence: lane `lane` holds in e[r] the entry of
@@ -259,6 +316,13 @@ struct PageWindow {
 #pragma unroll
     for (int r = 0; r < kRegs; ++r)
       e[r] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, (first_ + 64 * r + lane) * 4, 0, 0);
+  }
+
+  // Waits for the window loads once, here, so that no later wait counts them
+  // (the compiler cannot tell on every path that they have completed).
+  __device__ __forceinline__ void settle() {
+#pragma unroll
+    for (int r = 0; r < kRegs; ++r) asm volatile("" : "+v"(e[r]));
   }
 
   // Page of logical token t0 (t0 >= first * 256, wavefront-uniform).
@@ -294,34 +358,8 @@ __device__ __forceinline__ TileBuffers tile_buffers(const uint16_t* __restrict__
 }
 
 template <int D, int GP>
-__device__ __forceinline__ void matched_load(TileRegs<D, GP>& R, const uint16_t* __restrict__ k,
-                                             const uint16_t* __restrict__ v, int page, int t0,
-                                             int end, int64_t RS, int kh, int lane, int w, int rg,
-                                             int d0) {
-  using C = Matched<D, GP>;
-  const TileBuffers buf = tile_buffers(k, v, page, t0, end, RS, kh, D);
-  const int qh = lane & 15, qg = lane >> 4;
-#pragma unroll
-  for (int g = 0; g < C::kNG; ++g) {
-    const int off = ((w * C::kTW + 16 * g + qh) * int(RS) + 8 * qg) * 2;
-#pragma unroll
-    for (int c = 0; c < C::kCH; ++c) R.k[g][c] = buffer_load16(buf.k, off + 64 * c);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int par = 0; par < 2; ++par)
-      R.v[j][par] =
-          buffer_load16(buf.v, ((j * (C::kTile / 4) + 2 * rg + par) * int(RS) + d0) * 2);
-}
-
-template <int D, int GP>
 struct MatchedShared {
-  union alignas(16) {
-    uint16_t pbuf[GP][Matched<D, GP>::kTile];
-    float red[2][GP][D];
-  } u;
-  float wmax[4][16];
+  float wmax[2][4][16];  // per-tile maxima, double-buffered by tile parity
   float lsum[4][16];
   float mfin[16];
   int last;
@@ -334,7 +372,7 @@ struct MatchedShared {
 // same arithmetic as lse_merge_kernel, and resets the counter to 0, so the
 // counters are zero again when the kernel ends (graph replays need no reset).
 template <int D, int GP, bool kFused>
-__global__ void __launch_bounds__(kThreads, GP >= 16 ? 1 : 2)
+__global__ void __launch_bounds__(kThreads, 2)
 matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
                          const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                          const int32_t* __restrict__ table, int64_t tsb, int width,
@@ -345,11 +383,16 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   using C = Matched<D, GP>;
   constexpr int TILE = C::kTile;
   __shared__ MatchedShared<D, GP> sm;
+  // V rows of the tile being computed and of the one being loaded; two arrays
+  // (not one) so that the compiler's wait before reading one slot does not
+  // count the copies still in flight into the other.
+  __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
+  __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
 
   const int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = lane & 15, qg = lane >> 4;
-  const int rg = tid / C::kLPR, d0 = (tid % C::kLPR) * 8;
   const int start = p * T;
   // The partition's table entries do not depend on the length: fetch them
   // together with it, so the first KV loads wait for one round trip.
@@ -360,7 +403,7 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
   const int64_t RS = int64_t(Hkv) * D;
 
-  // MFMA B operand: the GQA group's query rows.
+  // MFMA B operand of QK: the GQA group's query rows.
   bf16x8_t qf[C::kCH];
   {
     const bool live = qh < G;
@@ -371,20 +414,48 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
       qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
   }
 
-  float M[GP];             // running max of raw scores, per head (uniform)
-  float acc[GP][8];        // PV accumulator for (head, d0 + e)
+  // Tile-relative byte offsets: K pieces of this lane, and the source of
+  // each 16-byte LDS piece this lane fills (row, piece) = (slot / kPieces,
+  // slot % kPieces); the padding piece and rows past the wavefront's share
+  // read past the buffer, i.e. zeros.
+  const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
+  int voff[C::kDma];
 #pragma unroll
-  for (int h = 0; h < GP; ++h) {
-    M[h] = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  for (int i = 0; i < C::kDma; ++i) {
+    const int slot = 64 * i + lane;
+    const int row = slot / C::kPieces, piece = slot % C::kPieces;
+    voff[i] = row < C::kTW && piece < D / 8 ? ((w * C::kTW + row) * int(RS) + 8 * piece) * 2
+                                            : 0x7ffffff0;
   }
-  float m_own = -INFINITY;  // running max of head qh (same value as M[qh])
+  // This lane's transposed-read address within its wavefront's LDS rows.
+  const int trb = w * C::kSlot + (4 * qg + ((lane & 15) >> 2)) * C::kPitch + 8 * (lane & 3);
+
+  floatx4_t acc[C::kNB];   // O[head 4*qg + r][16j + qh]
+#pragma unroll
+  for (int j = 0; j < C::kNB; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  float m4[4];             // running max of heads 4*qg + r
+#pragma unroll
+  for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
+  float m_own = -INFINITY;  // running max of head qh
   float l_own = 0.f;        // this lane's share of head qh's denominator
 
-  auto process = [&](const TileRegs<D, GP>& R, int ti) __attribute__((always_inline)) {
-    const int t0 = start + ti * TILE;
-    const int nvalid = end - t0;
+  // Issues the loads of tile ti (ti < 0: an empty load, nothing fetched).
+  auto issue = [&](KTile<D, GP>& R, char* slot, int ti) __attribute__((always_inline)) {
+    const int t0 = start + (ti > 0 ? ti : 0) * TILE;
+    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, ti >= 0 ? end : t0, RS, kh, D);
+#pragma unroll
+    for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+      for (int ch = 0; ch < C::kCH; ++ch)
+        R.k[g][ch] = buffer_load16(buf.k, koff + g * 16 * int(RS) * 2 + 64 * ch);
+#pragma unroll
+    for (int i = 0; i < C::kDma; ++i)
+      lds_copy16(buf.v, slot + w * C::kSlot + 1024 * i, voff[i]);
+  };
+
+  auto process = [&](const KTile<D, GP>& R, const char* slot, int ti)
+                     __attribute__((always_inline)) {
+    const int nvalid = end - (start + ti * TILE);
     // ---- scores
     floatx4_t s[C::kNG];
 #pragma unroll
@@ -395,100 +466,103 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
         s[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, R.k[g][ch]),
                                                         qf[ch], s[g], 0, 0, 0);
     }
+    mfma_result_barrier(s);
+    if (nvalid < TILE) {
+#pragma unroll
+      for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (w * C::kTW + 16 * g + 4 * qg + r >= nvalid) s[g][r] = -INFINITY;
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int g = 0; g < C::kNG; ++g)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = w * C::kTW + 16 * g + 4 * qg + r;
-        if (tok >= nvalid) s[g][r] = -INFINITY;
-        mx = fmaxf(mx, s[g][r]);
-      }
+      mx = fmaxf(fmaxf(mx, fmaxf(s[g][0], s[g][1])), fmaxf(s[g][2], s[g][3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    if (lane < 16) sm.wmax[w][lane] = mx;
-    __syncthreads();
-    // ---- running max update (reference order: m' = max(m, rowmax s))
-    float alpha[GP];
+    float (*wm)[16] = sm.wmax[ti & 1];
+    if (lane < 16) wm[w][lane] = mx;
+    lds_barrier();
+    // ---- running maxima (reference order: m' = max(m, rowmax s))
+    float alpha[4];
+    bool moved = false;
 #pragma unroll
-    for (int h = 0; h < GP; ++h) {
-      const float tm = fmaxf(fmaxf(sm.wmax[0][h], sm.wmax[1][h]), fmaxf(sm.wmax[2][h], sm.wmax[3][h]));
-      const float mn = fmaxf(M[h], tm);
-      alpha[h] = exp2_fast((M[h] - mn) * c);
-      M[h] = mn;
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * qg + r;
+      const float tm = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+      const float mn = fmaxf(m4[r], tm);
+      moved |= mn != m4[r];
+      alpha[r] = exp2_fast((m4[r] - mn) * c);
+      m4[r] = mn;
     }
-    {
-      const float tm = fmaxf(fmaxf(sm.wmax[0][qh], sm.wmax[1][qh]), fmaxf(sm.wmax[2][qh], sm.wmax[3][qh]));
-      const float mn = fmaxf(m_own, tm);
-      const float a_own = exp2_fast((m_own - mn) * c);
-      m_own = mn;
-      const float neg_mc = -(mn * c);
-      float psum = 0.f;
+    const float tm = fmaxf(fmaxf(wm[0][qh], wm[1][qh]), fmaxf(wm[2][qh], wm[3][qh]));
+    const float mn = fmaxf(m_own, tm);
+    const float a_own = exp2_fast((m_own - mn) * c);
+    m_own = mn;
+    const float neg_mc = -(mn * c);
+    float psum = 0.f;
+    uint32_t pb[C::kNG][2];  // bf16 probabilities, the PV A operand
 #pragma unroll
-      for (int g = 0; g < C::kNG; ++g) {
-        uint32_t bits[4];
+    for (int g = 0; g < C::kNG; ++g) {
+      float pr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pr = exp2_fast(fmaf(s[g][r], c, neg_mc));
-          psum += pr;
-          bits[r] = bf16_bits(pr);
-        }
-        if (qh < GP)
-          *reinterpret_cast<u32x2_t*>(&sm.u.pbuf[qh][w * C::kTW + 16 * g + 4 * qg]) =
-              u32x2_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+      for (int r = 0; r < 4; ++r) {
+        pr[r] = exp2_fast(fmaf(s[g][r], c, neg_mc));
+        psum += pr[r];
       }
-      l_own = l_own * a_own + psum;
+      pb[g][0] = qh < G ? pack_bf16(pr[0], pr[1]) : 0u;
+      pb[g][1] = qh < G ? pack_bf16(pr[2], pr[3]) : 0u;
     }
-    __syncthreads();
-    // ---- PV
+    l_own = l_own * a_own + psum;
+    // ---- PV (rescale only when a running maximum moved; alpha = 1 otherwise)
+    if (__builtin_amdgcn_ballot_w64(moved)) {
 #pragma unroll
-    for (int h = 0; h < GP; ++h)
+      for (int j = 0; j < C::kNB; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
+        for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
+    }
+    const char* base = slot + trb;
+    if constexpr (C::kNG == 1) {
+      const short4_t a = __builtin_bit_cast(short4_t, u32x2_t{pb[0][0], pb[0][1]});
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row0 = j * (TILE / 4) + 2 * rg;
-      uint32_t pp[GP];
+      for (int j = 0; j < C::kNB; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, lds_read_tr(base + 32 * j), acc[j],
+                                                           0, 0, 0);
+    } else {
 #pragma unroll
-      for (int h = 0; h < GP; ++h) pp[h] = *reinterpret_cast<const uint32_t*>(&sm.u.pbuf[h][row0]);
+      for (int g = 0; g < C::kNG; g += 2) {
+        const bf16x8_t a =
+            __builtin_bit_cast(bf16x8_t, u32x4_t{pb[g][0], pb[g][1], pb[g + 1][0], pb[g + 1][1]});
 #pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const uint32_t a = R.v[j][0][e4], bw = R.v[j][1][e4];
-        const uint32_t lo = (a & 0xffffu) | (bw << 16);
-        const uint32_t hi = (a >> 16) | (bw & 0xffff0000u);
-#pragma unroll
-        for (int h = 0; h < GP; ++h) {
-          acc[h][2 * e4] = dot2(lo, pp[h], acc[h][2 * e4]);
-          acc[h][2 * e4 + 1] = dot2(hi, pp[h], acc[h][2 * e4 + 1]);
+        for (int j = 0; j < C::kNB; ++j) {
+          const short4_t lo = lds_read_tr(base + 16 * g * C::kPitch + 32 * j);
+          const short4_t hi = lds_read_tr(base + 16 * (g + 1) * C::kPitch + 32 * j);
+          const bf16x8_t bv = __builtin_bit_cast(
+              bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo)[0], __builtin_bit_cast(u32x2_t, lo)[1],
+                                __builtin_bit_cast(u32x2_t, hi)[0], __builtin_bit_cast(u32x2_t, hi)[1]});
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
         }
       }
     }
   };
 
-  // Reverse tile walk (matched_splitkv.py:71): last tile first.  Up to GQA
-  // groups of 4 the registers hold a second tile, so the loads of the next tile
-  // are in flight while the current one is computed.
-  if constexpr (GP <= 4) {
-    if (count > 0) {
-      TileRegs<D, GP> R;
-      const int tl = start + (count - 1) * TILE;
-      matched_load<D, GP>(R, k, v, pw.page(tl), tl, end, RS, kh, lane, w, rg, d0);
-      for (int ti = count - 1; ti >= 0; --ti) {
-        TileRegs<D, GP> N;
-        if (ti > 0) {
-          const int tn = start + (ti - 1) * TILE;
-          matched_load<D, GP>(N, k, v, pw.page(tn), tn, end, RS, kh, lane, w, rg, d0);
-        }
-        process(R, ti);
-        R = N;
-      }
-    }
-  } else {
-    for (int ti = count - 1; ti >= 0; --ti) {
-      TileRegs<D, GP> R;
-      const int t0 = start + ti * TILE;
-      matched_load<D, GP>(R, k, v, pw.page(t0), t0, end, RS, kh, lane, w, rg, d0);
-      process(R, ti);
+  // Reverse tile walk (matched_splitkv.py:71): last tile first.  Two register
+  // sets and two LDS slots alternate: the loads of the next tile are issued
+  // before the current one is computed.  The load after the last tile is an
+  // empty one (a buffer of 0 bytes, nothing fetched), so every iteration
+  // issues the same loads.
+  pw.settle();
+  if (count > 0) {
+    KTile<D, GP> A, B;
+    int ti = count - 1;
+    issue(A, vs0, ti);
+    while (true) {
+      issue(B, vs1, ti - 1);
+      process(A, vs0, ti);
+      if (--ti < 0) break;
+      issue(A, vs0, ti - 1);
+      process(B, vs1, ti);
+      if (--ti < 0) break;
     }
   }
 
@@ -498,24 +572,21 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   l += __shfl_xor(l, 32);
   if (lane < 16) sm.lsum[w][lane] = l;
   if (tid < 16) sm.mfin[tid] = m_own;
+  __syncthreads();  // every wavefront is done with its V rows (aliased by red)
+  // O of wavefront w for the group's heads: waves 0, 1 in vs0, waves 2, 3 in vs1.
+  auto red = [&](int wave) __attribute__((always_inline)) {
+    return reinterpret_cast<float*>(wave < 2 ? vs0 : vs1) + (wave & 1) * C::kOut;
+  };
+  {
+    float* mine = red(w);
 #pragma unroll
-  for (int msk = C::kLPR; msk < 64; msk <<= 1)
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * qg + r;
+      if (h < GP)
 #pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], msk);
-  __syncthreads();  // pbuf (aliased by red) no longer read
-  if (lane < C::kLPR && w < 2)
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.u.red[w][h][d0 + e] = acc[h][e];
-  __syncthreads();
-  if (lane < C::kLPR && w >= 2)
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.u.red[w - 2][h][d0 + e] += acc[h][e];
+        for (int j = 0; j < C::kNB; ++j) mine[h * D + 16 * j + qh] = acc[j][r];
+    }
+  }
   __syncthreads();
 
   const int idx0 = tid * C::kE;
@@ -527,17 +598,22 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
     const int64_t orow = (int64_t(b) * Hq + kh * G + h) * splits + p;
     float* dst = partials + orow * D + dd;
     const float lv = den > 0.f ? fmaf(sm.mfin[h], scale, ln_fast(safe)) : -INFINITY;
+    float val[C::kE];
+#pragma unroll
+    for (int e = 0; e < C::kE; ++e) {
+      const int i = idx0 + e;
+      val[e] = ((red(0)[i] + red(1)[i]) + (red(2)[i] + red(3)[i])) * inv;
+    }
     if constexpr (kFused) {
       // Device-scope stores (global_store sc1): written through to the
       // coherence point, so another XCD can read them without any L2 flush.
 #pragma unroll
       for (int e = 0; e < C::kE; ++e)
-        __hip_atomic_store(dst + e, (sm.u.red[0][h][dd + e] + sm.u.red[1][h][dd + e]) * inv,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(dst + e, val[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (dd == 0) __hip_atomic_store(lse_out + orow, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
 #pragma unroll
-      for (int e = 0; e < C::kE; ++e) dst[e] = (sm.u.red[0][h][dd + e] + sm.u.red[1][h][dd + e]) * inv;
+      for (int e = 0; e < C::kE; ++e) dst[e] = val[e];
       if (dd == 0) lse_out[orow] = lv;
     }
   }
@@ -642,6 +718,7 @@ online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 
+  pw.settle();
   for (int t0 = start; t0 < end; t0 += TILE) {
     const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
     const int nvalid = end - t0;
