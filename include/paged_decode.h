@@ -150,6 +150,32 @@ int pd_ml_merge(const float* maxima, const float* denoms, const float* accums, v
                 int32_t batch, int32_t num_heads, int32_t head_dim, int32_t partitions,
                 pd_stream_t stream);
 
+/* KV-cache write of token rows through a flat slot mapping; replaces the
+ * store_kvcache Triton kernel of the nano-vLLM overlay
+ * (overlays/nano-vllm/nanovllm/layers/attention.py:10-38).  For token i with
+ * slot = slot_mapping[i] >= 0, copies row_elems (= num_kv_heads * head_dim)
+ * bf16 of key + i*key_stride to k_cache + slot*row_elems, and the same for
+ * value/v_cache; slot -1 (a padded graph entry) is skipped.  Rows, caches and
+ * strides must be 16-byte aligned (strides multiples of 8 elements, at least
+ * row_elems).  Contents are trusted: slots must lie inside the caches. */
+int pd_store_kv(const void* key, int64_t key_stride, const void* value, int64_t value_stride,
+                void* k_cache, void* v_cache, const int32_t* slot_mapping, int64_t num_tokens,
+                int32_t row_elems, pd_stream_t stream);
+
+/* KV-cache write of a [batch, num_kv_heads, steps, head_dim] chunk into
+ * 256-slot pages; replaces the index_copy_ of PagedHybridCache.update
+ * (src/paged_decode/hybrid.py:63-72).  Element (b, h, s, d) goes to page
+ * table[b, positions[s] / 256], slot positions[s] % 256, kv head h.  `positions`
+ * is int64 [steps]; a negative position or table entry, or a page index at or
+ * past table_width, skips the row.  head_dim in {64, 128, 256}; strides in
+ * elements, multiples of 8; pointers 16-byte aligned. */
+int pd_store_kv_pages(const void* key, int64_t key_stride_b, int64_t key_stride_h,
+                      int64_t key_stride_s, const void* value, int64_t value_stride_b,
+                      int64_t value_stride_h, int64_t value_stride_s, void* k_pages,
+                      void* v_pages, const int32_t* table, int64_t table_stride_b,
+                      int32_t table_width, const int64_t* positions, int32_t batch,
+                      int32_t num_kv_heads, int32_t steps, int32_t head_dim, pd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -587,7 +587,7 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
         for (int j = 0; j < C::kNB; ++j) mine[h * D + 16 * j + qh] = acc[j][r];
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   const int idx0 = tid * C::kE;
   const int h = idx0 / D, dd = idx0 % D;  // kE divides D, so one head per thread

@@ -40,6 +40,9 @@ SIGNATURES = {
     "pd_split_fixed": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp,
                        _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_ml_merge": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
+    "pd_store_kv": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _vp],
+    "pd_store_kv_pages": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i32,
+                          _vp, _i32, _i32, _i32, _i32, _vp],
 }
 
 _lib = None
@@ -140,3 +143,22 @@ def ml_merge(maxima, denoms, accums, out, batch):
     _, h, parts, d = accums.shape
     check(lib().pd_ml_merge(maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(),
                             out.data_ptr(), batch, h, d, parts, stream_handle(out.device)))
+
+
+def store_kv(key, value, k_cache, v_cache, slot_mapping):
+    """key/value [N, Hkv, D] (rows 16-byte aligned); caches [..., Hkv, D] flat over slots."""
+    n, hkv, d = key.shape
+    check(lib().pd_store_kv(key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+                            k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), n,
+                            hkv * d, stream_handle(key.device)))
+
+
+def store_kv_pages(key, value, k_pages, v_pages, tables, positions):
+    """key/value [B, Hkv, S, D]; pages [P, 256, Hkv, D]; tables int32 [B, W]; positions int64 [S]."""
+    b, hkv, steps, d = key.shape
+    check(lib().pd_store_kv_pages(key.data_ptr(), key.stride(0), key.stride(1), key.stride(2),
+                                  value.data_ptr(), value.stride(0), value.stride(1),
+                                  value.stride(2), k_pages.data_ptr(), v_pages.data_ptr(),
+                                  tables.data_ptr(), tables.stride(0), tables.shape[1],
+                                  positions.data_ptr(), b, hkv, steps, d,
+                                  stream_handle(key.device)))
