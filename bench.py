@@ -232,6 +232,49 @@ def bandwidth_sweep(torch, seed=64, calls=20):
     return result
 
 
+def kv_write_rates(torch, calls=512):
+    """KV-cache page writes (pd_store_kv_pages): a 2048-token prefill chunk and one decode
+    token, B=1, Hkv=2, D=256 (the end-to-end decoder's full-attention geometry)."""
+    from paged_decode.kv_write import write_pages
+    out = {}
+    for steps in (2048, 1):
+        gen = torch.Generator(device="cuda").manual_seed(steps)
+        width = 2112 // PAGE + 1
+        tables = torch.randperm(width, generator=gen, device="cuda").to(torch.int32).view(1, width)
+        key = torch.randn((1, steps, 2, 256), generator=gen, device="cuda").to(torch.bfloat16).transpose(1, 2)
+        value = torch.randn((1, steps, 2, 256), generator=gen, device="cuda").to(torch.bfloat16).transpose(1, 2)
+        pages = [torch.empty((width, PAGE, 2, 256), device="cuda", dtype=torch.bfloat16) for _ in range(2)]
+        positions = torch.arange(steps, device="cuda", dtype=torch.int64)
+        us = graph_time_us(torch, lambda: write_pages(key, value, pages[0], pages[1], tables, positions),
+                           calls, unroll=128)
+        moved = 4 * steps * 2 * 256 * 2  # K and V read, K and V written
+        out[f"tokens_{steps}"] = {"us_per_call": round(us, 3), "gbps": round(moved / us / 1e3, 1)}
+    return out
+
+
+def e2e_decoder(torch, output_tokens=64):
+    """Random-init 24-layer Qwen3.5-geometry decoder (hidden 2048, full attention Hq 8 /
+    Hkv 2 / D 256 every fourth layer, vocab 151936), B=1, greedy decode, one hipGraph per
+    step through pd_store_kv_pages + the matched split-KV decode."""
+    from paged_decode import hybrid
+    model = hybrid.random_init_model(hybrid.decoder_config(), "cuda", 0)
+    runner = hybrid.HybridRunner(model=model, backend="hip_matched", mode="graph",
+                                 max_context=2048 + output_tokens)
+    out = {"workload": "random-init decoder, 24 layers (6 full attention), hidden 2048, vocab 151936, "
+                       "bf16 N(0,0.02), B=1, greedy, graph mode"}
+    for plen in (512, 2048):
+        gen = torch.Generator().manual_seed(plen)
+        prompt = [torch.randint(0, 151936, (plen,), generator=gen).tolist()]
+        res = runner.generate(prompt, output_tokens=output_tokens, timing=True)
+        ms = sorted(res["decode_ms"])
+        mean = sum(ms) / len(ms)
+        out[f"prompt_{plen}"] = {"decode_steps": len(ms), "step_us_median": round(1000 * ms[len(ms) // 2], 1),
+                                 "tokens_per_s": round(1000 / mean, 1)}
+    del runner, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def committed_traffic(key):
     """HBM bytes per dispatch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary."""
     try:
@@ -337,6 +380,8 @@ def main():
                             "us_per_call": round(u528, 3), "tbps": round(b528 / u528 / 1e6, 3)}
         del c528
         extra["bandwidth_sweep"] = bandwidth_sweep(torch)
+        extra["kv_write"] = kv_write_rates(torch)
+        extra["e2e_decoder"] = e2e_decoder(torch)
 
     cpu = None
     if not args.no_cpu:
