@@ -1,0 +1,344 @@
+// Device-side building blocks shared by the paged decode kernels for MI355X
+// (gfx950, CDNA4): numerics, buffer-resource loads, the LSE merge arithmetic,
+// the matched-partition tile geometry, LDS copy/transposed-read helpers and
+// the block-table window.  Included by the kernel translation units only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+namespace pdk {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef float floatx2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;  // ln 2 rounded to float32
+constexpr int kThreads = 256;
+
+// ---------------------------------------------------------------- numerics
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// float32 -> bfloat16 bits, round to nearest even; NaN -> quiet NaN.
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Native gfx950 transcendental instructions (v_exp_f32 = 2^x, v_log_f32 =
+// log2 x, v_rcp_f32 = 1/x); ln and e^x by change of base.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+__device__ __forceinline__ float ln_fast(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
+__device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// a.lo*b.lo + a.hi*b.hi + c over bf16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+__device__ __forceinline__ u32x4_t load16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+// Buffer resource (V#) over `bytes` bytes at `base`; word 3 is the gfx9-family
+// raw-buffer format.  Loads at or past `bytes` return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// E consecutive floats at byte offset `off`; kCoherent sets the sc1 cache
+// policy bit (device-scope coherent, so a line another XCD wrote is re-read).
+// The builtins' results are bit-cast as whole vectors to float vectors before
+// any element is read: reading elements of their integer vector results
+// directly made this compiler emit a single dword load for the whole vector.
+template <int E, bool kCoherent>
+__device__ __forceinline__ void buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, int off,
+                                                float (&x)[E]) {
+  constexpr int aux = kCoherent ? 16 : 0;
+  if constexpr (E == 1) {
+    x[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, aux));
+  } else if constexpr (E == 2) {
+    const u32x2_t t = __builtin_amdgcn_raw_buffer_load_b64(rsrc, off, 0, aux);
+    const floatx2_t f = __builtin_bit_cast(floatx2_t, t);
+    x[0] = f.x;
+    x[1] = f.y;
+  } else {
+    static_assert(E % 4 == 0, "vector width");
+#pragma unroll
+    for (int i = 0; i < E; i += 4) {
+      const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 4 * i, 0, aux);
+      const floatx4_t f = __builtin_bit_cast(floatx4_t, t);
+      x[i] = f.x;
+      x[i + 1] = f.y;
+      x[i + 2] = f.z;
+      x[i + 3] = f.w;
+    }
+  }
+}
+
+// ------------------------------------------------------ LSE merge arithmetic
+// Shared by the standalone merge kernel and the fused decode so that both give
+// bit-identical outputs.
+//
+// Merge weights of one (b, h) row, computed by one full wavefront: lane owns
+// splits `lane` and `lane + 64` (splits <= 128).  M = max lse (-inf -> 0),
+// S = sum exp(lse - M), L = ln S + M (+inf when S == 0), w_p = exp(lse_p - L)
+// (matched_splitkv.py:107-120; an all-empty row gets w = 0 everywhere).  The
+// two loads are unconditional buffer loads (zero past the row, replaced by
+// -inf), so they issue without a branch and queue behind earlier loads.
+template <bool kCoherent>
+__device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lane,
+                                            float& w0, float& w1) {
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(lrow, splits * 4);
+  float a[1], c[1];
+  buffer_load_f32<1, kCoherent>(rsrc, lane * 4, a);
+  buffer_load_f32<1, kCoherent>(rsrc, (lane + 64) * 4, c);
+  const float v0 = lane < splits ? a[0] : -INFINITY;
+  const float v1 = lane + 64 < splits ? c[0] : -INFINITY;
+  float mx = wave_max(fmaxf(v0, v1));
+  if (mx == -INFINITY) mx = 0.f;
+  const float total = wave_sum(exp_fast(v0 - mx) + exp_fast(v1 - mx));
+  const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
+  w0 = exp_fast(v0 - logsum);
+  w1 = exp_fast(v1 - logsum);
+}
+
+// acc[e] = fma(w_p, partial_p[e], acc[e]) for p = 0, 1, ..., splits-1 in order
+// (matched_splitkv.py:121-126).  `row` is the (b, h) row of partials
+// [splits][D]; this thread owns elements dd .. dd+E-1.  Splits are loaded kBatch
+// at a time as straight-line vector loads; the first batch is issued before
+// `prepare()` (which computes the weights), so the partial loads overlap the
+// LSE loads and reductions (a scheduling barrier keeps them issued first).
+// weight(s0, j) returns w_{s0+j}; it must be 0 for splits <= s0+j < 128 and
+// finite for every index.  Past the last split the loads return zero, so the
+// padding steps are fma(w, 0, acc) with w >= 0 finite and leave acc unchanged
+// (acc is never -0: it starts at +0 and a round-to-nearest sum is -0 only if
+// both addends are), so the batch size does not change the result's bits.
+// w_s of a row whose weights lane l holds as w0 = w_l and w1 = w_{l+64}
+// (lse_weights).  For s >= 128 it returns w_{s-64}, a finite value that only
+// multiplies the zero a load past the row returns.
+__device__ __forceinline__ float wave_weight(float w0, float w1, int s) {
+  const float src = s < 64 ? w0 : w1;
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src), s & 63));
+}
+
+template <int E>
+struct MergeBatch {
+  static constexpr int value = E == 1 ? 64 : (E == 2 ? 48 : (E == 4 ? 40 : (E == 8 ? 16 : 8)));
+};
+
+template <int E, bool kCoherent, typename PrepareFn, typename WeightFn>
+__device__ __forceinline__ void merge_splits(const float* __restrict__ row, int D, int dd,
+                                             int splits, PrepareFn prepare, WeightFn weight,
+                                             float (&acc)[E]) {
+  constexpr int kBatch = MergeBatch<E>::value;
+  // `row` must be wavefront-uniform: the resource lives in scalar registers.
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(row, splits * D * 4);
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  float x[kBatch][E];
+  auto load = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      buffer_load_f32<E, kCoherent>(rsrc, ((s0 + j) * D + dd) * 4, x[j]);
+  };
+  auto accumulate = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const float wj = weight(s0, j);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = fmaf(wj, x[j][e], acc[e]);
+    }
+  };
+  load(0);
+  __builtin_amdgcn_sched_barrier(0);
+  prepare();
+  accumulate(0);
+  for (int s0 = kBatch; s0 < splits; s0 += kBatch) {
+    load(s0);
+    accumulate(s0);
+  }
+}
+
+// ------------------------------------------------------- matched partition
+//
+// Tile geometry: TILE = 16384 / D tokens (64/128/256 for D = 256/128/64), the
+// reference's tile_tokens (splitkv_plan.py:33), so a tile is always 32 KiB of K
+// and 32 KiB of V and never crosses a 256-token page.  Wavefront w owns tokens
+// [w*TILE/4, (w+1)*TILE/4) of every tile, in groups of 16, for both products.
+//
+// QK^T on v_mfma_f32_16x16x32_bf16: A = K rows (lane L -> token L%16, d = 32c +
+// 8*(L/16) .. +8, loaded straight into registers), B = Q of the GQA group
+// (lane -> head L%16), so lane L holds S[token 4*(L/16)+r][head L%16],
+// r = 0..3.  Padded heads (>= G) have zero Q and zero probabilities.
+//
+// PV on MFMA, with the bf16 probabilities as the A operand taken directly from
+// the QK result registers: lane L holds P[head L%16][tokens 4*(L/16) + r] of
+// each 16-token group, the A layout of v_mfma_f32_16x16x16_bf16 for one group
+// and, for two groups g, g+1 side by side, of v_mfma_f32_16x16x32_bf16
+// (k = 8*(L/16) + e <-> token 16g + 4*(L/16) + e for e < 4, 16(g+1) +
+// 4*(L/16) + e-4 above).  The B operand needs V columns (4 consecutive tokens
+// of one d per lane).  V rows therefore go to LDS by buffer_load ... lds (no
+// registers; lane l of a copy fills bytes 16l .. 16l+15 of its 1 KiB, and
+// reads past the buffer write zeros), each row padded by 16 bytes so that
+// the transposed reads hit distinct banks, and are read with
+// ds_read_b64_tr_b16: in each 16-lane group, when source lane 4c + b
+// addresses row c, columns 4b .. 4b+3 of a 4 x 16 block, lane n receives
+// column n of the block (rows 0..3).  Output lane L holds O[head 4*(L/16) + r]
+// [d = 16j + L%16] of column block j.
+template <int D, int GP>
+struct Matched {
+  static constexpr int kTile = 16384 / D;
+  static constexpr int kTW = kTile / 4;                      // tokens per wavefront
+  static constexpr int kNG = kTW / 16;                       // 16-token groups per wavefront
+  static constexpr int kCH = D / 32;                         // 32-wide k-chunks of QK
+  static constexpr int kNB = D / 16;                         // 16-column blocks of PV
+  static constexpr int kPieces = D / 8 + 1;                  // 16-byte pieces per LDS row
+  static constexpr int kPitch = 16 * kPieces;                // bytes per V row in LDS
+  static constexpr int kDma = (kTW * kPitch + 1023) / 1024;  // 1 KiB copies per wavefront
+  static constexpr int kSlot = 1024 * kDma;                  // LDS bytes of a wavefront's rows
+  static constexpr int kOut = GP * D;                        // outputs of one GQA group
+  static constexpr int kE = kOut >= kThreads ? kOut / kThreads : 1;  // per thread
+  static_assert(kNG >= 1 && kCH >= 1 && 2 * kOut * 4 <= 4 * kSlot, "geometry");
+};
+
+template <int D, int GP>
+struct KTile {
+  u32x4_t k[Matched<D, GP>::kNG][Matched<D, GP>::kCH];
+};
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// 16 bytes at byte offset `off` of a buffer (zero past its end).
+__device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int off) {
+  const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+  return t;
+}
+
+// Four bf16 of one column, transposed out of LDS (see above).  `p` points
+// into a __shared__ array; the LDS address-space casts live in these helpers
+// so that kernel bodies only handle ordinary pointers.
+__device__ __forceinline__ short4_t lds_read_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(const_cast<char*>(p)));
+}
+
+// Copies 16 bytes at byte offset `off` of a buffer into LDS: lane l of the
+// wavefront writes bytes [dst + 16l, dst + 16l + 16); `dst` is wavefront-uniform.
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t rsrc, char* dst, int off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16,
+                                           off, 0, 0, 0);
+}
+
+// Workgroup barrier for LDS data written with ds_write only.  __syncthreads()
+// also waits for every outstanding vector-memory operation, including the
+// LDS copies of the next tile that are meant to stay in flight; this waits
+// for the LDS instructions only.  The memory clobber keeps the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Wait states between the last MFMA writing `x` and the first vector-ALU read
+// of it.  The hardware does not interlock this dependency, and this compiler
+// emitted none when a branch separated the MFMA from the read: rows 8-15 of
+// the 16x16 result were then read before the MFMA had written them.  24 wait
+// states cover the 8-pass MFMAs used here; the empty statements keep every
+// element's reads after them.
+template <int N>
+__device__ __forceinline__ void mfma_result_barrier(floatx4_t (&x)[N]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(x[N - 1]));
+#pragma unroll
+  for (int i = 0; i < N - 1; ++i) asm volatile("" : "+v"(x[i]));
+}
+
+// bf16 bits of (a, b), round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2_t{a, b}, bf16x2_t));
+}
+
+// Block-table window of one sequence: lane `lane` holds in e[r] the entry of
+// page first + 64 r + lane (r < kRegs), loaded unconditionally through a
+// buffer over the row's `width` entries (zero past the row), so the loads
+// issue at kernel entry in the same round trip as the sequence length.
+// page(t0) of a tile inside the window is a readlane; past the window it is
+// a load of the entry (zero past the row, so a length beyond width * 256 reads
+// page 0 instead of memory outside the table).
+template <int kRegs>
+struct PageWindow {
+  const int32_t* row;
+  int width, first;
+  int32_t e[kRegs];
+
+  __device__ __forceinline__ void load(const int32_t* __restrict__ trow, int width_, int first_,
+                                       int lane) {
+    row = trow;
+    width = width_;
+    first = first_;
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(trow, width_ * 4);
+#pragma unroll
+    for (int r = 0; r < kRegs; ++r)
+      e[r] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, (first_ + 64 * r + lane) * 4, 0, 0);
+  }
+
+  // Waits for the window loads once, here, so that no later wait counts them
+  // (the compiler cannot tell on every path that they have completed).
+  __device__ __forceinline__ void settle() {
+#pragma unroll
+    for (int r = 0; r < kRegs; ++r) asm volatile("" : "+v"(e[r]));
+  }
+
+  // Page of logical token t0 (t0 >= first * 256, wavefront-uniform).
+  __device__ __forceinline__ int page(int t0) const {
+    const int idx = (t0 >> 8) - first;
+    if (idx < 64 * kRegs) {
+      int pg = __builtin_amdgcn_readlane(e[0], idx & 63);
+#pragma unroll
+      for (int r = 1; r < kRegs; ++r) {
+        const int x = __builtin_amdgcn_readlane(e[r], idx & 63);
+        pg = (idx >> 6) == r ? x : pg;
+      }
+      return pg;
+    }
+    return (t0 >> 8) < width ? row[t0 >> 8] : 0;
+  }
+};
+
+// The K and V rows of one tile as buffers that end after row nvalid - 1, so
+// rows past the sequence end read as zero without being fetched (NaN-poisoned
+// slots and dead pages are never touched) and every load is unconditional.
+// Byte sizes fit 32 bits: nvalid <= 256 and Hkv*D*512 < 2^31 (launcher check).
+struct TileBuffers {
+  __amdgpu_buffer_rsrc_t k, v;
+};
+
+__device__ __forceinline__ TileBuffers tile_buffers(const uint16_t* __restrict__ k,
+                                                    const uint16_t* __restrict__ v, int page,
+                                                    int t0, int end, int64_t RS, int kh, int D) {
+  const int64_t base = (int64_t(page) * 256 + (t0 & 255)) * RS + int64_t(kh) * D;
+  const int bytes = (end - t0 < 256 ? end - t0 : 256) * int(RS) * 2;
+  return {buffer_rsrc(k + base, bytes), buffer_rsrc(v + base, bytes)};
+}
+
+}  // namespace pdk

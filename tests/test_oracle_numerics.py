@@ -43,4 +43,4 @@ def test_ulp_distance():
     assert bf16_ulp_distance(np.float32(0), np.float32(-0.0)) == 0
     assert bf16_ulp_distance(-one, -nxt) == 1
     assert next_pow2(36) == 64 and next_pow2(1) == 1 and next_pow2(64) == 64
-    assert math.isclose(float(bf16_round(np.float32(1 / 3))), 0.333984375)
+    assert math.isclose(float(np.asarray(bf16_round(np.float32(1 / 3))).reshape(-1)[0]), 0.333984375)
