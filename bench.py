@@ -31,6 +31,11 @@ UNROLL = 128               # calls per captured graph (reference convention)
 PAGE = 256
 
 
+def progress(msg):
+    """One line per finished measurement, on stderr (the JSON line stays alone on stdout)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def algorithmic_bytes(lengths, batch, hq, hkv, dim, with_output=True):
     """Bytes the operator must move: K+V rows, Q, output, live table entries, lengths."""
     kv = sum(int(n) for n in lengths) * hkv * dim * 2 * 2
@@ -354,6 +359,8 @@ def main():
     fused_us = graph_time_us(torch, case["fused"], args.steps)
     part_us = graph_time_us(torch, case["partition"], args.steps)
     merge_us = graph_time_us(torch, case["merge"], args.steps)
+    progress(f"headline: {us:.3f} us/call, partition {part_us:.3f}, merge {merge_us:.3f}, "
+             f"fused {fused_us:.3f}")
     nbytes = algorithmic_bytes([ctx], 1, 16, 4, 256)
     part_bytes = algorithmic_bytes([ctx], 1, 16, 4, 256, with_output=False)
     tbps = nbytes / us / 1e6
@@ -379,15 +386,22 @@ def main():
         extra["ctx_528"] = {"plan": f"{c528['plan'].splits}x{c528['plan'].tokens_per_split}",
                             "us_per_call": round(u528, 3), "tbps": round(b528 / u528 / 1e6, 3)}
         del c528
+        progress("reference protocol, 1024-token partitions and context 528 done")
         extra["bandwidth_sweep"] = bandwidth_sweep(torch)
+        progress(f"bandwidth sweep: {extra['bandwidth_sweep']['us_per_call']} us/call")
         extra["kv_write"] = kv_write_rates(torch)
+        progress("kv write done")
         extra["e2e_decoder"] = e2e_decoder(torch)
+        progress("e2e decoder done")
 
     cpu = None
     if not args.no_cpu:
+        # The box's CPU share for one GPU is 16 threads, whatever os.cpu_count() reports.
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
         one = cpu_baseline(ctx, 1, args.cpu_budget)
-        allc = cpu_baseline(ctx, os.cpu_count() or 1, args.cpu_budget)
-        best = min((one, 1), (allc, os.cpu_count() or 1), key=lambda x: x[0]["us"])
+        allc = cpu_baseline(ctx, threads, args.cpu_budget)
+        progress(f"cpu baseline: {one['us']:.0f} us (1 thread), {allc['us']:.0f} us (all)")
+        best = min((one, 1), (allc, threads), key=lambda x: x[0]["us"])
         cpu = {"value": round(nbytes / best[0]["us"] / 1e6, 6), "unit": "TB/s",
                "cores": best[1], "kind": "port",
                "us_per_call": round(best[0]["us"], 1),
