@@ -57,6 +57,25 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Reductions over the four 16-lane rows of a wavefront (lanes L, L^16, L^32,
+// L^48) with v_permlane16_swap / v_permlane32_swap: each swap returns the
+// pair {x[L], x[L^16]} (or {x[L], x[L^32]}) in some order, so a commutative
+// op over the pair is the same for every lane.  Pure VALU, no LDS traffic.
+// The sum adds x[L] + x[L^16] first, then the xor-32 partner, the same
+// association as a butterfly over shuffles at distance 16 then 32.
+__device__ __forceinline__ float max_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ u32x4_t load16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
@@ -218,9 +237,7 @@ struct Matched {
   static constexpr int kPitch = 16 * kPieces;                // bytes per V row in LDS
   static constexpr int kDma = (kTW * kPitch + 1023) / 1024;  // 1 KiB copies per wavefront
   static constexpr int kSlot = 1024 * kDma;                  // LDS bytes of a wavefront's rows
-  static constexpr int kOut = GP * D;                        // outputs of one GQA group
-  static constexpr int kE = kOut >= kThreads ? kOut / kThreads : 1;  // per thread
-  static_assert(kNG >= 1 && kCH >= 1 && 2 * kOut * 4 <= 4 * kSlot, "geometry");
+  static_assert(kNG >= 1 && kCH >= 1, "geometry");
 };
 
 template <int D, int GP>

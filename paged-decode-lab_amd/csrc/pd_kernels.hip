@@ -5,7 +5,8 @@
 //   matched_partition  one 256-thread workgroup per (split, kv head, sequence):
 //                      QK^T on MFMA (v_mfma_f32_16x16x32_bf16), FP32 online
 //                      softmax over 16384/D-token tiles walked last-to-first,
-//                      PV on v_dot2_f32_bf16 with bf16(p) shared through LDS,
+//                      PV on MFMA with bf16(p) taken from the QK result
+//                      registers and V staged in LDS by buffer_load ... lds,
 //                      normalized FP32 partial + LSE out.
 //   lse_merge          one D-thread workgroup per (sequence, query head):
 //                      stable log-sum-exp merge of the split partials, bf16 out.
@@ -112,10 +113,10 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   float m_own = -INFINITY;  // running max of head qh
   float l_own = 0.f;        // this lane's share of head qh's denominator
 
-  // Issues the loads of tile ti (ti < 0: an empty load, nothing fetched).
+  // Issues the loads of tile ti (0 <= ti < count).
   auto issue = [&](KTile<D, GP>& R, char* slot, int ti) __attribute__((always_inline)) {
-    const int t0 = start + (ti > 0 ? ti : 0) * TILE;
-    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, ti >= 0 ? end : t0, RS, kh, D);
+    const int t0 = start + ti * TILE;
+    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
 #pragma unroll
     for (int g = 0; g < C::kNG; ++g)
 #pragma unroll
@@ -126,7 +127,9 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
       lds_copy16(buf.v, slot + w * C::kSlot + 1024 * i, voff[i]);
   };
 
-  auto process = [&](const KTile<D, GP>& R, const char* slot, int ti)
+  // first: ti == count - 1, the first tile walked; acc is still zero there,
+  // so its rescale by alpha (0 for a running max of -inf) is skipped.
+  auto process = [&](const KTile<D, GP>& R, const char* slot, int ti, bool first)
                      __attribute__((always_inline)) {
     const int nvalid = end - (start + ti * TILE);
     // ---- scores
@@ -151,8 +154,7 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
 #pragma unroll
     for (int g = 0; g < C::kNG; ++g)
       mx = fmaxf(fmaxf(mx, fmaxf(s[g][0], s[g][1])), fmaxf(s[g][2], s[g][3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max_rows(mx);
     float (*wm)[16] = sm.wmax[ti & 1];
     if (lane < 16) wm[w][lane] = mx;
     lds_barrier();
@@ -188,7 +190,7 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
     }
     l_own = l_own * a_own + psum;
     // ---- PV (rescale only when a running maximum moved; alpha = 1 otherwise)
-    if (__builtin_amdgcn_ballot_w64(moved)) {
+    if (!first && __builtin_amdgcn_ballot_w64(moved)) {
 #pragma unroll
       for (int j = 0; j < C::kNB; ++j)
 #pragma unroll
@@ -221,73 +223,80 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
 
   // Reverse tile walk (matched_splitkv.py:71): last tile first.  Two register
   // sets and two LDS slots alternate: the loads of the next tile are issued
-  // before the current one is computed.  The load after the last tile is an
-  // empty one (a buffer of 0 bytes, nothing fetched), so every iteration
-  // issues the same loads.
+  // before the current one is computed.  The loop handles tiles in pairs and
+  // the last one or two tiles are peeled, so no load is issued past tile 0
+  // (an issue takes the CU's load path for as long as a real one).
   pw.settle();
   if (count > 0) {
     KTile<D, GP> A, B;
     int ti = count - 1;
     issue(A, vs0, ti);
-    while (true) {
+    bool first = true;
+    while (ti >= 2) {
       issue(B, vs1, ti - 1);
-      process(A, vs0, ti);
-      if (--ti < 0) break;
-      issue(A, vs0, ti - 1);
-      process(B, vs1, ti);
-      if (--ti < 0) break;
+      process(A, vs0, ti, first);
+      issue(A, vs0, ti - 2);
+      process(B, vs1, ti - 1, false);
+      ti -= 2;
+      first = false;
+    }
+    if (ti == 1) {
+      issue(B, vs1, 0);
+      process(A, vs0, 1, first);
+      process(B, vs1, 0, false);
+    } else {
+      process(A, vs0, 0, first);
     }
   }
 
   // ---- epilogue: combine the 4 waves' accumulators and denominators
-  float l = l_own;
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
+  const float l = sum_rows(l_own);
   if (lane < 16) sm.lsum[w][lane] = l;
   if (tid < 16) sm.mfin[tid] = m_own;
   __syncthreads();  // every wavefront is done with its V rows (aliased by red)
-  // O of wavefront w for the group's heads: waves 0, 1 in vs0, waves 2, 3 in vs1.
+  // O of wavefront w as 16-byte slots: slot (q, j, n) holds the four heads
+  // 4q .. 4q+3 of column 16j + n, i.e. lane 16q + n's acc[j] as it is (one
+  // ds_write_b128 per column block).  Only the row groups q < NQ hold real
+  // heads.  Waves 0, 1 use vs0 and waves 2, 3 use vs1.
+  constexpr int NQ = GP >= 4 ? GP / 4 : 1;
+  constexpr int kSlots = NQ * C::kNB * 16;
+  static_assert(2 * kSlots * 16 <= 4 * C::kSlot, "reduction buffer");
   auto red = [&](int wave) __attribute__((always_inline)) {
-    return reinterpret_cast<float*>(wave < 2 ? vs0 : vs1) + (wave & 1) * C::kOut;
+    return reinterpret_cast<floatx4_t*>(wave < 2 ? vs0 : vs1) + (wave & 1) * kSlots;
   };
-  {
-    float* mine = red(w);
+  if (qg < NQ) {
+    floatx4_t* mine = red(w) + qg * C::kNB * 16 + qh;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * qg + r;
-      if (h < GP)
-#pragma unroll
-        for (int j = 0; j < C::kNB; ++j) mine[h * D + 16 * j + qh] = acc[j][r];
-    }
+    for (int j = 0; j < C::kNB; ++j) mine[16 * j] = acc[j];
   }
   lds_barrier();
 
-  const int idx0 = tid * C::kE;
-  const int h = idx0 / D, dd = idx0 % D;  // kE divides D, so one head per thread
-  if (idx0 < C::kOut && h < G) {
-    const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
-    const float safe = den > 0.f ? den : 1.f;
-    const float inv = rcp_fast(safe);
-    const int64_t orow = (int64_t(b) * Hq + kh * G + h) * splits + p;
-    float* dst = partials + orow * D + dd;
-    const float lv = den > 0.f ? fmaf(sm.mfin[h], scale, ln_fast(safe)) : -INFINITY;
-    float val[C::kE];
+  // Thread t sums slot t (and t + 256, ...) over the waves in a fixed order
+  // and writes the normalized values of its (up to) four heads; for each head
+  // the threads of a wavefront write consecutive columns.
+  for (int sl = tid; sl < kSlots; sl += kThreads) {
+    const int q = sl / (C::kNB * 16), col = sl % (C::kNB * 16);
+    const floatx4_t o0 = red(0)[sl], o1 = red(1)[sl], o2 = red(2)[sl], o3 = red(3)[sl];
 #pragma unroll
-    for (int e = 0; e < C::kE; ++e) {
-      const int i = idx0 + e;
-      val[e] = ((red(0)[i] + red(1)[i]) + (red(2)[i] + red(3)[i])) * inv;
-    }
-    if constexpr (kFused) {
-      // Device-scope stores (global_store sc1): written through to the
-      // coherence point, so another XCD can read them without any L2 flush.
-#pragma unroll
-      for (int e = 0; e < C::kE; ++e)
-        __hip_atomic_store(dst + e, val[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (dd == 0) __hip_atomic_store(lse_out + orow, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-#pragma unroll
-      for (int e = 0; e < C::kE; ++e) dst[e] = val[e];
-      if (dd == 0) lse_out[orow] = lv;
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * q + r;
+      if (h >= G) break;
+      const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
+      const float safe = den > 0.f ? den : 1.f;
+      const float val = ((o0[r] + o1[r]) + (o2[r] + o3[r])) * rcp_fast(safe);
+      const int64_t orow = (int64_t(b) * Hq + kh * G + h) * splits + p;
+      const float lv = den > 0.f ? fmaf(sm.mfin[h], scale, ln_fast(safe)) : -INFINITY;
+      if constexpr (kFused) {
+        // Device-scope stores (global_store sc1): written through to the
+        // coherence point, so another XCD can read them without any L2 flush.
+        __hip_atomic_store(partials + orow * D + col, val, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (col == 0)
+          __hip_atomic_store(lse_out + orow, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        partials[orow * D + col] = val;
+        if (col == 0) lse_out[orow] = lv;
+      }
     }
   }
 
