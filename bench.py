@@ -237,6 +237,29 @@ def bandwidth_sweep(torch, seed=64, calls=20):
     return result
 
 
+def context_sweep(torch, contexts=(8192, 32768, 131072)):
+    """D256 GQA 4:1 (Hq 16, Hkv 4), B=1 at longer contexts, planner plan.  At 131072
+    tokens the KV (537 MB) exceeds the 256 MB last-level cache, so the reads come
+    from HBM; the shorter ones are partly cache-resident across replays."""
+    out = {}
+    for ctx in contexts:
+        case = matched_case(torch, 1, 16, 4, 256, ctx, [ctx], 11)
+        calls = max(32, min(512, 4 * 131072 // ctx))
+        us = graph_time_us(torch, case["full"], calls, unroll=16)
+        part_us = graph_time_us(torch, case["partition"], calls, unroll=16)
+        nbytes = algorithmic_bytes([ctx], 1, 16, 4, 256)
+        pbytes = algorithmic_bytes([ctx], 1, 16, 4, 256, with_output=False)
+        p = case["plan"]
+        out[f"ctx_{ctx}"] = {"plan": f"{p.splits}x{p.tokens_per_split}",
+                             "us_per_call": round(us, 2), "tbps": round(nbytes / us / 1e6, 3),
+                             "pct_peak": round(100 * nbytes / us / 1e6 / PEAK_TBPS, 1),
+                             "partition_us": round(part_us, 2),
+                             "partition_pct_peak": round(100 * pbytes / part_us / 1e6 / PEAK_TBPS, 1)}
+        del case
+        torch.cuda.empty_cache()
+    return out
+
+
 def kv_write_rates(torch, calls=512):
     """KV-cache page writes (pd_store_kv_pages): a 2048-token prefill chunk and one decode
     token, B=1, Hkv=2, D=256 (the end-to-end decoder's full-attention geometry)."""
@@ -387,6 +410,9 @@ def main():
                             "us_per_call": round(u528, 3), "tbps": round(b528 / u528 / 1e6, 3)}
         del c528
         progress("reference protocol, 1024-token partitions and context 528 done")
+        extra["context_sweep_d256_gqa4"] = context_sweep(torch)
+        progress("context sweep: " + ", ".join(f"{k} {v['pct_peak']}%" for k, v in
+                                                extra["context_sweep_d256_gqa4"].items()))
         extra["bandwidth_sweep"] = bandwidth_sweep(torch)
         progress(f"bandwidth sweep: {extra['bandwidth_sweep']['us_per_call']} us/call")
         extra["kv_write"] = kv_write_rates(torch)

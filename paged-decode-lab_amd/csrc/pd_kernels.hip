@@ -335,16 +335,18 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
 }
 
 // ------------------------------------------------------------- LSE merge
-// One workgroup of D threads per (b, h) row, one output element per thread.
+// One wavefront per (b, h) row and 64-column chunk (grid rows x D/64), one
+// output element per lane, so a row's partials are read by D/64 CUs at once.
 // Every wavefront computes the row's weights itself (the same arithmetic, so
-// the same bits) and broadcasts them with readlane: no LDS, no barrier.
+// the same bits in every chunk) and broadcasts them with readlane: no LDS, no
+// barrier.
 template <int D>
-__global__ void __launch_bounds__(D)
+__global__ void __launch_bounds__(64)
 lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ lse,
                  uint16_t* __restrict__ out, int splits) {
   const int64_t row = blockIdx.x;
-  const int dd = threadIdx.x;
-  const int lane = dd & 63;
+  const int lane = threadIdx.x;
+  const int dd = blockIdx.y * 64 + lane;
   float w0 = 0.f, w1 = 0.f, acc[1];
   merge_splits<1, false>(
       partials + row * splits * D, D, dd, splits,
@@ -686,15 +688,16 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
   if (rows > 0x7fffffff) return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto* o = static_cast<uint16_t*>(out);
+  const dim3 grid(unsigned(rows), head_dim / 64);
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(lse_merge_kernel<64>, dim3(rows), dim3(64), 0, st, partials, lse, o, splits);
+      hipLaunchKernelGGL(lse_merge_kernel<64>, grid, dim3(64), 0, st, partials, lse, o, splits);
       break;
     case 128:
-      hipLaunchKernelGGL(lse_merge_kernel<128>, dim3(rows), dim3(128), 0, st, partials, lse, o, splits);
+      hipLaunchKernelGGL(lse_merge_kernel<128>, grid, dim3(64), 0, st, partials, lse, o, splits);
       break;
     default:
-      hipLaunchKernelGGL(lse_merge_kernel<256>, dim3(rows), dim3(256), 0, st, partials, lse, o, splits);
+      hipLaunchKernelGGL(lse_merge_kernel<256>, grid, dim3(64), 0, st, partials, lse, o, splits);
       break;
   }
   return launch_status("pd_lse_merge");
