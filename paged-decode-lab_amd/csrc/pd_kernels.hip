@@ -334,6 +334,193 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   }
 }
 
+// ----------------------------------------------------- single-tile partition
+// The same partial + LSE as matched_partition_kernel for plans whose splits
+// are exactly one tile (tokens_per_split == 16384 / D: the headline D=256
+// plan of 64-token splits, and every plan of small contexts).  With a single
+// tile there is no running maximum to carry, so the workgroup splits the PV
+// product by output columns instead of by tokens: after the QK scores and the
+// tile maximum, every wavefront writes its bf16 probabilities to LDS, and
+// wavefront w then multiplies the whole tile's P by V columns
+// [w*D/4, (w+1)*D/4) on v_mfma_f32_16x16x32_bf16.  That needs one more barrier
+// but no cross-wave reduction of O at the end, and half the PV instructions
+// of the 16-token grouping at D=256.  Scores, maxima, probabilities,
+// denominators and LSEs are bit-identical to matched_partition_kernel's; the
+// partial differs only in the fp32 summation order of P V.
+template <int D>
+struct TileP {
+  static constexpr int kTile = 16384 / D;
+  // Bytes per head row of P: 8 bytes of padding put the 16 rows of a
+  // ds_write_b64 / ds_read_b64 in different banks (row r starts at bank 2r).
+  static constexpr int kPitch = 2 * kTile + 8;
+  static constexpr int kCols = D / 4;        // output columns per wavefront
+  static constexpr int kNBW = kCols / 16;    // 16-column blocks per wavefront
+  static constexpr int kKS = kTile / 32;     // 32-token k-steps of PV
+};
+
+template <int D, int GP>
+__global__ void __launch_bounds__(kThreads, 2)
+matched_tile_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
+                    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                    const int32_t* __restrict__ table, int64_t tsb, int width,
+                    const int32_t* __restrict__ lengths, float* __restrict__ partials,
+                    float* __restrict__ lse_out, int Hq, int Hkv, int G, int splits,
+                    float scale, float c) {
+  using C = Matched<D, GP>;
+  using P = TileP<D>;
+  constexpr int TILE = C::kTile;
+  __shared__ float wmax[4][16];
+  __shared__ float lsum[4][16];
+  __shared__ __attribute__((aligned(16))) char vs[4 * C::kSlot];
+  __shared__ __attribute__((aligned(16))) char ps[16 * P::kPitch];
+
+  const int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qh = lane & 15, qg = lane >> 4;
+  const int start = p * TILE;
+  PageWindow<1> pw;  // entry 0 of lane 0 is the tile's page
+  pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
+  const int length = lengths[b];
+  const int end = min(start + TILE, length);
+  const int64_t RS = int64_t(Hkv) * D;
+  const int64_t row0 = (int64_t(b) * Hq + kh * G) * splits + p;  // (head 0 of the group, p)
+
+  if (end <= start) {
+    // Empty split: partial 0 (acc 0 times rcp(1)) and LSE -inf, as the
+    // general kernel writes for count == 0.
+    for (int i = tid; i < G * D; i += kThreads)
+      partials[(row0 + int64_t(i / D) * splits) * D + i % D] = 0.f;
+    if (tid < G) lse_out[row0 + int64_t(tid) * splits] = -INFINITY;
+    return;
+  }
+
+  bf16x8_t qf[C::kCH];
+  {
+    const bool live = qh < G;
+    const uint16_t* qrow =
+        q + int64_t(b) * qsb + int64_t(kh * G + (live ? qh : 0)) * qsh + 8 * qg;
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch)
+      qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
+  }
+  const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
+  int voff[C::kDma];
+#pragma unroll
+  for (int i = 0; i < C::kDma; ++i) {
+    const int slot = 64 * i + lane;
+    const int row = slot / C::kPieces, piece = slot % C::kPieces;
+    voff[i] = row < C::kTW && piece < D / 8 ? ((w * C::kTW + row) * int(RS) + 8 * piece) * 2
+                                            : 0x7ffffff0;
+  }
+
+  pw.settle();
+  KTile<D, GP> R;
+  {
+    const TileBuffers buf = tile_buffers(k, v, pw.page(start), start, end, RS, kh, D);
+#pragma unroll
+    for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+      for (int ch = 0; ch < C::kCH; ++ch)
+        R.k[g][ch] = buffer_load16(buf.k, koff + g * 16 * int(RS) * 2 + 64 * ch);
+#pragma unroll
+    for (int i = 0; i < C::kDma; ++i) lds_copy16(buf.v, vs + w * C::kSlot + 1024 * i, voff[i]);
+  }
+
+  // ---- scores of this wavefront's tokens, tile maximum per head
+  const int nvalid = end - start;
+  floatx4_t s[C::kNG];
+#pragma unroll
+  for (int g = 0; g < C::kNG; ++g) {
+    s[g] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch)
+      s[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, R.k[g][ch]),
+                                                      qf[ch], s[g], 0, 0, 0);
+  }
+  mfma_result_barrier(s);
+  if (nvalid < TILE) {
+#pragma unroll
+    for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (w * C::kTW + 16 * g + 4 * qg + r >= nvalid) s[g][r] = -INFINITY;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < C::kNG; ++g)
+    mx = fmaxf(fmaxf(mx, fmaxf(s[g][0], s[g][1])), fmaxf(s[g][2], s[g][3]));
+  mx = max_rows(mx);
+  if (lane < 16) wmax[w][lane] = mx;
+  lds_barrier();
+  // m' = max(-inf, tile max) = the tile maximum (matched_splitkv.py:77-78).
+  const float m_own = fmaxf(fmaxf(wmax[0][qh], wmax[1][qh]), fmaxf(wmax[2][qh], wmax[3][qh]));
+  const float neg_mc = -(m_own * c);
+  float psum = 0.f;
+#pragma unroll
+  for (int g = 0; g < C::kNG; ++g) {
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = exp2_fast(fmaf(s[g][r], c, neg_mc));
+      psum += pr[r];
+    }
+    // P[head qh][tokens w*kTW + 16g + 4qg .. +3] into the head's LDS row.
+    const u32x2_t pb{qh < G ? pack_bf16(pr[0], pr[1]) : 0u, qh < G ? pack_bf16(pr[2], pr[3]) : 0u};
+    *reinterpret_cast<u32x2_t*>(ps + qh * P::kPitch + (w * C::kTW + 16 * g + 4 * qg) * 2) = pb;
+  }
+  const float l = sum_rows(psum);
+  if (lane < 16) lsum[w][lane] = l;
+  __syncthreads();  // P rows, denominators and every wavefront's V rows are in LDS
+
+  // ---- PV: O[heads][this wavefront's columns] over the whole tile.  k-step
+  // ks covers tokens 32ks .. 32ks+31; lane L supplies k = 8(L/16) + e <->
+  // token 32ks + 8(L/16) + e for both operands.
+  floatx4_t acc[P::kNBW];
+#pragma unroll
+  for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < P::kKS; ++ks) {
+    // Two 8-byte reads: the 8-byte row padding keeps them bank-conflict free
+    // but leaves odd rows off 16-byte alignment.
+    const char* prow = ps + qh * P::kPitch + (32 * ks + 8 * qg) * 2;
+    const u32x2_t a0 = *reinterpret_cast<const u32x2_t*>(prow);
+    const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(prow + 8);
+    const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{a0[0], a0[1], a1[0], a1[1]});
+    const int t_lo = 32 * ks + 8 * qg + (qh >> 2), t_hi = t_lo + 4;
+    const char* lo_row = vs + (t_lo / C::kTW) * C::kSlot + (t_lo % C::kTW) * C::kPitch;
+    const char* hi_row = vs + (t_hi / C::kTW) * C::kSlot + (t_hi % C::kTW) * C::kPitch;
+#pragma unroll
+    for (int j = 0; j < P::kNBW; ++j) {
+      const int cb = (w * P::kCols + 16 * j) * 2 + 8 * (qh & 3);
+      const short4_t lo = lds_read_tr(lo_row + cb);
+      const short4_t hi = lds_read_tr(hi_row + cb);
+      const bf16x8_t bv = __builtin_bit_cast(
+          bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo)[0], __builtin_bit_cast(u32x2_t, lo)[1],
+                            __builtin_bit_cast(u32x2_t, hi)[0], __builtin_bit_cast(u32x2_t, hi)[1]});
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
+    }
+  }
+
+  // ---- epilogue: lane L holds O[head 4*qg + r][w*D/4 + 16j + qh]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * qg + r;
+    if (h >= G) break;
+    const float den = (lsum[0][h] + lsum[1][h]) + (lsum[2][h] + lsum[3][h]);
+    const float safe = den > 0.f ? den : 1.f;
+    const float inv = rcp_fast(safe);
+    float* dst = partials + (row0 + int64_t(h) * splits) * D + w * P::kCols + qh;
+#pragma unroll
+    for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = acc[j][r] * inv;
+    if (w == 0 && qh == 0) {
+      const float mh = fmaxf(fmaxf(wmax[0][h], wmax[1][h]), fmaxf(wmax[2][h], wmax[3][h]));
+      lse_out[row0 + int64_t(h) * splits] =
+          den > 0.f ? fmaf(mh, scale, ln_fast(safe)) : -INFINITY;
+    }
+  }
+}
+
 // ------------------------------------------------------------- LSE merge
 // One wavefront per (b, h) row and 64-column chunk (grid rows x D/64), one
 // output element per lane, so a row's partials are read by D/64 CUs at once.
@@ -569,6 +756,22 @@ struct PartitionArgs {
   float scale, c;
 };
 
+template <int D>
+void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
+#define PD_LAUNCH_TILE(GPV)                                                                   \
+  hipLaunchKernelGGL((matched_tile_kernel<D, GPV>), grid, dim3(kThreads), 0, stream, a.q,     \
+                     a.qsb, a.qsh, a.k, a.v, a.table, a.tsb, a.width, a.lengths, a.partials,  \
+                     a.lse, a.Hq, a.Hkv, a.G, a.splits, a.scale, a.c)
+  switch (gp) {
+    case 1: PD_LAUNCH_TILE(1); break;
+    case 2: PD_LAUNCH_TILE(2); break;
+    case 4: PD_LAUNCH_TILE(4); break;
+    case 8: PD_LAUNCH_TILE(8); break;
+    default: PD_LAUNCH_TILE(16); break;
+  }
+#undef PD_LAUNCH_TILE
+}
+
 template <int D, bool kFused>
 void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_GP(GPV)                                                                     \
@@ -630,6 +833,14 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
   const dim3 grid(splits, num_kv_heads, batch);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int gp = padded_group(G);
+  if (!fused && tokens_per_split == tile_tokens) {
+    switch (head_dim) {
+      case 64: launch_tile_d<64>(gp, grid, st, a); break;
+      case 128: launch_tile_d<128>(gp, grid, st, a); break;
+      default: launch_tile_d<256>(gp, grid, st, a); break;
+    }
+    return launch_status(what);
+  }
   switch (head_dim * 2 + (fused ? 1 : 0)) {
     case 128: launch_partition_d<64, false>(gp, grid, st, a); break;
     case 129: launch_partition_d<64, true>(gp, grid, st, a); break;
