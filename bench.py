@@ -359,12 +359,17 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU run")
     ap.add_argument("--profile", default=None, metavar="headline,sweep",
                     help="only make eager launches for rocprofv3 (calibration copy + cases)")
+    ap.add_argument("--require-idle-gpu", action="store_true",
+                    help="refuse to run (before any GPU work) if amd-smi lists other processes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the operator has no multi-GPU path)", file=sys.stderr)
         sys.exit(2)
 
+    from paged_decode import benchmark_protocol
+    if args.require_idle_gpu:
+        benchmark_protocol.require_idle_gpu()
     import torch
     from paged_decode import _native
     _native.lib()
@@ -455,6 +460,7 @@ def main():
                      "us_per_launch": round(part_us, 3)},
         "cpu_baseline": cpu,
         **extra,
+        "environment": benchmark_protocol.fingerprint(torch),
     }
     print(json.dumps(line))
 
