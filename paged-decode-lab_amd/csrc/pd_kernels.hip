@@ -113,8 +113,8 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   float m_own = -INFINITY;  // running max of head qh
   float l_own = 0.f;        // this lane's share of head qh's denominator
 
-  // Issues the loads of tile ti (0 <= ti < count).
-  auto issue = [&](KTile<D, GP>& R, char* slot, int ti) __attribute__((always_inline)) {
+  // Loads of tile ti (0 <= ti < count): K rows into registers, V rows into LDS.
+  auto issue_k = [&](KTile<D, GP>& R, int ti) __attribute__((always_inline)) {
     const int t0 = start + ti * TILE;
     const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
 #pragma unroll
@@ -122,6 +122,10 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
 #pragma unroll
       for (int ch = 0; ch < C::kCH; ++ch)
         R.k[g][ch] = buffer_load16(buf.k, koff + g * 16 * int(RS) * 2 + 64 * ch);
+  };
+  auto issue_v = [&](char* slot, int ti) __attribute__((always_inline)) {
+    const int t0 = start + ti * TILE;
+    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
 #pragma unroll
     for (int i = 0; i < C::kDma; ++i)
       lds_copy16(buf.v, slot + w * C::kSlot + 1024 * i, voff[i]);
@@ -129,7 +133,9 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
 
   // first: ti == count - 1, the first tile walked; acc is still zero there,
   // so its rescale by alpha (0 for a running max of -inf) is skipped.
-  auto process = [&](const KTile<D, GP>& R, const char* slot, int ti, bool first)
+  // knext >= 0: once the QK products have read R, R is refilled with the K
+  // rows of tile knext (two tiles ahead of ti in the walk).
+  auto process = [&](KTile<D, GP>& R, const char* slot, int ti, bool first, int knext)
                      __attribute__((always_inline)) {
     const int nvalid = end - (start + ti * TILE);
     // ---- scores
@@ -141,6 +147,12 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
       for (int ch = 0; ch < C::kCH; ++ch)
         s[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, R.k[g][ch]),
                                                         qf[ch], s[g], 0, 0, 0);
+    }
+    if (knext >= 0) {
+      // After every QK product has been issued, so the refill reuses R's
+      // registers instead of keeping two generations of K live.
+      __builtin_amdgcn_sched_barrier(0);
+      issue_k(R, knext);
     }
     mfma_result_barrier(s);
     if (nvalid < TILE) {
@@ -222,30 +234,72 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   };
 
   // Reverse tile walk (matched_splitkv.py:71): last tile first.  Two register
-  // sets and two LDS slots alternate: the loads of the next tile are issued
-  // before the current one is computed.  The loop handles tiles in pairs and
-  // the last one or two tiles are peeled, so no load is issued past tile 0
-  // (an issue takes the CU's load path for as long as a real one).
+  // sets and two LDS slots alternate.  V rows are loaded one tile ahead, into
+  // the LDS slot the previous tile's PV has finished reading.  Below D = 256
+  // the K rows are loaded two tiles ahead, into the register set whose QK
+  // products have just been issued (kFar); at D = 256 two live K sets do not
+  // fit the 256-VGPR budget of two waves per SIMD, so K is loaded one tile
+  // ahead, with the V rows.  The loop handles tiles in pairs and the last ones
+  // are peeled, so no load is issued past tile 0 (an issue takes the CU's load
+  // path for as long as a real one).
+  constexpr bool kFar = D < 256;
   pw.settle();
-  if (count > 0) {
+  if constexpr (kFar) {
+    if (count == 1) {
+      KTile<D, GP> A;
+      issue_k(A, 0);
+      issue_v(vs0, 0);
+      process(A, vs0, 0, true, -1);
+    } else if (count > 1) {
+      KTile<D, GP> A, B;
+      int ti = count - 1;
+      issue_k(A, ti);
+      issue_v(vs0, ti);
+      issue_k(B, ti - 1);
+      bool first = true;
+      while (ti >= 3) {
+        issue_v(vs1, ti - 1);
+        process(A, vs0, ti, first, ti - 2);
+        issue_v(vs0, ti - 2);
+        process(B, vs1, ti - 1, false, ti - 3);
+        ti -= 2;
+        first = false;
+      }
+      if (ti == 2) {
+        issue_v(vs1, 1);
+        process(A, vs0, 2, first, 0);
+        issue_v(vs0, 0);
+        process(B, vs1, 1, false, -1);
+        process(A, vs0, 0, false, -1);
+      } else {  // ti == 1
+        issue_v(vs1, 0);
+        process(A, vs0, 1, first, -1);
+        process(B, vs1, 0, false, -1);
+      }
+    }
+  } else if (count > 0) {
     KTile<D, GP> A, B;
     int ti = count - 1;
-    issue(A, vs0, ti);
+    issue_k(A, ti);
+    issue_v(vs0, ti);
     bool first = true;
     while (ti >= 2) {
-      issue(B, vs1, ti - 1);
-      process(A, vs0, ti, first);
-      issue(A, vs0, ti - 2);
-      process(B, vs1, ti - 1, false);
+      issue_k(B, ti - 1);
+      issue_v(vs1, ti - 1);
+      process(A, vs0, ti, first, -1);
+      issue_k(A, ti - 2);
+      issue_v(vs0, ti - 2);
+      process(B, vs1, ti - 1, false, -1);
       ti -= 2;
       first = false;
     }
     if (ti == 1) {
-      issue(B, vs1, 0);
-      process(A, vs0, 1, first);
-      process(B, vs1, 0, false);
+      issue_k(B, 0);
+      issue_v(vs1, 0);
+      process(A, vs0, 1, first, -1);
+      process(B, vs1, 0, false, -1);
     } else {
-      process(A, vs0, 0, first);
+      process(A, vs0, 0, first, -1);
     }
   }
 
