@@ -454,9 +454,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(part_tbps * 1000, 1), "peak": PEAK_TBPS * 1000,
                      "unit": "GB/s", "frac": round(part_tbps / PEAK_TBPS, 4),
                      "traffic": committed_traffic(
-                         "matched_partition_kernel<256,4,false> d256 gqa4 ctx2064"),
+                         "matched_tile_kernel<256,4> d256 gqa4 ctx2064"),
                      "traffic_source": "profiles/traffic.json (2.0 x FETCH_SIZE + WRITE_SIZE)",
-                     "kernel": "matched_partition_kernel<256,4>", "bytes_per_launch": part_bytes,
+                     "kernel": "matched_tile_kernel<256,4> (the partition for single-tile splits)",
+                     "bytes_per_launch": part_bytes,
                      "us_per_launch": round(part_us, 3)},
         "cpu_baseline": cpu,
         **extra,
