@@ -260,6 +260,43 @@ def context_sweep(torch, contexts=(8192, 32768, 131072)):
     return out
 
 
+def paged_backend_rates(torch, seed=64):
+    """paged_decode backends hip_base (one workgroup per sequence x query head) and
+    hip_splitk (fixed 1024-token partitions + m/l/acc merge) on the bandwidth-sweep
+    shape and on the edge-coverage shapes (B=128, a quarter of the lengths 0, the rest
+    U[1,4096]).  Both read each sequence's K/V once per query head, as the reference's
+    grids do, so their HBM traffic is G times the algorithmic bytes counted here."""
+    import numpy as np
+    from paged_decode.runtime import allocate_resources, paged_decode
+    from paged_decode.spec import DecodeSpec
+    out = {}
+    rng = np.random.default_rng(seed)
+    c3 = rng.integers(1, 32769, size=64).tolist()
+    rng4 = np.random.default_rng(4)
+    c4 = [0 if i % 4 == 0 else int(x) for i, x in enumerate(rng4.integers(1, 4097, size=128))]
+    shapes = [("bandwidth sweep B=64 Hq=32 Hkv=8 D=128", 64, 32, 8, 128, 32768, c3,
+               int(100e9 // (PAGE * 8 * 128 * 2))),
+              ("edge coverage B=128 D=64 MHA 16/16", 128, 16, 16, 64, 4096, c4, None),
+              ("edge coverage B=128 D=256 GQA 32/4", 128, 32, 4, 256, 4096, c4, None)]
+    for name, batch, hq, hkv, dim, cap, lengths, pool in shapes:
+        q, k, v, table, lens = make_inputs(torch, batch, hq, hkv, dim, cap, lengths, seed, pool)
+        spec = DecodeSpec(batch, hq, hkv, dim, cap)
+        nbytes = algorithmic_bytes(lengths, batch, hq, hkv, dim)
+        row = {}
+        for backend in ("hip_base", "hip_splitk"):
+            res = allocate_resources(spec, "cuda", backend)
+            fn = lambda: paged_decode(q, k, v, table, lens, resources=res, backend=backend)
+            calls = 8 if pool else 64
+            us = graph_time_us(torch, fn, calls, unroll=4 if pool else 16, warmup=2)
+            row[backend] = {"us_per_call": round(us, 2), "tbps": round(nbytes / us / 1e6, 3),
+                            "pct_peak": round(100 * nbytes / us / 1e6 / PEAK_TBPS, 1)}
+            del res
+        out[name] = row
+        del q, k, v, table, lens
+        torch.cuda.empty_cache()
+    return out
+
+
 def kv_write_rates(torch, calls=512):
     """KV-cache page writes (pd_store_kv_pages): a 2048-token prefill chunk and one decode
     token, B=1, Hkv=2, D=256 (the end-to-end decoder's full-attention geometry)."""
@@ -420,6 +457,8 @@ def main():
                                                 extra["context_sweep_d256_gqa4"].items()))
         extra["bandwidth_sweep"] = bandwidth_sweep(torch)
         progress(f"bandwidth sweep: {extra['bandwidth_sweep']['us_per_call']} us/call")
+        extra["paged_decode_backends"] = paged_backend_rates(torch)
+        progress("paged_decode backends done")
         extra["kv_write"] = kv_write_rates(torch)
         progress("kv write done")
         extra["e2e_decoder"] = e2e_decoder(torch)

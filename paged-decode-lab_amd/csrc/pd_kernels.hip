@@ -5,14 +5,15 @@
 //   matched_partition  one 256-thread workgroup per (split, kv head, sequence):
 //                      QK^T on MFMA (v_mfma_f32_16x16x32_bf16), FP32 online
 //                      softmax over 16384/D-token tiles walked last-to-first,
-//                      PV on MFMA with bf16(p) taken from the QK result
-//                      registers and V staged in LDS by buffer_load ... lds,
-//                      normalized FP32 partial + LSE out.
-//   lse_merge          one D-thread workgroup per (sequence, query head):
+//                      PV on MFMA with the probabilities taken from the QK
+//                      result registers and V staged in LDS by buffer_load ...
+//                      lds.  Three protocols: matched (bf16 p, normalized FP32
+//                      partial + LSE), base (FP32 p, whole context, bf16 out)
+//                      and fixed split (FP32 p, (m, l, acc) per partition).
+//   matched_tile       the matched protocol for splits of exactly one tile,
+//                      with PV split across the wavefronts by output columns.
+//   lse_merge          one wavefront per (sequence, query head, 64 columns):
 //                      stable log-sum-exp merge of the split partials, bf16 out.
-//   online_decode      one 256-thread workgroup per (sequence, query head
-//                      [, fixed partition]): FP32 online softmax with fp32 p,
-//                      either normalized bf16 out (base) or (m, l, acc) state.
 //   ml_merge           one wavefront per (sequence, query head): merge of the
 //                      (m, l, acc) states.
 //
@@ -39,21 +40,43 @@ struct MatchedShared {
   int last;
 };
 
-// kFused = false: the partition alone (pd_partition).
+// kMode selects the protocol of the partition:
+//   kMatched  normalized FP32 partial + LSE, bf16(p) in PV, exp2 with
+//             SCALE_LOG2 (matched_splitkv.py:52-98); kFused = true adds the
+//             in-kernel merge (below).
+//   kBase     the whole context as one partition, FP32 p, natural exp of the
+//             scaled scores, output acc / denom in bf16 (kernels.py:10-41).
+//   kSplit    the same arithmetic over fixed partitions, storing (m, l, acc)
+//             in the reference's units (kernels.py:44-80): m of the scaled
+//             scores into `maxima`, l into `lse_out`, unnormalized acc into
+//             `partials`.
+// FP32 p goes through the bf16 MFMA as three bf16 terms hi + mid + lo (each
+// the RNE bf16 of the previous remainder), which represent p to 2^-27 of its
+// value, finer than p's own float32 rounding; with exact bf16 x bf16 products
+// and FP32 accumulation, P V is then the FP32 sum the reference computes, in
+// another summation order.
+//
 // kFused = true: after writing its partial, each workgroup releases it at
 // device scope and increments counters[b, kh]; the workgroup that completes
 // the count acquires, merges all splits of its GQA group into `out` with the
 // same arithmetic as lse_merge_kernel, and resets the counter to 0, so the
 // counters are zero again when the kernel ends (graph replays need no reset).
-template <int D, int GP, bool kFused>
+//
+// A workgroup serves query heads [qb, qb + Gs) of kv head kh: the whole group
+// (hs = 1) when it has at most 16 heads, else 16-head slices of it (grid.y =
+// Hkv * hs), so the base and fixed-split protocols also cover G > 16.
+constexpr int kMatched = 0, kBase = 1, kSplit = 2;
+
+template <int D, int GP, bool kFused, int kMode>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
                          const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                          const int32_t* __restrict__ table, int64_t tsb, int width,
                          const int32_t* __restrict__ lengths, float* __restrict__ partials,
                          float* __restrict__ lse_out, int* __restrict__ counters,
-                         uint16_t* __restrict__ out, int Hq, int Hkv, int G, int splits, int T,
-                         float scale, float c) {
+                         uint16_t* __restrict__ out, float* __restrict__ maxima, int Hq,
+                         int Hkv, int G, int hs, int splits, int T, float scale, float c) {
+  static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
   using C = Matched<D, GP>;
   constexpr int TILE = C::kTile;
   __shared__ MatchedShared<D, GP> sm;
@@ -63,7 +86,10 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
   __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
 
-  const int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int p = blockIdx.x, b = blockIdx.z;
+  const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
+  const int qb = kh * G + 16 * slice;            // first query head of this workgroup
+  const int Gs = min(16, G - 16 * slice);        // query heads of this workgroup
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = lane & 15, qg = lane >> 4;
@@ -80,9 +106,8 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
   // MFMA B operand of QK: the GQA group's query rows.
   bf16x8_t qf[C::kCH];
   {
-    const bool live = qh < G;
-    const uint16_t* qrow =
-        q + int64_t(b) * qsb + int64_t(kh * G + (live ? qh : 0)) * qsh + 8 * qg;
+    const bool live = qh < Gs;
+    const uint16_t* qrow = q + int64_t(b) * qsb + int64_t(qb + (live ? qh : 0)) * qsh + 8 * qg;
 #pragma unroll
     for (int ch = 0; ch < C::kCH; ++ch)
       qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
@@ -155,6 +180,13 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
       issue_k(R, knext);
     }
     mfma_result_barrier(s);
+    if constexpr (kMode != kMatched) {
+      // Scores in the reference's units: dot(q, k) * SCALE (kernels.py:30).
+#pragma unroll
+      for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[g][r] *= scale;
+    }
     if (nvalid < TILE) {
 #pragma unroll
       for (int g = 0; g < C::kNG; ++g)
@@ -179,26 +211,42 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
       const float tm = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
       const float mn = fmaxf(m4[r], tm);
       moved |= mn != m4[r];
-      alpha[r] = exp2_fast((m4[r] - mn) * c);
+      alpha[r] = kMode == kMatched ? exp2_fast((m4[r] - mn) * c) : exp_fast(m4[r] - mn);
       m4[r] = mn;
     }
     const float tm = fmaxf(fmaxf(wm[0][qh], wm[1][qh]), fmaxf(wm[2][qh], wm[3][qh]));
     const float mn = fmaxf(m_own, tm);
-    const float a_own = exp2_fast((m_own - mn) * c);
+    const float a_own = kMode == kMatched ? exp2_fast((m_own - mn) * c) : exp_fast(m_own - mn);
     m_own = mn;
     const float neg_mc = -(mn * c);
     float psum = 0.f;
-    uint32_t pb[C::kNG][2];  // bf16 probabilities, the PV A operand
+    // PV A operand: bf16 probabilities (matched), or the three bf16 terms of
+    // the FP32 probabilities (base / split), lo first.
+    constexpr int kTerms = kMode == kMatched ? 1 : 3;
+    uint32_t pb[kTerms][C::kNG][2];
 #pragma unroll
     for (int g = 0; g < C::kNG; ++g) {
       float pr[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pr[r] = exp2_fast(fmaf(s[g][r], c, neg_mc));
+        pr[r] = kMode == kMatched ? exp2_fast(fmaf(s[g][r], c, neg_mc)) : exp_fast(s[g][r] - mn);
         psum += pr[r];
       }
-      pb[g][0] = qh < G ? pack_bf16(pr[0], pr[1]) : 0u;
-      pb[g][1] = qh < G ? pack_bf16(pr[2], pr[3]) : 0u;
+      if constexpr (kMode == kMatched) {
+        pb[0][g][0] = qh < Gs ? pack_bf16(pr[0], pr[1]) : 0u;
+        pb[0][g][1] = qh < Gs ? pack_bf16(pr[2], pr[3]) : 0u;
+      } else {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const uint32_t hi = pack_bf16(pr[2 * h2], pr[2 * h2 + 1]);
+          const float r0 = pr[2 * h2] - bf16_lo(hi), r1 = pr[2 * h2 + 1] - bf16_hi(hi);
+          const uint32_t mid = pack_bf16(r0, r1);
+          const uint32_t lo = pack_bf16(r0 - bf16_lo(mid), r1 - bf16_hi(mid));
+          pb[0][g][h2] = qh < Gs ? lo : 0u;
+          pb[1][g][h2] = qh < Gs ? mid : 0u;
+          pb[2][g][h2] = qh < Gs ? hi : 0u;
+        }
+      }
     }
     l_own = l_own * a_own + psum;
     // ---- PV (rescale only when a running maximum moved; alpha = 1 otherwise)
@@ -210,16 +258,17 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
     }
     const char* base = slot + trb;
     if constexpr (C::kNG == 1) {
-      const short4_t a = __builtin_bit_cast(short4_t, u32x2_t{pb[0][0], pb[0][1]});
 #pragma unroll
-      for (int j = 0; j < C::kNB; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, lds_read_tr(base + 32 * j), acc[j],
-                                                           0, 0, 0);
+      for (int j = 0; j < C::kNB; ++j) {
+        const short4_t bv = lds_read_tr(base + 32 * j);
+#pragma unroll
+        for (int t = 0; t < kTerms; ++t)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+              __builtin_bit_cast(short4_t, u32x2_t{pb[t][0][0], pb[t][0][1]}), bv, acc[j], 0, 0, 0);
+      }
     } else {
 #pragma unroll
       for (int g = 0; g < C::kNG; g += 2) {
-        const bf16x8_t a =
-            __builtin_bit_cast(bf16x8_t, u32x4_t{pb[g][0], pb[g][1], pb[g + 1][0], pb[g + 1][1]});
 #pragma unroll
         for (int j = 0; j < C::kNB; ++j) {
           const short4_t lo = lds_read_tr(base + 16 * g * C::kPitch + 32 * j);
@@ -227,7 +276,12 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
           const bf16x8_t bv = __builtin_bit_cast(
               bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo)[0], __builtin_bit_cast(u32x2_t, lo)[1],
                                 __builtin_bit_cast(u32x2_t, hi)[0], __builtin_bit_cast(u32x2_t, hi)[1]});
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
+#pragma unroll
+          for (int t = 0; t < kTerms; ++t) {
+            const bf16x8_t a = __builtin_bit_cast(
+                bf16x8_t, u32x4_t{pb[t][g][0], pb[t][g][1], pb[t][g + 1][0], pb[t][g + 1][1]});
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
+          }
         }
       }
     }
@@ -334,11 +388,24 @@ matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qs
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int h = 4 * q + r;
-      if (h >= G) break;
+      if (h >= Gs) break;
       const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
       const float safe = den > 0.f ? den : 1.f;
-      const float val = ((o0[r] + o1[r]) + (o2[r] + o3[r])) * rcp_fast(safe);
-      const int64_t orow = (int64_t(b) * Hq + kh * G + h) * splits + p;
+      const float num = (o0[r] + o1[r]) + (o2[r] + o3[r]);
+      const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
+      if constexpr (kMode == kBase) {
+        // acc / denom, 0 for an empty sequence (kernels.py:40).
+        out[(int64_t(b) * Hq + qb + h) * D + col] = uint16_t(bf16_bits(num / safe));
+        continue;
+      } else if constexpr (kMode == kSplit) {
+        partials[orow * D + col] = num;
+        if (col == 0) {
+          maxima[orow] = sm.mfin[h];
+          lse_out[orow] = den;
+        }
+        continue;
+      }
+      const float val = num * rcp_fast(safe);
       const float lv = den > 0.f ? fmaf(sm.mfin[h], scale, ln_fast(safe)) : -INFINITY;
       if constexpr (kFused) {
         // Device-scope stores (global_store sc1): written through to the
@@ -596,141 +663,6 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
   out[row * D + dd] = uint16_t(bf16_bits(acc[0]));
 }
 
-// ------------------------------------------------- base / fixed-split kernel
-//
-// One 256-thread workgroup per (b, h[, partition]).  Each row of K/V is read
-// by D/8 lanes (16 bytes each); the 256/(D/8) row groups walk 16384/D-token
-// tiles (one page each), every row group keeping its own (m, l, acc) state
-// with fp32 p, merged across row groups and waves at the end.  With fp32
-// probabilities the result does not depend on the tile schedule beyond
-// float32 rounding.
-template <int D>
-struct Online {
-  static constexpr int kLPR = D / 8;
-  static constexpr int kRG = kThreads / kLPR;
-  static constexpr int kTile = 8 * kRG;  // 16384 / D
-};
-
-template <int D, bool kSplit>
-__global__ void __launch_bounds__(kThreads)
-online_decode_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
-                     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                     const int32_t* __restrict__ table, int64_t tsb, int width,
-                     const int32_t* __restrict__ lengths, uint16_t* __restrict__ out,
-                     float* __restrict__ maxima, float* __restrict__ denoms,
-                     float* __restrict__ accums, int Hq, int Hkv, int G, int parts,
-                     int part_size, float scale) {
-  using C = Online<D>;
-  constexpr int TILE = C::kTile;
-  constexpr int LPR = C::kLPR;
-  __shared__ float wm[4], wl[4];
-  __shared__ float wacc[4][D];
-
-  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int rg = tid / LPR, d0 = (tid % LPR) * 8;
-  const int kh = h / G;
-  const int start = kSplit ? part * part_size : 0;
-  PageWindow<1> pw;  // fetched with the length, as in the matched partition
-  pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
-  const int length = lengths[b];
-  const int end = kSplit ? min(start + part_size, length) : length;
-  const int64_t RS = int64_t(Hkv) * D;
-
-  const u32x4_t qv = load16(q + int64_t(b) * qsb + int64_t(h) * qsh + d0);
-
-  float m = -INFINITY, l = 0.f, acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-
-  pw.settle();
-  for (int t0 = start; t0 < end; t0 += TILE) {
-    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
-    const int nvalid = end - t0;
-    u32x4_t kr[8], vr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int off = ((rg + i * C::kRG) * int(RS) + d0) * 2;
-      kr[i] = buffer_load16(buf.k, off);
-      vr[i] = buffer_load16(buf.v, off);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // all 16 loads in flight before the first use
-    float s[8];
-    float smax = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float x = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) x = dot2(kr[i][e], qv[e], x);
-#pragma unroll
-      for (int msk = 1; msk < LPR; msk <<= 1) x += __shfl_xor(x, msk);
-      x *= scale;
-      s[i] = rg + i * C::kRG < nvalid ? x : -INFINITY;
-      smax = fmaxf(smax, s[i]);
-    }
-    const float mn = fmaxf(m, smax);
-    // A row group with no valid row so far keeps m = -inf; subtract 0 instead
-    // of -inf so that exp(-inf - -inf) never turns the empty state into NaN.
-    const float mref = mn == -INFINITY ? 0.f : mn;
-    const float alpha = exp_fast(m - mref);
-    l *= alpha;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float pr = exp_fast(s[i] - mref);
-      l += pr;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[2 * e] = fmaf(pr, bf16_lo(vr[i][e]), acc[2 * e]);
-        acc[2 * e + 1] = fmaf(pr, bf16_hi(vr[i][e]), acc[2 * e + 1]);
-      }
-    }
-    m = mn;
-  }
-
-  // Merge row groups inside the wave (lanes sharing d0), then across waves.
-#pragma unroll
-  for (int msk = LPR; msk < 64; msk <<= 1) {
-    const float mo = __shfl_xor(m, msk);
-    const float lo = __shfl_xor(l, msk);
-    const float mn = fmaxf(m, mo);
-    const float fa = m == -INFINITY ? 0.f : exp_fast(m - mn);
-    const float fb = mo == -INFINITY ? 0.f : exp_fast(mo - mn);
-    l = l * fa + lo * fb;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = acc[e] * fa + __shfl_xor(acc[e], msk) * fb;
-    m = mn;
-  }
-  if (lane == 0) {
-    wm[w] = m;
-    wl[w] = l;
-  }
-  if (lane < LPR)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) wacc[w][d0 + e] = acc[e];
-  __syncthreads();
-  if (tid < D) {
-    float mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-    float f[4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x) f[x] = wm[x] == -INFINITY ? 0.f : exp_fast(wm[x] - mx);
-    const float tot = (wl[0] * f[0] + wl[1] * f[1]) + (wl[2] * f[2] + wl[3] * f[3]);
-    const float num = (wacc[0][tid] * f[0] + wacc[1][tid] * f[1]) +
-                      (wacc[2][tid] * f[2] + wacc[3][tid] * f[3]);
-    if constexpr (kSplit) {
-      const int64_t idx = (int64_t(b) * Hq + h) * parts + part;
-      accums[idx * D + tid] = num;
-      if (tid == 0) {
-        maxima[idx] = mx;
-        denoms[idx] = tot;
-      }
-    } else {
-      out[(int64_t(b) * Hq + h) * D + tid] = uint16_t(bf16_bits(num / (tot > 0.f ? tot : 1.f)));
-    }
-  }
-}
-
 // ------------------------------------------------------------ m/l/acc merge
 template <int VEC>
 __global__ void __launch_bounds__(64)
@@ -806,7 +738,8 @@ struct PartitionArgs {
   float* lse;
   int* counters;
   uint16_t* out;
-  int Hq, Hkv, G, splits, T;
+  float* maxima;
+  int Hq, Hkv, G, hs, splits, T;
   float scale, c;
 };
 
@@ -826,13 +759,13 @@ void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a
 #undef PD_LAUNCH_TILE
 }
 
-template <int D, bool kFused>
+template <int D, bool kFused, int kMode = kMatched>
 void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_GP(GPV)                                                                     \
-  hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused>), grid, dim3(kThreads), 0,     \
-                     stream, a.q, a.qsb, a.qsh, a.k, a.v, a.table, a.tsb, a.width,          \
-                     a.lengths, a.partials, a.lse, a.counters, a.out, a.Hq, a.Hkv, a.G,       \
-                     a.splits, a.T, a.scale, a.c)
+  hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused, kMode>), grid, dim3(kThreads),  \
+                     0, stream, a.q, a.qsb, a.qsh, a.k, a.v, a.table, a.tsb, a.width,       \
+                     a.lengths, a.partials, a.lse, a.counters, a.out, a.maxima, a.Hq, a.Hkv, \
+                     a.G, a.hs, a.splits, a.T, a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_GP(1); break;
     case 2: PD_LAUNCH_GP(2); break;
@@ -881,7 +814,8 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
     return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
   PartitionArgs a{static_cast<const uint16_t*>(q), qsb, qsh, static_cast<const uint16_t*>(k),
                   static_cast<const uint16_t*>(v), table, tsb, width, lengths, partials, lse,
-                  counters, static_cast<uint16_t*>(out), num_heads, num_kv_heads, G, splits,
+                  counters, static_cast<uint16_t*>(out), nullptr, num_heads, num_kv_heads, G, 1,
+                  splits,
                   tokens_per_split, float(scale),
                   float(scale * 1.4426950408889634)};  // SCALE_LOG2 (matched_splitkv.py:363)
   const dim3 grid(splits, num_kv_heads, batch);
@@ -970,7 +904,9 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
 
 namespace {
 
-template <bool kSplit>
+// pd_base and pd_split_fixed: the partition kernel in its base / fixed-split
+// protocol, one workgroup per (partition, kv head [, 16-head slice], sequence).
+template <bool kSplitMode>
 int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
                   const int32_t* table, int64_t tsb, int32_t width, const int32_t* lengths,
                   void* out,
@@ -981,13 +917,15 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
                          num_kv_heads, head_dim))
     return st;
   if (!std::isfinite(scale)) return pd::fail(PD_EINVAL, "scale must be finite");
-  if (batch > 65535 || num_heads > 65535)
+  const int G = num_heads / num_kv_heads;
+  const int hs = (G + 15) / 16;
+  if (batch > 65535 || int64_t(num_kv_heads) * hs > 65535)
     return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
-  if (kSplit) {
+  const int tile = 16384 / head_dim;
+  if (kSplitMode) {
     if (parts < 1) return pd::fail(PD_EINVAL, "partitions must be positive");
-    if (part_size <= 0 || part_size % (16384 / head_dim))
-      return pd::fail(PD_EINVAL, "partition_size must be a positive multiple of %d",
-                      16384 / head_dim);
+    if (part_size <= 0 || part_size % tile)
+      return pd::fail(PD_EINVAL, "partition_size must be a positive multiple of %d", tile);
     if (int64_t(parts) * part_size >= (int64_t(1) << 31))
       return pd::fail(PD_EINVAL, "partitions * partition_size must stay below 2^31");
     if (!maxima || !denoms || !accums)
@@ -995,24 +933,22 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   } else if (!out) {
     return pd::fail(PD_EINVAL, "invalid output buffer");
   }
-  const int G = num_heads / num_kv_heads;
-  const dim3 grid(kSplit ? parts : 1, num_heads, batch);
+  // The base protocol is one partition as long as the table: lengths never
+  // exceed width * 256 (the contract of the live table width).
+  const int T = kSplitMode ? part_size : width * 256;
+  PartitionArgs a{static_cast<const uint16_t*>(q), qsb, qsh, static_cast<const uint16_t*>(k),
+                  static_cast<const uint16_t*>(v), table, tsb, width, lengths, accums, denoms,
+                  nullptr, static_cast<uint16_t*>(out), maxima, num_heads, num_kv_heads, G, hs,
+                  kSplitMode ? parts : 1, T, float(scale), float(scale * 1.4426950408889634)};
+  const dim3 grid(kSplitMode ? parts : 1, num_kv_heads * hs, batch);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const auto* qq = static_cast<const uint16_t*>(q);
-  const auto* kk = static_cast<const uint16_t*>(k);
-  const auto* vv = static_cast<const uint16_t*>(v);
-  auto* o = static_cast<uint16_t*>(out);
-  const float s32 = float(scale);
-#define PD_LAUNCH_ONLINE(DV)                                                                  \
-  hipLaunchKernelGGL((online_decode_kernel<DV, kSplit>), grid, dim3(kThreads), 0, st, qq, qsb, \
-                     qsh, kk, vv, table, tsb, width, lengths, o, maxima, denoms, accums,      \
-                     num_heads, num_kv_heads, G, parts, part_size, s32)
+  const int gp = padded_group(G < 16 ? G : 16);
+  constexpr int kMode = kSplitMode ? kSplit : kBase;
   switch (head_dim) {
-    case 64: PD_LAUNCH_ONLINE(64); break;
-    case 128: PD_LAUNCH_ONLINE(128); break;
-    default: PD_LAUNCH_ONLINE(256); break;
+    case 64: launch_partition_d<64, false, kMode>(gp, grid, st, a); break;
+    case 128: launch_partition_d<128, false, kMode>(gp, grid, st, a); break;
+    default: launch_partition_d<256, false, kMode>(gp, grid, st, a); break;
   }
-#undef PD_LAUNCH_ONLINE
   return launch_status(what);
 }
 
