@@ -150,3 +150,22 @@ def test_context_beyond_the_prefetched_table_window(backend):
     assert_close_dense(actual, torch_dense(*g))
     assert_within_one_ulp(actual, oracle_for(case, backend, spec))
 
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+@pytest.mark.parametrize("dim,hq,hkv", [(128, 32, 1), (64, 24, 1), (256, 40, 2), (128, 17, 1)])
+def test_groups_larger_than_16_heads(backend, dim, hq, hkv):
+    """A kv head with more than 16 query heads is served in 16-head slices (the reference
+    grid has no group limit for these backends)."""
+    lengths = [0, 1, 300, 1100]
+    q, k, v, table, lens = make_case(lengths, hq, hkv, dim, seed=23, capacity=1100)
+    poison_tails(k, v, table, lens)
+    case = (q, k, v, table, lens)
+    g = to_gpu(case)
+    spec = DecodeSpec(len(lengths), hq, hkv, dim, 1100)
+    res = allocate_resources(spec, "cuda", backend)
+    actual = paged_decode(*g, resources=res, backend=backend).clone()
+    torch.cuda.synchronize()
+    assert_close_dense(actual, torch_dense(*g))
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec), f"{backend} G={hq // hkv}")
+    assert torch.count_nonzero(actual[0]) == 0
