@@ -167,11 +167,11 @@ struct MergeBatch {
   static constexpr int value = E == 1 ? 64 : (E == 2 ? 48 : (E == 4 ? 40 : (E == 8 ? 16 : 8)));
 };
 
-template <int E, bool kCoherent, typename PrepareFn, typename WeightFn>
+template <int E, bool kCoherent, int kBatch = MergeBatch<E>::value, typename PrepareFn,
+          typename WeightFn>
 __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int D, int dd,
                                              int splits, PrepareFn prepare, WeightFn weight,
                                              float (&acc)[E]) {
-  constexpr int kBatch = MergeBatch<E>::value;
   // `row` must be wavefront-uniform: the resource lives in scalar registers.
   const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(row, splits * D * 4);
 #pragma unroll

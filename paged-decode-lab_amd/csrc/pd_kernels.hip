@@ -648,7 +648,9 @@ matched_tile_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
 // Every wavefront computes the row's weights itself (the same arithmetic, so
 // the same bits in every chunk) and broadcasts them with readlane: no LDS, no
 // barrier.
-template <int D>
+// kBatch: splits loaded per straight-line batch; 128 (one memory round trip
+// for any split count) when there are more than 64 splits, else 64.
+template <int D, int kBatch>
 __global__ void __launch_bounds__(64)
 lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ lse,
                  uint16_t* __restrict__ out, int splits) {
@@ -656,7 +658,7 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
   const int lane = threadIdx.x;
   const int dd = blockIdx.y * 64 + lane;
   float w0 = 0.f, w1 = 0.f, acc[1];
-  merge_splits<1, false>(
+  merge_splits<1, false, kBatch>(
       partials + row * splits * D, D, dd, splits,
       [&] { lse_weights<false>(lse + row * splits, splits, lane, w0, w1); },
       [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
@@ -888,17 +890,19 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto* o = static_cast<uint16_t*>(out);
   const dim3 grid(unsigned(rows), head_dim / 64);
+#define PD_LAUNCH_MERGE(DV)                                                                    \
+  if (splits > 64)                                                                             \
+    hipLaunchKernelGGL((lse_merge_kernel<DV, 128>), grid, dim3(64), 0, st, partials, lse, o,   \
+                       splits);                                                                \
+  else                                                                                         \
+    hipLaunchKernelGGL((lse_merge_kernel<DV, 64>), grid, dim3(64), 0, st, partials, lse, o,    \
+                       splits)
   switch (head_dim) {
-    case 64:
-      hipLaunchKernelGGL(lse_merge_kernel<64>, grid, dim3(64), 0, st, partials, lse, o, splits);
-      break;
-    case 128:
-      hipLaunchKernelGGL(lse_merge_kernel<128>, grid, dim3(64), 0, st, partials, lse, o, splits);
-      break;
-    default:
-      hipLaunchKernelGGL(lse_merge_kernel<256>, grid, dim3(64), 0, st, partials, lse, o, splits);
-      break;
+    case 64: PD_LAUNCH_MERGE(64); break;
+    case 128: PD_LAUNCH_MERGE(128); break;
+    default: PD_LAUNCH_MERGE(256); break;
   }
+#undef PD_LAUNCH_MERGE
   return launch_status("pd_lse_merge");
 }
 
