@@ -69,13 +69,13 @@ constexpr int kMatched = 0, kBase = 1, kSplit = 2;
 
 template <int D, int GP, bool kFused, int kMode>
 __global__ void __launch_bounds__(kThreads, 2)
-matched_partition_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
-                         const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                         const int32_t* __restrict__ table, int64_t tsb, int width,
-                         const int32_t* __restrict__ lengths, float* __restrict__ partials,
+matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
+                         const uint16_t* __restrict__ q, int tsb, int width, int T, int qsb,
+                         int qsh, int G, int hs, int Hq, const uint16_t* __restrict__ k,
+                         const uint16_t* __restrict__ v, float* __restrict__ partials,
                          float* __restrict__ lse_out, int* __restrict__ counters,
-                         uint16_t* __restrict__ out, float* __restrict__ maxima, int Hq,
-                         int Hkv, int G, int hs, int splits, int T, float scale, float c) {
+                         uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv,
+                         int splits, float scale, float c) {
   static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
   using C = Matched<D, GP>;
   constexpr int TILE = C::kTile;
@@ -481,12 +481,11 @@ struct TileP {
 
 template <int D, int GP>
 __global__ void __launch_bounds__(kThreads, 2)
-matched_tile_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
-                    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                    const int32_t* __restrict__ table, int64_t tsb, int width,
-                    const int32_t* __restrict__ lengths, float* __restrict__ partials,
-                    float* __restrict__ lse_out, int Hq, int Hkv, int G, int splits,
-                    float scale, float c) {
+matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
+                    const uint16_t* __restrict__ q, int tsb, int width, int qsb, int qsh, int G,
+                    int Hq, int splits, const uint16_t* __restrict__ k,
+                    const uint16_t* __restrict__ v, float* __restrict__ partials,
+                    float* __restrict__ lse_out, int Hkv, float scale, float c) {
   using C = Matched<D, GP>;
   using P = TileP<D>;
   constexpr int TILE = C::kTile;
@@ -506,6 +505,10 @@ matched_tile_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
   const int end = min(start + TILE, length);
   const int64_t RS = int64_t(Hkv) * D;
   const int64_t row0 = (int64_t(b) * Hq + kh * G) * splits + p;  // (head 0 of the group, p)
+  // Wait for the table entry here, before the branch on the length: otherwise
+  // the compiler sinks the table load below the branch and the first KV loads
+  // wait for two memory round trips (length, then table) instead of one.
+  pw.settle();
 
   if (end <= start) {
     // Empty split: partial 0 (acc 0 times rcp(1)) and LSE -inf, as the
@@ -535,7 +538,6 @@ matched_tile_kernel(const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh,
                                             : 0x7ffffff0;
   }
 
-  pw.settle();
   KTile<D, GP> R;
   {
     const TileBuffers buf = tile_buffers(k, v, pw.page(start), start, end, RS, kh, D);
@@ -720,6 +722,8 @@ int check_qkv(const void* q, int64_t qsb, int64_t qsh, const void* k, const void
       qsh < 0)
     return pd::fail(PD_EINVAL,
                     "Q/K/V rows must be 16-byte aligned (strides multiples of 8 elements)");
+  if (qsb >= (int64_t(1) << 31) || qsh >= (int64_t(1) << 31))
+    return pd::fail(PD_EINVAL, "Q strides must stay below 2^31 elements");
   if (int64_t(num_kv_heads) * head_dim * 512 >= (int64_t(1) << 31))
     return pd::fail(PD_EINVAL, "a 256-slot page of one KV tensor must stay below 2 GiB");
   if (width < 1 || width >= (1 << 22))
@@ -727,13 +731,17 @@ int check_qkv(const void* q, int64_t qsb, int64_t qsh, const void* k, const void
   return PD_OK;
 }
 
+// Kernel argument order puts what the first memory accesses need (table row,
+// length, query rows) first: those arguments fit the SGPRs the hardware fills
+// before the first instruction (kernarg preloading), so the first loads do
+// not wait for a kernel-argument fetch.  Strides are int32 (checked).
 struct PartitionArgs {
   const uint16_t* q;
-  int64_t qsb, qsh;
+  int qsb, qsh;
   const uint16_t* k;
   const uint16_t* v;
   const int32_t* table;
-  int64_t tsb;
+  int tsb;
   int width;
   const int32_t* lengths;
   float* partials;
@@ -748,9 +756,9 @@ struct PartitionArgs {
 template <int D>
 void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_TILE(GPV)                                                                   \
-  hipLaunchKernelGGL((matched_tile_kernel<D, GPV>), grid, dim3(kThreads), 0, stream, a.q,     \
-                     a.qsb, a.qsh, a.k, a.v, a.table, a.tsb, a.width, a.lengths, a.partials,  \
-                     a.lse, a.Hq, a.Hkv, a.G, a.splits, a.scale, a.c)
+  hipLaunchKernelGGL((matched_tile_kernel<D, GPV>), grid, dim3(kThreads), 0, stream, a.table, \
+                     a.lengths, a.q, a.tsb, a.width, a.qsb, a.qsh, a.G, a.Hq, a.splits, a.k,  \
+                     a.v, a.partials, a.lse, a.Hkv, a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_TILE(1); break;
     case 2: PD_LAUNCH_TILE(2); break;
@@ -765,9 +773,9 @@ template <int D, bool kFused, int kMode = kMatched>
 void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_GP(GPV)                                                                     \
   hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused, kMode>), grid, dim3(kThreads),  \
-                     0, stream, a.q, a.qsb, a.qsh, a.k, a.v, a.table, a.tsb, a.width,       \
-                     a.lengths, a.partials, a.lse, a.counters, a.out, a.maxima, a.Hq, a.Hkv, \
-                     a.G, a.hs, a.splits, a.T, a.scale, a.c)
+                     0, stream, a.table, a.lengths, a.q, a.tsb, a.width, a.T, a.qsb, a.qsh,  \
+                     a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,        \
+                     a.maxima, a.Hkv, a.splits, a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_GP(1); break;
     case 2: PD_LAUNCH_GP(2); break;
@@ -814,8 +822,11 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
     return pd::fail(PD_EINVAL, "positive finite scale required");
   if (batch > 65535 || num_kv_heads > 65535)
     return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
-  PartitionArgs a{static_cast<const uint16_t*>(q), qsb, qsh, static_cast<const uint16_t*>(k),
-                  static_cast<const uint16_t*>(v), table, tsb, width, lengths, partials, lse,
+  if (tsb < 0 || tsb >= (int64_t(1) << 31))
+    return pd::fail(PD_EINVAL, "block table row stride must be in [0, 2^31)");
+  PartitionArgs a{static_cast<const uint16_t*>(q), int(qsb), int(qsh),
+                  static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), table,
+                  int(tsb), width, lengths, partials, lse,
                   counters, static_cast<uint16_t*>(out), nullptr, num_heads, num_kv_heads, G, 1,
                   splits,
                   tokens_per_split, float(scale),
@@ -940,8 +951,11 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   // The base protocol is one partition as long as the table: lengths never
   // exceed width * 256 (the contract of the live table width).
   const int T = kSplitMode ? part_size : width * 256;
-  PartitionArgs a{static_cast<const uint16_t*>(q), qsb, qsh, static_cast<const uint16_t*>(k),
-                  static_cast<const uint16_t*>(v), table, tsb, width, lengths, accums, denoms,
+  if (tsb < 0 || tsb >= (int64_t(1) << 31))
+    return pd::fail(PD_EINVAL, "block table row stride must be in [0, 2^31)");
+  PartitionArgs a{static_cast<const uint16_t*>(q), int(qsb), int(qsh),
+                  static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), table,
+                  int(tsb), width, lengths, accums, denoms,
                   nullptr, static_cast<uint16_t*>(out), maxima, num_heads, num_kv_heads, G, hs,
                   kSplitMode ? parts : 1, T, float(scale), float(scale * 1.4426950408889634)};
   const dim3 grid(kSplitMode ? parts : 1, num_kv_heads * hs, batch);
