@@ -40,12 +40,6 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 __device__ __forceinline__ float ln_fast(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
 __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// a.lo*b.lo + a.hi*b.hi + c over bf16 pairs (v_dot2_f32_bf16).
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
