@@ -45,3 +45,44 @@ def torch_dense(q, k, v, tables, lengths, scale=None):
 def assert_close_dense(actual, expected):
     assert torch.isfinite(actual).all()
     torch.testing.assert_close(actual.float(), expected.float(), atol=2e-2, rtol=2e-2)
+
+
+def pooled_case(lengths, hq, hkv, dim, capacity, pool_pages, seed, device="cuda"):
+    """Device inputs at full benchmark size: each sequence's pages are drawn without
+    replacement from a pool of ``pool_pages`` physical pages per cache, in random
+    order.  Only live pages get N(0, 1) bf16 values; the rest of the pool holds NaN, so
+    a read outside the live tokens poisons the output.  Table entries past a row's live
+    pages are -1."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    width = (capacity + 255) // 256
+    live = [(int(n) + 255) // 256 for n in lengths]
+    physical = torch.randperm(pool_pages, device=device, generator=gen)[: sum(live)]
+    table = torch.full((len(lengths), width), -1, dtype=torch.int32, device=device)
+    offset = 0
+    for b, n in enumerate(live):
+        table[b, :n] = physical[offset:offset + n].to(torch.int32)
+        offset += n
+    k = torch.full((pool_pages, 256, hkv, dim), float("nan"), dtype=torch.bfloat16, device=device)
+    v = torch.full_like(k, float("nan"))
+    for chunk in torch.split(physical.long(), 512):
+        k[chunk] = torch.randn((len(chunk), 256, hkv, dim), generator=gen, device=device,
+                               dtype=torch.bfloat16)
+        v[chunk] = torch.randn((len(chunk), 256, hkv, dim), generator=gen, device=device,
+                               dtype=torch.bfloat16)
+    q = torch.randn((len(lengths), hq, dim), generator=gen, device=device, dtype=torch.bfloat16)
+    lens = torch.tensor([int(n) for n in lengths], dtype=torch.int32, device=device)
+    return q, k, v, table, lens
+
+
+def host_rows(q, k, v, table, lengths, rows):
+    """The sequences ``rows`` of a device case as a compact NumPy case for the oracle:
+    their live pages copied to the host and renumbered, the table -1 padded."""
+    lens = lengths[rows].cpu().numpy().astype(np.int32)
+    live = [(int(n) + 255) // 256 for n in lens]
+    pages = torch.cat([table[r, :n] for r, n in zip(rows, live)]).long()
+    compact = np.full((len(rows), table.shape[1]), -1, dtype=np.int32)
+    offset = 0
+    for i, n in enumerate(live):
+        compact[i, :n] = np.arange(offset, offset + n)
+        offset += n
+    return (to_np(q[rows]), to_np(k[pages]), to_np(v[pages]), compact, lens)
