@@ -239,12 +239,74 @@ struct KTile {
   u32x4_t k[Matched<D, GP>::kNG][Matched<D, GP>::kCH];
 };
 
+// K rows are fetched as whole 128-byte lines and rearranged into the MFMA
+// A-operand layout in registers.  A load in the operand layout itself (lane
+// 16g + r: row r, 16 bytes at 16g of a 64-byte piece) covers 16 rows x 64
+// bytes, half lines whose consecutive lanes address different rows, and one
+// CU streams such loads at about half the rate of loads whose eight
+// consecutive lanes cover one line (38 vs 72 GB/s per CU, measured on
+// MI355X).  So load (h, sh) of a 16-row group gives lane S row 8sh + S/8,
+// 16-byte chunk S%8 of line h (kline_offset), and lines_to_mfma turns the
+// pair sh = 0, 1 into the operand registers of chunks 8h + g and 8h + 4 + g
+// of row r at lane 16g + r, the layout QK's MFMA and the query rows use:
+//   u = load 0 on lanes S%8 < 4, load 1 from lane S - 4 on lanes S%8 >= 4;
+//   v = load 0 from lane S + 4 on lanes S%8 < 4, load 1 on lanes S%8 >= 4
+// (bank-masked DPP moves within 16-lane rows: banks 1 and 3 are the lanes
+// S%8 >= 4), then one ds_bpermute per dword fetches lane 16g + r's value from
+// lane 8r + g (r < 8) or 8(r - 8) + g + 4 (r >= 8) of u and of v.
+// The single-tile kernel loads its one tile this way (all of it in flight at
+// once, so the load rate is what counts).  The multi-tile loop keeps loads in
+// the operand layout: there the rearrangement lengthens every tile's chain
+// and one streaming workgroup slowed from 57 to 41 GB/s.
+__device__ __forceinline__ int kline_offset(int lane, int RS) {
+  return ((lane >> 3) * RS + 8 * (lane & 7)) * 2;
+}
+__device__ __forceinline__ int kline_source(int lane) {
+  const int r = lane & 15, g = lane >> 4;
+  return 4 * (r < 8 ? 8 * r + g : 8 * (r - 8) + g + 4);
+}
+__device__ __forceinline__ void lines_to_mfma(u32x4_t& a, u32x4_t& b, int src) {
+  u32x4_t ra, rb;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int u = __builtin_amdgcn_update_dpp(int(a[e]), int(b[e]), 0x114, 0xf, 0xa, false);
+    const int v = __builtin_amdgcn_update_dpp(int(b[e]), int(a[e]), 0x104, 0xf, 0x5, false);
+    ra[e] = unsigned(__builtin_amdgcn_ds_bpermute(src, u));
+    rb[e] = unsigned(__builtin_amdgcn_ds_bpermute(src, v));
+  }
+  a = ra;
+  b = rb;
+}
+
+template <int D, int GP>
+__device__ __forceinline__ void ktile_to_mfma(KTile<D, GP>& R, int src) {
+#pragma unroll
+  for (int g = 0; g < Matched<D, GP>::kNG; ++g)
+#pragma unroll
+    for (int h = 0; h < Matched<D, GP>::kCH / 2; ++h) lines_to_mfma(R.k[g][2 * h], R.k[g][2 * h + 1], src);
+}
+
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // 16 bytes at byte offset `off` of a buffer (zero past its end).
 __device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int off) {
   const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
   return t;
+}
+
+// The K rows of a wavefront's share of a tile, as whole-line loads (rows
+// 16g + 8sh + S/8 from `kl`, the lane's kline_offset from the share's first
+// row); ktile_to_mfma then rearranges them for QK.
+template <int D, int GP>
+__device__ __forceinline__ void ktile_load(KTile<D, GP>& R, __amdgpu_buffer_rsrc_t rsrc, int kl,
+                                           int RS) {
+#pragma unroll
+  for (int g = 0; g < Matched<D, GP>::kNG; ++g)
+#pragma unroll
+    for (int h = 0; h < Matched<D, GP>::kCH / 2; ++h) {
+      R.k[g][2 * h] = buffer_load16(rsrc, kl + (32 * g) * RS + 128 * h);
+      R.k[g][2 * h + 1] = buffer_load16(rsrc, kl + (32 * g + 16) * RS + 128 * h);
+    }
 }
 
 // Four bf16 of one column, transposed out of LDS (see above).  `p` points

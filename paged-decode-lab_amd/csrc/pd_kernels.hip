@@ -528,7 +528,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     for (int ch = 0; ch < C::kCH; ++ch)
       qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
   }
-  const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
+  const int kl = kline_offset(lane, int(RS)) + w * C::kTW * int(RS) * 2;
   int voff[C::kDma];
 #pragma unroll
   for (int i = 0; i < C::kDma; ++i) {
@@ -541,14 +541,14 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   KTile<D, GP> R;
   {
     const TileBuffers buf = tile_buffers(k, v, pw.page(start), start, end, RS, kh, D);
-#pragma unroll
-    for (int g = 0; g < C::kNG; ++g)
-#pragma unroll
-      for (int ch = 0; ch < C::kCH; ++ch)
-        R.k[g][ch] = buffer_load16(buf.k, koff + g * 16 * int(RS) * 2 + 64 * ch);
+    ktile_load(R, buf.k, kl, int(RS));
 #pragma unroll
     for (int i = 0; i < C::kDma; ++i) lds_copy16(buf.v, vs + w * C::kSlot + 1024 * i, voff[i]);
   }
+  // Every K and V load of the tile is issued before the K rearrangement, which
+  // waits for K.
+  __builtin_amdgcn_sched_barrier(0);
+  ktile_to_mfma(R, kline_source(lane));
 
   // ---- scores of this wavefront's tokens, tile maximum per head
   const int nvalid = end - start;
