@@ -244,9 +244,10 @@ def context_sweep(torch, contexts=(8192, 32768, 131072)):
     out = {}
     for ctx in contexts:
         case = matched_case(torch, 1, 16, 4, 256, ctx, [ctx], 11)
-        calls = max(32, min(512, 4 * 131072 // ctx))
-        us = graph_time_us(torch, case["full"], calls, unroll=16)
-        part_us = graph_time_us(torch, case["partition"], calls, unroll=16)
+        # 128 unrolled calls per graph, as for the headline: a graph replay carries a
+        # launch cost of its own that a short unroll would spread over too few calls.
+        us = graph_time_us(torch, case["full"], 256, unroll=128)
+        part_us = graph_time_us(torch, case["partition"], 256, unroll=128)
         nbytes = algorithmic_bytes([ctx], 1, 16, 4, 256)
         pbytes = algorithmic_bytes([ctx], 1, 16, 4, 256, with_output=False)
         p = case["plan"]
@@ -261,11 +262,11 @@ def context_sweep(torch, contexts=(8192, 32768, 131072)):
 
 
 def paged_backend_rates(torch, seed=64):
-    """paged_decode backends hip_base (one workgroup per sequence x query head) and
+    """paged_decode backends hip_base (the whole context per sequence and kv head) and
     hip_splitk (fixed 1024-token partitions + m/l/acc merge) on the bandwidth-sweep
     shape and on the edge-coverage shapes (B=128, a quarter of the lengths 0, the rest
-    U[1,4096]).  Both read each sequence's K/V once per query head, as the reference's
-    grids do, so their HBM traffic is G times the algorithmic bytes counted here."""
+    U[1,4096]).  Both run one workgroup per kv head for its whole GQA group (16-head
+    slices above 16), so K/V is read once per kv head, as the algorithmic bytes count."""
     import numpy as np
     from paged_decode.runtime import allocate_resources, paged_decode
     from paged_decode.spec import DecodeSpec
