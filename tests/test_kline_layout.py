@@ -1,0 +1,76 @@
+"""Lane arithmetic of the single-tile kernel's whole-line K loads, on the CPU.
+
+pd_device.h loads each 16-row group of K as whole 128-byte lines (kline_offset:
+lane S gets row 8sh + S/8, 16-byte chunk S%8 of line h), then lines_to_mfma
+turns each pair of loads into the MFMA A-operand registers with two bank-masked
+DPP moves (row_shr:4 on banks 1 and 3, row_shl:4 on banks 0 and 2 of every
+16-lane row) and one ds_bpermute per dword from lane kline_source(L).  This test
+runs the same index arithmetic on NumPy lanes and checks the result against the
+operand layout the QK MFMA reads (lane 16g + r: row r, chunk 4ch + g), for every
+head dim.  On the GPU the kernel's outputs are bit-identical to loads made
+directly in the operand layout (tests/test_gpu_matched.py and the paged tests).
+"""
+import numpy as np
+import pytest
+
+LANES = np.arange(64)
+
+
+def dpp_row_shift(old, src, shift, bank_mask):
+    """update_dpp(old, src, row_shr:shift (shift > 0) or row_shl:-shift, row_mask 0xf,
+    bank_mask): lanes of the enabled banks (4-lane groups of each 16-lane row) read src
+    from lane - shift within their row; the others keep old."""
+    out = old.copy()
+    for lane in LANES:
+        bank = (lane & 15) >> 2
+        if not (bank_mask >> bank) & 1:
+            continue
+        src_lane = lane - shift
+        assert (src_lane >> 4) == (lane >> 4), "source outside the 16-lane row"
+        out[lane] = src[src_lane]
+    return out
+
+
+def kline_source(lane):
+    r, g = lane & 15, lane >> 4
+    return 4 * (8 * r + g if r < 8 else 8 * (r - 8) + g + 4)
+
+
+def bpermute(src, byte_index):
+    return src[byte_index // 4]
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_whole_line_loads_rearrange_into_the_operand_layout(dim):
+    chunks = dim // 8                      # 16-byte chunks per K row
+    # K rows of one 16-row group; each chunk is labelled (row, chunk)
+    label = lambda row, chunk: 1000 * row + chunk
+    lines = chunks // 8                    # 128-byte lines per row
+    regs = {}
+    for h in range(lines):
+        for sh in range(2):                # kline_offset + 128 h, rows + 8 sh
+            regs[(h, sh)] = np.array([label(8 * sh + s // 8, 8 * h + s % 8) for s in LANES])
+    idx = np.array([kline_source(int(lane)) for lane in LANES])
+    for h in range(lines):
+        a, b = regs[(h, 0)], regs[(h, 1)]
+        u = dpp_row_shift(a, b, 4, 0xA)
+        v = dpp_row_shift(b, a, -4, 0x5)
+        got = {2 * h: bpermute(u, idx), 2 * h + 1: bpermute(v, idx)}
+        for ch, reg in got.items():
+            want = np.array([label(lane & 15, 4 * ch + (lane >> 4)) for lane in LANES])
+            np.testing.assert_array_equal(reg, want)
+
+
+def test_operand_layout_loads_touch_half_lines_and_whole_line_loads_whole_ones():
+    """What the rearrangement is for: a load in the operand layout covers 64 bytes of
+    each of 16 rows (no 8 consecutive lanes share a line), a whole-line load covers 8
+    full lines with 8 consecutive lanes each."""
+    row_bytes = 512
+    operand = [(lane & 15) * row_bytes + 16 * (lane >> 4) for lane in LANES]
+    whole = [(lane // 8) * row_bytes + 16 * (lane % 8) for lane in LANES]
+    line_of = lambda addr: addr // 128
+    assert len({line_of(a) for a in operand}) == 16
+    assert len({line_of(a) for a in whole}) == 8
+    for start in range(0, 64, 8):
+        assert len({line_of(a) for a in whole[start:start + 8]}) == 1
+        assert len({line_of(a) for a in operand[start:start + 8]}) == 8
