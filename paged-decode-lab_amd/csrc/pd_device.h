@@ -208,8 +208,8 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
 //
 // PV on MFMA, with the bf16 probabilities as the A operand taken directly from
 // the QK result registers: lane L holds P[head L%16][tokens 4*(L/16) + r] of
-// each 16-token group, the A layout of v_mfma_f32_16x16x16_bf16 for one group
-// and, for two groups g, g+1 side by side, of v_mfma_f32_16x16x32_bf16
+// each 16-token group, which for two groups g, g+1 side by side is the A
+// layout of v_mfma_f32_16x16x32_bf16
 // (k = 8*(L/16) + e <-> token 16g + 4*(L/16) + e for e < 4, 16(g+1) +
 // 4*(L/16) + e-4 above).  The B operand needs V columns (4 consecutive tokens
 // of one d per lane).  V rows therefore go to LDS by buffer_load ... lds (no
@@ -315,6 +315,34 @@ __device__ __forceinline__ void ktile_load(KTile<D, GP>& R, __amdgpu_buffer_rsrc
 __device__ __forceinline__ short4_t lds_read_tr(const char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) short4_t*)(const_cast<char*>(p)));
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const char*)(p)));
+}
+
+// ds_read_b64_tr_b16 at LDS byte address base + OFF, issued from inline asm.
+// The compiler does not see an LDS read, so it neither adds waits for LDS
+// copies (buffer_load ... lds) into the same array nor waits for the result:
+// the caller orders the read after the copies it needs and passes the results
+// through lds_settle before using them.
+template <int OFF>
+__device__ __forceinline__ short4_t lds_read_tr_at(uint32_t base) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  short4_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
+  return r;
+}
+
+// Waits for every outstanding LDS read (lgkmcnt(0)) and makes the values
+// depend on that wait, so no use of them is scheduled before it.
+template <int N>
+__device__ __forceinline__ void lds_settle(short4_t (&a)[N], short4_t (&b)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(a[i]), "+v"(b[i]));
 }
 
 // Copies 16 bytes at byte offset `off` of a buffer into LDS: lane l of the

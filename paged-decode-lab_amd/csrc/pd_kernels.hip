@@ -10,6 +10,10 @@
 //                      lds.  Three protocols: matched (bf16 p, normalized FP32
 //                      partial + LSE), base (FP32 p, whole context, bf16 out)
 //                      and fixed split (FP32 p, (m, l, acc) per partition).
+//                      D = 64 and 128.
+//   matched_cols       the same three protocols at D = 256, with PV split
+//                      across the wavefronts by output columns (P through LDS)
+//                      and K loaded two tiles ahead.
 //   matched_tile       the matched protocol for splits of exactly one tile,
 //                      with PV split across the wavefronts by output columns.
 //   lse_merge          one wavefront per (sequence, query head, 64 columns):
@@ -24,6 +28,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 #include "pd_device.h"
 #include "pd_internal.h"
@@ -77,6 +82,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
                          uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv,
                          int splits, float scale, float c) {
   static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
+  static_assert(D < 256, "D = 256 runs matched_cols_kernel");
   using C = Matched<D, GP>;
   constexpr int TILE = C::kTile;
   __shared__ MatchedShared<D, GP> sm;
@@ -257,31 +263,21 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
         for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
     }
     const char* base = slot + trb;
-    if constexpr (C::kNG == 1) {
+    static_assert(C::kNG % 2 == 0, "16-token groups in pairs");
+#pragma unroll
+    for (int g = 0; g < C::kNG; g += 2) {
 #pragma unroll
       for (int j = 0; j < C::kNB; ++j) {
-        const short4_t bv = lds_read_tr(base + 32 * j);
+        const short4_t lo = lds_read_tr(base + 16 * g * C::kPitch + 32 * j);
+        const short4_t hi = lds_read_tr(base + 16 * (g + 1) * C::kPitch + 32 * j);
+        const bf16x8_t bv = __builtin_bit_cast(
+            bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo)[0], __builtin_bit_cast(u32x2_t, lo)[1],
+                              __builtin_bit_cast(u32x2_t, hi)[0], __builtin_bit_cast(u32x2_t, hi)[1]});
 #pragma unroll
-        for (int t = 0; t < kTerms; ++t)
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-              __builtin_bit_cast(short4_t, u32x2_t{pb[t][0][0], pb[t][0][1]}), bv, acc[j], 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int g = 0; g < C::kNG; g += 2) {
-#pragma unroll
-        for (int j = 0; j < C::kNB; ++j) {
-          const short4_t lo = lds_read_tr(base + 16 * g * C::kPitch + 32 * j);
-          const short4_t hi = lds_read_tr(base + 16 * (g + 1) * C::kPitch + 32 * j);
-          const bf16x8_t bv = __builtin_bit_cast(
-              bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo)[0], __builtin_bit_cast(u32x2_t, lo)[1],
-                                __builtin_bit_cast(u32x2_t, hi)[0], __builtin_bit_cast(u32x2_t, hi)[1]});
-#pragma unroll
-          for (int t = 0; t < kTerms; ++t) {
-            const bf16x8_t a = __builtin_bit_cast(
-                bf16x8_t, u32x4_t{pb[t][g][0], pb[t][g][1], pb[t][g + 1][0], pb[t][g + 1][1]});
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
-          }
+        for (int t = 0; t < kTerms; ++t) {
+          const bf16x8_t a = __builtin_bit_cast(
+              bf16x8_t, u32x4_t{pb[t][g][0], pb[t][g][1], pb[t][g + 1][0], pb[t][g + 1][1]});
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
         }
       }
     }
@@ -289,71 +285,42 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
 
   // Reverse tile walk (matched_splitkv.py:71): last tile first.  Two register
   // sets and two LDS slots alternate.  V rows are loaded one tile ahead, into
-  // the LDS slot the previous tile's PV has finished reading.  Below D = 256
-  // the K rows are loaded two tiles ahead, into the register set whose QK
-  // products have just been issued (kFar); at D = 256 two live K sets do not
-  // fit the 256-VGPR budget of two waves per SIMD, so K is loaded one tile
-  // ahead, with the V rows.  The loop handles tiles in pairs and the last ones
-  // are peeled, so no load is issued past tile 0 (an issue takes the CU's load
-  // path for as long as a real one).
-  constexpr bool kFar = D < 256;
+  // the LDS slot the previous tile's PV has finished reading; K rows two tiles
+  // ahead, into the register set whose QK products have just been issued.
+  // The loop handles tiles in pairs and the last ones are peeled, so no load
+  // is issued past tile 0 (an issue takes the CU's load path for as long as a
+  // real one).
   pw.settle();
-  if constexpr (kFar) {
-    if (count == 1) {
-      KTile<D, GP> A;
-      issue_k(A, 0);
-      issue_v(vs0, 0);
-      process(A, vs0, 0, true, -1);
-    } else if (count > 1) {
-      KTile<D, GP> A, B;
-      int ti = count - 1;
-      issue_k(A, ti);
-      issue_v(vs0, ti);
-      issue_k(B, ti - 1);
-      bool first = true;
-      while (ti >= 3) {
-        issue_v(vs1, ti - 1);
-        process(A, vs0, ti, first, ti - 2);
-        issue_v(vs0, ti - 2);
-        process(B, vs1, ti - 1, false, ti - 3);
-        ti -= 2;
-        first = false;
-      }
-      if (ti == 2) {
-        issue_v(vs1, 1);
-        process(A, vs0, 2, first, 0);
-        issue_v(vs0, 0);
-        process(B, vs1, 1, false, -1);
-        process(A, vs0, 0, false, -1);
-      } else {  // ti == 1
-        issue_v(vs1, 0);
-        process(A, vs0, 1, first, -1);
-        process(B, vs1, 0, false, -1);
-      }
-    }
-  } else if (count > 0) {
+  if (count == 1) {
+    KTile<D, GP> A;
+    issue_k(A, 0);
+    issue_v(vs0, 0);
+    process(A, vs0, 0, true, -1);
+  } else if (count > 1) {
     KTile<D, GP> A, B;
     int ti = count - 1;
     issue_k(A, ti);
     issue_v(vs0, ti);
+    issue_k(B, ti - 1);
     bool first = true;
-    while (ti >= 2) {
-      issue_k(B, ti - 1);
+    while (ti >= 3) {
       issue_v(vs1, ti - 1);
-      process(A, vs0, ti, first, -1);
-      issue_k(A, ti - 2);
+      process(A, vs0, ti, first, ti - 2);
       issue_v(vs0, ti - 2);
-      process(B, vs1, ti - 1, false, -1);
+      process(B, vs1, ti - 1, false, ti - 3);
       ti -= 2;
       first = false;
     }
-    if (ti == 1) {
-      issue_k(B, 0);
+    if (ti == 2) {
+      issue_v(vs1, 1);
+      process(A, vs0, 2, first, 0);
+      issue_v(vs0, 0);
+      process(B, vs1, 1, false, -1);
+      process(A, vs0, 0, false, -1);
+    } else {  // ti == 1
       issue_v(vs1, 0);
       process(A, vs0, 1, first, -1);
       process(B, vs1, 0, false, -1);
-    } else {
-      process(A, vs0, 0, first, -1);
     }
   }
 
@@ -455,6 +422,369 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   }
 }
 
+template <int D>
+struct TileP {
+  static constexpr int kTile = 16384 / D;
+  // Bytes per head row of P: 8 bytes of padding put the 16 rows of a
+  // ds_write_b64 / ds_read_b64 in different banks (row r starts at bank 2r).
+  static constexpr int kPitch = 2 * kTile + 8;
+  static constexpr int kCols = D / 4;        // output columns per wavefront
+  static constexpr int kNBW = kCols / 16;    // 16-column blocks per wavefront
+  static constexpr int kKS = kTile / 32;     // 32-token k-steps of PV
+};
+
+// ------------------------------------------- D = 256: P V split by columns
+// The partition for D = 256, the same three protocols as
+// matched_partition_kernel and the same scores, maxima, probabilities and
+// denominators (so the same LSEs), with the P V product split by output
+// columns as in matched_tile_kernel: per tile, every wavefront writes its bf16
+// probabilities (three bf16 terms for the base and fixed-split protocols) to
+// LDS, and wavefront w multiplies the whole tile's P by V columns
+// [64w, 64w + 64).  The accumulator then takes 16 VGPRs instead of 64, which
+// leaves room for a second K register set: K rows are loaded two tiles ahead
+// (refilled into the set whose QK products were just issued), as below
+// D = 256.  There is no cross-wave reduction of O at the end.
+//
+// Every wavefront reads every wavefront's V rows, so the V rows of tile ti - 1
+// are copied into the LDS slot of tile ti + 1 only after the first barrier of
+// tile ti (every wavefront has finished P V of tile ti + 1 by then), and P V
+// of tile ti starts after a second barrier, once each wavefront has waited for
+// its own copies of tile ti.  The K rows of tile ti - 2 are loaded right after
+// the V rows of tile ti - 1, so that wait never covers the K rows loaded two
+// tiles ahead: after the V rows of tile ti come the K rows of tile ti - 1 and
+// the V rows of tile ti - 1 and K rows of tile ti - 2 (8 + 9 + 8 loads per
+// wavefront), hence vmcnt(25) before that barrier.
+template <int GP, bool kFused, int kMode>
+__global__ void __launch_bounds__(kThreads, 2)
+matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
+                    const uint16_t* __restrict__ q, int tsb, int width, int T, int qsb, int qsh,
+                    int G, int hs, int Hq, const uint16_t* __restrict__ k,
+                    const uint16_t* __restrict__ v, float* __restrict__ partials,
+                    float* __restrict__ lse_out, int* __restrict__ counters,
+                    uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv, int splits,
+                    float scale, float c) {
+  static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
+  constexpr int D = 256;
+  using C = Matched<D, GP>;
+  using P = TileP<D>;
+  constexpr int TILE = C::kTile;
+  constexpr int kTerms = kMode == kMatched ? 1 : 3;
+  static_assert(C::kNG == 1 && C::kTW == 16 && P::kKS == 2, "D = 256 geometry");
+  __shared__ MatchedShared<D, GP> sm;
+  __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
+  __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
+  __shared__ __attribute__((aligned(16))) char ps[kTerms][16 * P::kPitch];
+
+  const int p = blockIdx.x, b = blockIdx.z;
+  const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
+  const int qb = kh * G + 16 * slice;
+  const int Gs = min(16, G - 16 * slice);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qh = lane & 15, qg = lane >> 4;
+  const int start = p * T;
+  PageWindow<2> pw;
+  pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
+  const int length = lengths[b];
+  const int end = min(start + T, length);
+  const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+  const int64_t RS = int64_t(Hkv) * D;
+
+  bf16x8_t qf[C::kCH];
+  {
+    const bool live = qh < Gs;
+    const uint16_t* qrow = q + int64_t(b) * qsb + int64_t(qb + (live ? qh : 0)) * qsh + 8 * qg;
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch)
+      qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
+  }
+  const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
+  int voff[C::kDma];
+#pragma unroll
+  for (int i = 0; i < C::kDma; ++i) {
+    const int slot = 64 * i + lane;
+    const int row = slot / C::kPieces, piece = slot % C::kPieces;
+    voff[i] = row < C::kTW && piece < D / 8 ? ((w * C::kTW + row) * int(RS) + 8 * piece) * 2
+                                            : 0x7ffffff0;
+  }
+
+  floatx4_t acc[P::kNBW];  // O[head 4*qg + r][64w + 16j + qh]
+#pragma unroll
+  for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  float m4[4];             // running max of heads 4*qg + r
+#pragma unroll
+  for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
+  float m_own = -INFINITY;  // running max of head qh
+  float l_own = 0.f;        // this lane's share of head qh's denominator
+
+  auto issue_k = [&](KTile<D, GP>& R, int ti) __attribute__((always_inline)) {
+    const int t0 = start + ti * TILE;
+    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch) R.k[0][ch] = buffer_load16(buf.k, koff + 64 * ch);
+  };
+  auto issue_v = [&](char* slot, int ti) __attribute__((always_inline)) {
+    const int t0 = start + ti * TILE;
+    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
+#pragma unroll
+    for (int i = 0; i < C::kDma; ++i)
+      lds_copy16(buf.v, slot + w * C::kSlot + 1024 * i, voff[i]);
+  };
+
+  // Tile ti in two parts around the copy of the V rows of tile ti - 1 (into
+  // the slot P V of tile ti + 1 has finished reading) and the refill of R with
+  // the K rows of tile ti - 2, which the caller issues between them: scores
+  // and the tile maximum, then probabilities and P V with the V rows in `slot`.
+  float s0[4];
+  auto scores = [&](KTile<D, GP>& R, int ti) __attribute__((always_inline)) {
+    const int nvalid = end - (start + ti * TILE);
+    floatx4_t s[1] = {floatx4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch)
+      s[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, R.k[0][ch]),
+                                                      qf[ch], s[0], 0, 0, 0);
+    mfma_result_barrier(s);
+    if constexpr (kMode != kMatched) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[0][r] *= scale;
+    }
+    if (nvalid < TILE) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (w * C::kTW + 4 * qg + r >= nvalid) s[0][r] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+    mx = max_rows(mx);
+    float (*wm)[16] = sm.wmax[ti & 1];
+    if (lane < 16) wm[w][lane] = mx;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s0[r] = s[0][r];
+    lds_barrier();
+  };
+  auto finish = [&](const char* slot, int ti, bool first) __attribute__((always_inline)) {
+    float (*wm)[16] = sm.wmax[ti & 1];
+    float alpha[4];
+    bool moved = false;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * qg + r;
+      const float tm = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+      const float mn = fmaxf(m4[r], tm);
+      moved |= mn != m4[r];
+      alpha[r] = kMode == kMatched ? exp2_fast((m4[r] - mn) * c) : exp_fast(m4[r] - mn);
+      m4[r] = mn;
+    }
+    const float tm = fmaxf(fmaxf(wm[0][qh], wm[1][qh]), fmaxf(wm[2][qh], wm[3][qh]));
+    const float mn = fmaxf(m_own, tm);
+    const float a_own = kMode == kMatched ? exp2_fast((m_own - mn) * c) : exp_fast(m_own - mn);
+    m_own = mn;
+    const float neg_mc = -(mn * c);
+    float psum = 0.f;
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = kMode == kMatched ? exp2_fast(fmaf(s0[r], c, neg_mc)) : exp_fast(s0[r] - mn);
+      psum += pr[r];
+    }
+    // P[head qh][tokens w*16 + 4qg .. +3] into row qh of each term's LDS tile
+    // (lo, mid, hi for the FP32 probabilities of the base / split protocols).
+    const int pofs = qh * P::kPitch + (w * C::kTW + 4 * qg) * 2;
+    if constexpr (kMode == kMatched) {
+      *reinterpret_cast<u32x2_t*>(ps[0] + pofs) =
+          u32x2_t{qh < Gs ? pack_bf16(pr[0], pr[1]) : 0u, qh < Gs ? pack_bf16(pr[2], pr[3]) : 0u};
+    } else {
+      uint32_t t3[3][2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const uint32_t hi = pack_bf16(pr[2 * h2], pr[2 * h2 + 1]);
+        const float r0 = pr[2 * h2] - bf16_lo(hi), r1 = pr[2 * h2 + 1] - bf16_hi(hi);
+        const uint32_t mid = pack_bf16(r0, r1);
+        const uint32_t lo = pack_bf16(r0 - bf16_lo(mid), r1 - bf16_hi(mid));
+        t3[0][h2] = qh < Gs ? lo : 0u;
+        t3[1][h2] = qh < Gs ? mid : 0u;
+        t3[2][h2] = qh < Gs ? hi : 0u;
+      }
+#pragma unroll
+      for (int t = 0; t < 3; ++t) *reinterpret_cast<u32x2_t*>(ps[t] + pofs) = u32x2_t{t3[t][0], t3[t][1]};
+    }
+    l_own = l_own * a_own + psum;
+    if (!first && __builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
+    }
+    // This wavefront's copies of tile ti have landed; after the barrier every
+    // wavefront's have, and every P row is written.
+    if (ti >= 2) asm volatile("s_waitcnt vmcnt(25)" ::: "memory");
+    else if (ti == 1) asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    // ---- P V over the whole tile, columns 64w .. 64w + 63: k-step ks covers
+    // tokens 32ks .. 32ks + 31; lane L supplies k = 8(L/16) + e <-> token
+    // 32ks + 8(L/16) + e for both operands (as in matched_tile_kernel).
+    auto pv_step = [&](auto KS) __attribute__((always_inline)) {
+      constexpr int ks = decltype(KS)::value;
+      bf16x8_t a[kTerms];
+#pragma unroll
+      for (int t = 0; t < kTerms; ++t) {
+        const char* prow = ps[t] + qh * P::kPitch + (32 * ks + 8 * qg) * 2;
+        const u32x2_t a0 = *reinterpret_cast<const u32x2_t*>(prow);
+        const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(prow + 8);
+        a[t] = __builtin_bit_cast(bf16x8_t, u32x4_t{a0[0], a0[1], a1[0], a1[1]});
+      }
+      // V rows 32ks + 8qg + (qh >> 2) (lo) and + 4 (hi): row t of the tile
+      // is row t % 16 of wavefront t / 16's slot part; columns 64w + 16j.
+      // The transposed reads are issued from inline asm (lds_read_tr_at): the
+      // compiler then adds no vmcnt wait of its own for the LDS copies it
+      // cannot tell apart from this slot's (the wait above covers them), and
+      // lds_settle makes the results wait for the reads.
+      const uint32_t vb = lds_address(slot) + (qg >> 1) * C::kSlot +
+                          (8 * (qg & 1) + (qh >> 2)) * C::kPitch + w * P::kCols * 2 + 8 * (qh & 3);
+      constexpr int kOff = ks * 2 * C::kSlot;
+      short4_t lo[P::kNBW], hi[P::kNBW];
+      lo[0] = lds_read_tr_at<kOff>(vb);
+      hi[0] = lds_read_tr_at<kOff + 4 * C::kPitch>(vb);
+      lo[1] = lds_read_tr_at<kOff + 32>(vb);
+      hi[1] = lds_read_tr_at<kOff + 4 * C::kPitch + 32>(vb);
+      lo[2] = lds_read_tr_at<kOff + 64>(vb);
+      hi[2] = lds_read_tr_at<kOff + 4 * C::kPitch + 64>(vb);
+      lo[3] = lds_read_tr_at<kOff + 96>(vb);
+      hi[3] = lds_read_tr_at<kOff + 4 * C::kPitch + 96>(vb);
+      lds_settle(lo, hi);
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j) {
+        const bf16x8_t bv = __builtin_bit_cast(
+            bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo[j])[0], __builtin_bit_cast(u32x2_t, lo[j])[1],
+                              __builtin_bit_cast(u32x2_t, hi[j])[0], __builtin_bit_cast(u32x2_t, hi[j])[1]});
+#pragma unroll
+        for (int t = 0; t < kTerms; ++t)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], bv, acc[j], 0, 0, 0);
+      }
+    };
+    pv_step(std::integral_constant<int, 0>{});
+    pv_step(std::integral_constant<int, 1>{});
+  };
+
+  // Reverse tile walk (matched_splitkv.py:71), last tile first; register sets
+  // A, B and LDS slots vs0, vs1 alternate.  The first loads, K(ti), V(ti),
+  // K(ti - 1), come in the steady-state order, so the vmcnt above is exact
+  // from the first tile on (smaller for the last two tiles).
+  pw.settle();
+  if (count > 0) {
+    KTile<D, GP> A, B;
+    int ti = count - 1;
+    issue_k(A, ti);
+    issue_v(vs0, ti);
+    if (ti >= 1) issue_k(B, ti - 1);
+    bool first = true;
+    // Pairs of tiles with every load of the steady state issued
+    // unconditionally (so the compiler's own waits for the K registers count
+    // the same loads on every path); the last two or three tiles are peeled.
+    while (ti >= 3) {
+      scores(A, ti);
+      issue_v(vs1, ti - 1);
+      issue_k(A, ti - 2);
+      finish(vs0, ti, first);
+      scores(B, ti - 1);
+      issue_v(vs0, ti - 2);
+      issue_k(B, ti - 3);
+      finish(vs1, ti - 1, false);
+      ti -= 2;
+      first = false;
+    }
+    if (ti == 2) {
+      scores(A, 2);
+      issue_v(vs1, 1);
+      issue_k(A, 0);
+      finish(vs0, 2, first);
+      scores(B, 1);
+      issue_v(vs0, 0);
+      finish(vs1, 1, false);
+      scores(A, 0);
+      finish(vs0, 0, false);
+    } else if (ti == 1) {
+      scores(A, 1);
+      issue_v(vs1, 0);
+      finish(vs0, 1, first);
+      scores(B, 0);
+      finish(vs1, 0, false);
+    } else {
+      scores(A, 0);
+      finish(vs0, 0, first);
+    }
+  }
+
+  // ---- epilogue: denominators over the waves; O needs no reduction
+  const float l = sum_rows(l_own);
+  if (lane < 16) sm.lsum[w][lane] = l;
+  lds_barrier();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * qg + r;
+    if (h >= Gs) break;
+    const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
+    const float safe = den > 0.f ? den : 1.f;
+    const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
+    const int col = w * P::kCols + qh;
+    if constexpr (kMode == kBase) {
+      // acc / denom, 0 for an empty sequence (kernels.py:40).
+      uint16_t* dst = out + (int64_t(b) * Hq + qb + h) * D + col;
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = uint16_t(bf16_bits(acc[j][r] / safe));
+    } else if constexpr (kMode == kSplit) {
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r];
+      if (w == 0 && qh == 0) {
+        maxima[orow] = m4[r];
+        lse_out[orow] = den;
+      }
+    } else {
+      const float inv = rcp_fast(safe);
+      const float lv = den > 0.f ? fmaf(m4[r], scale, ln_fast(safe)) : -INFINITY;
+      if constexpr (kFused) {
+        // Device-scope stores (global_store sc1), as in matched_partition_kernel.
+#pragma unroll
+        for (int j = 0; j < P::kNBW; ++j)
+          __hip_atomic_store(partials + orow * D + col + 16 * j, acc[j][r] * inv, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        if (w == 0 && qh == 0)
+          __hip_atomic_store(lse_out + orow, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+#pragma unroll
+        for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r] * inv;
+        if (w == 0 && qh == 0) lse_out[orow] = lv;
+      }
+    }
+  }
+
+  if constexpr (kFused) {
+    // Split-completion count and the last workgroup's merge, exactly as in
+    // matched_partition_kernel.
+    int* counter = counters + int64_t(b) * Hkv + kh;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (tid == 0)
+      sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                splits - 1;
+    __syncthreads();
+    if (!sm.last) return;
+    const int64_t row0 = int64_t(b) * Hq + kh * G;
+    constexpr int kV = D / 64;
+    for (int hh = __builtin_amdgcn_readfirstlane(w); hh < G; hh += 4) {
+      float w0 = 0.f, w1 = 0.f, mrg[kV];
+      merge_splits<kV, true>(
+          partials + (row0 + hh) * splits * D, D, lane * kV, splits,
+          [&] { lse_weights<true>(lse_out + (row0 + hh) * splits, splits, lane, w0, w1); },
+          [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, mrg);
+      uint16_t* dst = out + (row0 + hh) * D + lane * kV;
+#pragma unroll
+      for (int e = 0; e < kV; ++e) dst[e] = uint16_t(bf16_bits(mrg[e]));
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ----------------------------------------------------- single-tile partition
 // The same partial + LSE as matched_partition_kernel for plans whose splits
 // are exactly one tile (tokens_per_split == 16384 / D: the headline D=256
@@ -468,16 +798,6 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
 // of the 16-token grouping at D=256.  Scores, maxima, probabilities,
 // denominators and LSEs are bit-identical to matched_partition_kernel's; the
 // partial differs only in the fp32 summation order of P V.
-template <int D>
-struct TileP {
-  static constexpr int kTile = 16384 / D;
-  // Bytes per head row of P: 8 bytes of padding put the 16 rows of a
-  // ds_write_b64 / ds_read_b64 in different banks (row r starts at bank 2r).
-  static constexpr int kPitch = 2 * kTile + 8;
-  static constexpr int kCols = D / 4;        // output columns per wavefront
-  static constexpr int kNBW = kCols / 16;    // 16-column blocks per wavefront
-  static constexpr int kKS = kTile / 32;     // 32-token k-steps of PV
-};
 
 template <int D, int GP>
 __global__ void __launch_bounds__(kThreads, 2)
@@ -769,13 +1089,20 @@ void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a
 #undef PD_LAUNCH_TILE
 }
 
+// D = 256 runs matched_cols_kernel, the other head dims matched_partition_kernel.
 template <int D, bool kFused, int kMode = kMatched>
 void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
-#define PD_LAUNCH_GP(GPV)                                                                     \
-  hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused, kMode>), grid, dim3(kThreads),  \
-                     0, stream, a.table, a.lengths, a.q, a.tsb, a.width, a.T, a.qsb, a.qsh,  \
-                     a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,        \
-                     a.maxima, a.Hkv, a.splits, a.scale, a.c)
+#define PD_LAUNCH_GP(GPV)                                                                      \
+  if constexpr (D == 256)                                                                      \
+    hipLaunchKernelGGL((matched_cols_kernel<GPV, kFused, kMode>), grid, dim3(kThreads), 0,      \
+                       stream, a.table, a.lengths, a.q, a.tsb, a.width, a.T, a.qsb, a.qsh,     \
+                       a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,        \
+                       a.maxima, a.Hkv, a.splits, a.scale, a.c);                               \
+  else                                                                                         \
+    hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused, kMode>), grid, dim3(kThreads), \
+                       0, stream, a.table, a.lengths, a.q, a.tsb, a.width, a.T, a.qsb, a.qsh, \
+                       a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,       \
+                       a.maxima, a.Hkv, a.splits, a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_GP(1); break;
     case 2: PD_LAUNCH_GP(2); break;

@@ -140,10 +140,11 @@ def _bits(t):
     ([2051, 1, 0, 1025], 32, 4, 256, 4096, 1), ([2051, 1, 0, 1025], 32, 2, 128, 4096, 6),
     ([3000, 17], 12, 4, 64, 4096, 0), ([4096] * 3, 16, 1, 256, 4096, 0)])
 def test_fused_decode_matches_two_launches(lengths, hq, hkv, dim, cap, splits):
-    """The fused launch runs the general partition kernel.  Plans whose splits span
-    several tiles use that same kernel in two launches, so everything is bit-identical.
-    Single-tile plans use the column-split kernel in two launches: the same scores,
-    maxima, denominators and LSEs (bit-identical), a P V sum in another fp32 order."""
+    """The fused launch runs the multi-tile partition kernel of its head dim.  Plans
+    whose splits span several tiles use that same kernel in two launches, so everything
+    is bit-identical.  Single-tile plans use the single-tile kernel in two launches: the
+    same scores, maxima, denominators and LSEs (bit-identical), and a P V sum that may
+    be in another fp32 order (D < 256)."""
     g = to_gpu(make_case(lengths, hq, hkv, dim, seed=31, capacity=cap))
     res = allocate_matched_resources(DecodeSpec(len(lengths), hq, hkv, dim, cap), "cuda",
                                      num_splits=splits, fused=True)
