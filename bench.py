@@ -356,6 +356,7 @@ def profile_launches(torch, which, calls=50):
     calibrate: a 256 MiB device copy (known bytes: 256 MiB read + 256 MiB
     written), used to scale FETCH_SIZE / WRITE_SIZE.  headline: partition and
     merge at the headline shape.  sweep: partition and merge of the bandwidth sweep.
+    long: partition and merge at D256 GQA 4:1, B=1, context 131072 (KV from HBM).
     """
     import numpy as np
     src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device="cuda")
@@ -382,6 +383,13 @@ def profile_launches(torch, which, calls=50):
             case["merge"]()
         torch.cuda.synchronize()
         del case
+    if "long" in which:
+        case = matched_case(torch, 1, 16, 4, 256, 131072, [131072], 11)
+        for _ in range(10):
+            case["partition"]()
+            case["merge"]()
+        torch.cuda.synchronize()
+        del case
     torch.cuda.empty_cache()
     print(json.dumps({"profiled": which}))
 
@@ -395,7 +403,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the extra measurements")
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU run")
-    ap.add_argument("--profile", default=None, metavar="headline,sweep",
+    ap.add_argument("--profile", default=None, metavar="headline,sweep,long",
                     help="only make eager launches for rocprofv3 (calibration copy + cases)")
     ap.add_argument("--require-idle-gpu", action="store_true",
                     help="refuse to run (before any GPU work) if amd-smi lists other processes")
