@@ -470,6 +470,7 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   constexpr int TILE = C::kTile;
   constexpr int kTerms = kMode == kMatched ? 1 : 3;
   static_assert(C::kNG == 1 && C::kTW == 16 && P::kKS == 2, "D = 256 geometry");
+  static_assert(C::kCH == 8 && C::kDma == 9, "8 K and 9 V loads per tile: the vmcnt values");
   __shared__ MatchedShared<D, GP> sm;
   __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
   __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
