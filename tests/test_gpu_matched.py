@@ -271,3 +271,18 @@ def test_single_split_beyond_the_prefetched_table_window():
     assert res.plan.tokens_per_split == 40960
     check_all(case, g, res, out)
 
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_d256_tile_counts_of_the_column_split_kernel(fused):
+    """D=256 multi-tile splits run matched_cols_kernel, whose pipeline peels the last
+    two or three tiles: splits of 1 to 8 tiles (64 tokens each), full and partial."""
+    lengths = [1, 64, 65, 128, 130, 192, 200, 256, 300, 384, 450, 511, 512]
+    case = make_case(lengths, 16, 4, 256, seed=41, capacity=512)
+    g = to_gpu(case)
+    res = allocate_matched_resources(DecodeSpec(len(lengths), 16, 4, 256, 512), "cuda",
+                                     num_splits=1, fused=fused)
+    assert res.plan.tokens_per_split == 512
+    out = matched_decode(*g, resources=res)
+    torch.cuda.synchronize()
+    check_all(case, g, res, out, where=f"fused={fused}")

@@ -169,3 +169,20 @@ def test_groups_larger_than_16_heads(backend, dim, hq, hkv):
     assert_close_dense(actual, torch_dense(*g))
     assert_within_one_ulp(actual, oracle_for(case, backend, spec), f"{backend} G={hq // hkv}")
     assert torch.count_nonzero(actual[0]) == 0
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+def test_d256_tile_counts_of_the_column_split_kernel(backend):
+    """D=256 runs matched_cols_kernel for both backends: whole contexts (base) and
+    1024-token partitions (split) of 1 to 20 tiles, full and partial."""
+    lengths = [1, 64, 65, 129, 192, 255, 320, 1023, 1024, 1025, 1100, 1280]
+    q, k, v, table, lens = make_case(lengths, 8, 2, 256, seed=43, capacity=1280)
+    poison_tails(k, v, table, lens)
+    case = (q, k, v, table, lens)
+    g = to_gpu(case)
+    spec = DecodeSpec(len(lengths), 8, 2, 256, 1280)
+    res = allocate_resources(spec, "cuda", backend)
+    actual = paged_decode(*g, resources=res, backend=backend).clone()
+    torch.cuda.synchronize()
+    assert_close_dense(actual, torch_dense(*g))
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec), backend)
