@@ -442,8 +442,8 @@ struct TileP {
 // LDS, and wavefront w multiplies the whole tile's P by V columns
 // [64w, 64w + 64).  The accumulator then takes 16 VGPRs instead of 64, which
 // leaves room for a second K register set: K rows are loaded two tiles ahead
-// (refilled into the set whose QK products were just issued), as below
-// D = 256.  There is no cross-wave reduction of O at the end.
+// (into the set whose QK products the tile has just used), as below D = 256.
+// There is no cross-wave reduction of O at the end.
 //
 // Every wavefront reads every wavefront's V rows, so the V rows of tile ti - 1
 // are copied into the LDS slot of tile ti + 1 only after the first barrier of
