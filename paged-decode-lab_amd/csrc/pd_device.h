@@ -214,8 +214,9 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
 // 4*(L/16) + e-4 above).  The B operand needs V columns (4 consecutive tokens
 // of one d per lane).  V rows therefore go to LDS by buffer_load ... lds (no
 // registers; lane l of a copy fills bytes 16l .. 16l+15 of its 1 KiB, and
-// reads past the buffer write zeros), each row padded by 16 bytes so that
-// the transposed reads hit distinct banks, and are read with
+// reads past the buffer write zeros), with the 16-byte pieces of each row
+// swizzled (vswz) so that the transposed reads hit distinct banks, and are
+// read with
 // ds_read_b64_tr_b16: in each 16-lane group, when source lane 4c + b
 // addresses row c, columns 4b .. 4b+3 of a 4 x 16 block, lane n receives
 // column n of the block (rows 0..3).  Output lane L holds O[head 4*(L/16) + r]
@@ -227,12 +228,37 @@ struct Matched {
   static constexpr int kNG = kTW / 16;                       // 16-token groups per wavefront
   static constexpr int kCH = D / 32;                         // 32-wide k-chunks of QK
   static constexpr int kNB = D / 16;                         // 16-column blocks of PV
-  static constexpr int kPieces = D / 8 + 1;                  // 16-byte pieces per LDS row
+  static constexpr int kPieces = D / 8;                      // 16-byte pieces per V row
   static constexpr int kPitch = 16 * kPieces;                // bytes per V row in LDS
-  static constexpr int kDma = (kTW * kPitch + 1023) / 1024;  // 1 KiB copies per wavefront
+  static constexpr int kDma = kTW * kPitch / 1024;           // 1 KiB copies per wavefront
   static constexpr int kSlot = 1024 * kDma;                  // LDS bytes of a wavefront's rows
-  static_assert(kNG >= 1 && kCH >= 1, "geometry");
+  static_assert(kNG >= 1 && kCH >= 1 && kTW * kPitch % 1024 == 0, "geometry");
 };
+
+// V rows sit in LDS unpadded (kPitch = 2D bytes), with the 16-byte pieces of
+// each row permuted: piece p of row r is stored at position p ^ vswz(r).  A
+// transposed read (ds_read_b64_tr_b16) addresses 4 consecutive rows at the
+// same two pieces; with vswz(r) = 2 (r % 4) those land on 8 different piece
+// positions modulo 8, i.e. 128 distinct bytes: all banks, no conflict.
+__device__ __forceinline__ int vswz(int row) { return 2 * (row & 3); }
+
+// Source byte offset (tile-relative) of the 16 bytes that DMA copy i of
+// wavefront w places at LDS position 16 * (64 i + lane) of its rows.
+template <int D, int GP>
+__device__ __forceinline__ int v_copy_offset(int i, int lane, int w, int RS) {
+  using C = Matched<D, GP>;
+  const int slot = 64 * i + lane;
+  const int row = slot / C::kPieces, pos = slot % C::kPieces;
+  return ((w * C::kTW + row) * RS + 8 * (pos ^ vswz(row))) * 2;
+}
+
+// Byte offset within a V row of this lane's 8 bytes of a transposed read of
+// the 16 columns from col0 (a multiple of 16): lane l % 4 = b reads columns
+// col0 + 4b .. +3, in rows r with r % 4 = rmod.
+__device__ __forceinline__ int v_read_offset(int col0, int lane, int rmod) {
+  const int b = lane & 3;
+  return 16 * (((col0 >> 3) + (b >> 1)) ^ (2 * rmod)) + 8 * (b & 1);
+}
 
 template <int D, int GP>
 struct KTile {
@@ -334,6 +360,14 @@ __device__ __forceinline__ short4_t lds_read_tr_at(uint32_t base) {
   short4_t r;
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
   return r;
+}
+
+// s_waitcnt vmcnt(N): at most N vector-memory loads of this wavefront remain
+// outstanding (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // Waits for every outstanding LDS read (lgkmcnt(0)) and makes the values

@@ -119,21 +119,16 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
       qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
   }
 
-  // Tile-relative byte offsets: K pieces of this lane, and the source of
-  // each 16-byte LDS piece this lane fills (row, piece) = (slot / kPieces,
-  // slot % kPieces); the padding piece and rows past the wavefront's share
-  // read past the buffer, i.e. zeros.
+  // Tile-relative byte offsets: K pieces of this lane, and the source of each
+  // 16-byte LDS piece this lane fills (v_copy_offset); rows past the sequence
+  // end read past the buffer, i.e. zeros.
   const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) {
-    const int slot = 64 * i + lane;
-    const int row = slot / C::kPieces, piece = slot % C::kPieces;
-    voff[i] = row < C::kTW && piece < D / 8 ? ((w * C::kTW + row) * int(RS) + 8 * piece) * 2
-                                            : 0x7ffffff0;
-  }
-  // This lane's transposed-read address within its wavefront's LDS rows.
-  const int trb = w * C::kSlot + (4 * qg + ((lane & 15) >> 2)) * C::kPitch + 8 * (lane & 3);
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP>(i, lane, w, int(RS));
+  // This lane's transposed-read row within its wavefront's LDS rows (rows
+  // 4qg + qh/4 of each 16-row group, so row % 4 = qh / 4).
+  const int trb = w * C::kSlot + (4 * qg + (qh >> 2)) * C::kPitch;
 
   floatx4_t acc[C::kNB];   // O[head 4*qg + r][16j + qh]
 #pragma unroll
@@ -268,8 +263,9 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
     for (int g = 0; g < C::kNG; g += 2) {
 #pragma unroll
       for (int j = 0; j < C::kNB; ++j) {
-        const short4_t lo = lds_read_tr(base + 16 * g * C::kPitch + 32 * j);
-        const short4_t hi = lds_read_tr(base + 16 * (g + 1) * C::kPitch + 32 * j);
+        const int col = v_read_offset(16 * j, lane, qh >> 2);
+        const short4_t lo = lds_read_tr(base + 16 * g * C::kPitch + col);
+        const short4_t hi = lds_read_tr(base + 16 * (g + 1) * C::kPitch + col);
         const bf16x8_t bv = __builtin_bit_cast(
             bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo)[0], __builtin_bit_cast(u32x2_t, lo)[1],
                               __builtin_bit_cast(u32x2_t, hi)[0], __builtin_bit_cast(u32x2_t, hi)[1]});
@@ -452,8 +448,8 @@ struct TileP {
 // its own copies of tile ti.  The K rows of tile ti - 2 are loaded right after
 // the V rows of tile ti - 1, so that wait never covers the K rows loaded two
 // tiles ahead: after the V rows of tile ti come the K rows of tile ti - 1 and
-// the V rows of tile ti - 1 and K rows of tile ti - 2 (8 + 9 + 8 loads per
-// wavefront), hence vmcnt(25) before that barrier.
+// the V rows of tile ti - 1 and K rows of tile ti - 2 (8 + 8 + 8 loads per
+// wavefront), hence vmcnt(24) before that barrier.
 template <int GP, bool kFused, int kMode>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
@@ -470,7 +466,7 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   constexpr int TILE = C::kTile;
   constexpr int kTerms = kMode == kMatched ? 1 : 3;
   static_assert(C::kNG == 1 && C::kTW == 16 && P::kKS == 2, "D = 256 geometry");
-  static_assert(C::kCH == 8 && C::kDma == 9, "8 K and 9 V loads per tile: the vmcnt values");
+  constexpr int kKLoads = C::kCH, kVLoads = C::kDma;  // per wavefront and tile
   __shared__ MatchedShared<D, GP> sm;
   __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
   __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
@@ -502,12 +498,7 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) {
-    const int slot = 64 * i + lane;
-    const int row = slot / C::kPieces, piece = slot % C::kPieces;
-    voff[i] = row < C::kTW && piece < D / 8 ? ((w * C::kTW + row) * int(RS) + 8 * piece) * 2
-                                            : 0x7ffffff0;
-  }
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP>(i, lane, w, int(RS));
 
   floatx4_t acc[P::kNBW];  // O[head 4*qg + r][64w + 16j + qh]
 #pragma unroll
@@ -617,9 +608,9 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     }
     // This wavefront's copies of tile ti have landed; after the barrier every
     // wavefront's have, and every P row is written.
-    if (ti >= 2) asm volatile("s_waitcnt vmcnt(25)" ::: "memory");
-    else if (ti == 1) asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (ti >= 2) wait_vmcnt<2 * kKLoads + kVLoads>();
+    else if (ti == 1) wait_vmcnt<kKLoads + kVLoads>();
+    else wait_vmcnt<0>();
     lds_barrier();
     // ---- P V over the whole tile, columns 64w .. 64w + 63: k-step ks covers
     // tokens 32ks .. 32ks + 31; lane L supplies k = 8(L/16) + e <-> token
@@ -641,17 +632,15 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       // cannot tell apart from this slot's (the wait above covers them), and
       // lds_settle makes the results wait for the reads.
       const uint32_t vb = lds_address(slot) + (qg >> 1) * C::kSlot +
-                          (8 * (qg & 1) + (qh >> 2)) * C::kPitch + w * P::kCols * 2 + 8 * (qh & 3);
+                          (8 * (qg & 1) + (qh >> 2)) * C::kPitch;
       constexpr int kOff = ks * 2 * C::kSlot;
       short4_t lo[P::kNBW], hi[P::kNBW];
-      lo[0] = lds_read_tr_at<kOff>(vb);
-      hi[0] = lds_read_tr_at<kOff + 4 * C::kPitch>(vb);
-      lo[1] = lds_read_tr_at<kOff + 32>(vb);
-      hi[1] = lds_read_tr_at<kOff + 4 * C::kPitch + 32>(vb);
-      lo[2] = lds_read_tr_at<kOff + 64>(vb);
-      hi[2] = lds_read_tr_at<kOff + 4 * C::kPitch + 64>(vb);
-      lo[3] = lds_read_tr_at<kOff + 96>(vb);
-      hi[3] = lds_read_tr_at<kOff + 4 * C::kPitch + 96>(vb);
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j) {
+        const uint32_t vj = vb + v_read_offset(w * P::kCols + 16 * j, lane, qh >> 2);
+        lo[j] = lds_read_tr_at<kOff>(vj);
+        hi[j] = lds_read_tr_at<kOff + 4 * C::kPitch>(vj);
+      }
       lds_settle(lo, hi);
 #pragma unroll
       for (int j = 0; j < P::kNBW; ++j) {
@@ -852,12 +841,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   const int kl = kline_offset(lane, int(RS)) + w * C::kTW * int(RS) * 2;
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) {
-    const int slot = 64 * i + lane;
-    const int row = slot / C::kPieces, piece = slot % C::kPieces;
-    voff[i] = row < C::kTW && piece < D / 8 ? ((w * C::kTW + row) * int(RS) + 8 * piece) * 2
-                                            : 0x7ffffff0;
-  }
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP>(i, lane, w, int(RS));
 
   KTile<D, GP> R;
   {
@@ -936,7 +920,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     const char* hi_row = vs + (t_hi / C::kTW) * C::kSlot + (t_hi % C::kTW) * C::kPitch;
 #pragma unroll
     for (int j = 0; j < P::kNBW; ++j) {
-      const int cb = (w * P::kCols + 16 * j) * 2 + 8 * (qh & 3);
+      const int cb = v_read_offset(w * P::kCols + 16 * j, lane, qh >> 2);
       const short4_t lo = lds_read_tr(lo_row + cb);
       const short4_t hi = lds_read_tr(hi_row + cb);
       const bf16x8_t bv = __builtin_bit_cast(

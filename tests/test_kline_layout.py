@@ -74,3 +74,46 @@ def test_operand_layout_loads_touch_half_lines_and_whole_line_loads_whole_ones()
     for start in range(0, 64, 8):
         assert len({line_of(a) for a in whole[start:start + 8]}) == 1
         assert len({line_of(a) for a in operand[start:start + 8]}) == 8
+
+
+def vswz(row):
+    return 2 * (row & 3)
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_v_rows_swizzle_round_trips_and_transposed_reads_are_conflict_free(dim):
+    """pd_device.h stores V rows in LDS unpadded, 16-byte piece p of row r at position
+    p ^ vswz(r) (v_copy_offset), and reads them back with v_read_offset.  Every copy
+    lane fills one distinct position, every transposed read finds the logical columns
+    it asks for, and the 16 lanes of a read hit 128 distinct bytes (all banks)."""
+    pieces = dim // 8
+    pitch = 16 * pieces
+    rows = 16384 // dim // 4               # rows per wavefront
+    copies = rows * pitch // 1024
+    # DMA: LDS position 16 * (64 i + lane) <- global (row, piece pos ^ vswz(row))
+    stored = {}
+    for i in range(copies):
+        for lane in range(64):
+            slot = 64 * i + lane
+            row, pos = divmod(slot, pieces)
+            stored[(row, pos)] = (row, pos ^ vswz(row))
+    assert len(stored) == rows * pieces
+    assert sorted(stored.values()) == [(r, p) for r in range(rows) for p in range(pieces)]
+
+    def v_read_offset(col0, lane, rmod):
+        b = lane & 3
+        return 16 * (((col0 >> 3) + (b >> 1)) ^ (2 * rmod)) + 8 * (b & 1)
+
+    for first_row in range(0, rows, 4):
+        for col0 in range(0, dim, 16):
+            banks = set()
+            for lane in range(16):
+                c, b = lane >> 2, lane & 3
+                row = first_row + c
+                off = v_read_offset(col0, lane, row % 4)
+                pos, within = divmod(off, 16)
+                # the logical piece stored there holds columns col0 + 4b .. + 3
+                assert stored[(row, pos)] == (row, (col0 + 4 * b) // 8)
+                assert within == 8 * (b & 1)
+                banks.add((row * pitch + off) % 128)
+            assert len(banks) == 16             # 16 x 8 bytes = 128 distinct bytes
