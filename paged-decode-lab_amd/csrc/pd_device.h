@@ -460,6 +460,68 @@ struct PageWindow {
   }
 };
 
+// ------------------------------------------------------------- batch order
+// Which sequence the workgroups of grid row z serve.  Every (split, kv head,
+// sequence) item computes the same values whichever workgroup runs it, so a
+// launch may hand the grid rows to the sequences in any order; taking them by
+// length evens out the work per CU.  The dispatcher sends workgroup i to XCD
+// i % 8; while the whole grid is resident (two workgroups per CU), workgroups
+// i and i + CUs share a CU; past that, each new workgroup takes the next free
+// slot.  `order` (chosen by the launcher from the grid and the CU count):
+//   < 0   row z serves sequence z;
+//   0     row z serves the sequence of length rank z (longest first: the grid
+//         runs in several rounds, and the longest items start first);
+//   H > 0 the grid is resident at once and rows z and z + H share CUs: rows
+//         without a partner (z in [B - H, H)) take the longest sequences, and
+//         each pair (z, z + H) one long and one short sequence.
+// Ranks order the lengths decreasing, ties by increasing index, so they are a
+// permutation of [0, B).
+constexpr int kMaxOrderedBatch = 256;
+static_assert(kMaxOrderedBatch == kThreads, "one thread per sequence");
+
+__device__ __forceinline__ int order_rank(int z, int B, int order) {
+  if (order <= 0 || B > 2 * order) return z;
+  const int H = order, P = B > H ? B - H : 0;  // P rows z in [0, P) have partner z + H
+  if (z >= H) return B - 1 - (z - H);
+  return z >= P ? z - P : H - P + z;
+}
+
+struct OrderedSequence {
+  int b, length;
+};
+
+// Requires 0 <= order, 2 <= B <= kMaxOrderedBatch, blockDim.x == kThreads and
+// every thread of the workgroup; `slens` holds kMaxOrderedBatch + 4 ints of LDS,
+// 16-byte aligned.  One load of the lengths, then thread t counts the
+// sequences ranked before sequence t; the one whose rank row z asks for
+// publishes its index.
+__device__ __forceinline__ OrderedSequence ordered_sequence(const int32_t* __restrict__ lengths,
+                                                            int B, int z, int order,
+                                                            int* __restrict__ slens) {
+  const int tid = threadIdx.x;
+  // Entries past B hold INT_MIN: never longer, and a tie only with an index >= B.
+  const int len = tid < B ? lengths[tid] : INT32_MIN;
+  slens[tid] = len;
+  if (tid == 0) slens[kMaxOrderedBatch] = z;  // overwritten below by the one match
+  __syncthreads();
+  if (tid < B) {
+    const int want = order_rank(z, B, order);
+    int rank = 0;
+    const int4* s4 = reinterpret_cast<const int4*>(slens);
+    for (int u = 0; u < B; u += 4) {
+      const int4 x = s4[u >> 2];
+      rank += int(x.x > len) + int(x.x == len && u < tid);
+      rank += int(x.y > len) + int(x.y == len && u + 1 < tid);
+      rank += int(x.z > len) + int(x.z == len && u + 2 < tid);
+      rank += int(x.w > len) + int(x.w == len && u + 3 < tid);
+    }
+    if (rank == want) slens[kMaxOrderedBatch] = tid;
+  }
+  __syncthreads();
+  const int b = __builtin_amdgcn_readfirstlane(slens[kMaxOrderedBatch]);
+  return {b, __builtin_amdgcn_readfirstlane(slens[b])};
+}
+
 // The K and V rows of one tile as buffers that end after row nvalid - 1, so
 // rows past the sequence end read as zero without being fetched (NaN-poisoned
 // slots and dead pages are never touched) and every load is unconditional.

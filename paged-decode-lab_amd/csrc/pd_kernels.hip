@@ -26,6 +26,7 @@
 // graph-capturable and replay correctly with new lengths, pages and KV.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <type_traits>
@@ -75,8 +76,8 @@ constexpr int kMatched = 0, kBase = 1, kSplit = 2;
 template <int D, int GP, bool kFused, int kMode>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
-                         const uint16_t* __restrict__ q, int tsb, int width, int T, int qsb,
-                         int qsh, int G, int hs, int Hq, const uint16_t* __restrict__ k,
+                         const uint16_t* __restrict__ q, int tsb, int width, int order, int T,
+                         int qsb, int qsh, int G, int hs, int Hq, const uint16_t* __restrict__ k,
                          const uint16_t* __restrict__ v, float* __restrict__ partials,
                          float* __restrict__ lse_out, int* __restrict__ counters,
                          uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv,
@@ -91,8 +92,9 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   // count the copies still in flight into the other.
   __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
   __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
+  __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
 
-  const int p = blockIdx.x, b = blockIdx.z;
+  const int p = blockIdx.x;
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
   const int qb = kh * G + 16 * slice;            // first query head of this workgroup
   const int Gs = min(16, G - 16 * slice);        // query heads of this workgroup
@@ -100,11 +102,14 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = lane & 15, qg = lane >> 4;
   const int start = p * T;
+  OrderedSequence seq{int(blockIdx.z), 0};
+  if (order >= 0) seq = ordered_sequence(lengths, int(gridDim.z), int(blockIdx.z), order, slens);
+  const int b = seq.b;
   // The partition's table entries do not depend on the length: fetch them
   // together with it, so the first KV loads wait for one round trip.
   PageWindow<2> pw;
   pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
-  const int length = lengths[b];
+  const int length = order >= 0 ? seq.length : lengths[b];
   const int end = min(start + T, length);
   const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
   const int64_t RS = int64_t(Hkv) * D;
@@ -453,8 +458,8 @@ struct TileP {
 template <int GP, bool kFused, int kMode>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
-                    const uint16_t* __restrict__ q, int tsb, int width, int T, int qsb, int qsh,
-                    int G, int hs, int Hq, const uint16_t* __restrict__ k,
+                    const uint16_t* __restrict__ q, int tsb, int width, int order, int T, int qsb,
+                    int qsh, int G, int hs, int Hq, const uint16_t* __restrict__ k,
                     const uint16_t* __restrict__ v, float* __restrict__ partials,
                     float* __restrict__ lse_out, int* __restrict__ counters,
                     uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv, int splits,
@@ -471,8 +476,9 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
   __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
   __shared__ __attribute__((aligned(16))) char ps[kTerms][16 * P::kPitch];
+  __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
 
-  const int p = blockIdx.x, b = blockIdx.z;
+  const int p = blockIdx.x;
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
   const int qb = kh * G + 16 * slice;
   const int Gs = min(16, G - 16 * slice);
@@ -480,9 +486,12 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = lane & 15, qg = lane >> 4;
   const int start = p * T;
+  OrderedSequence seq{int(blockIdx.z), 0};
+  if (order >= 0) seq = ordered_sequence(lengths, int(gridDim.z), int(blockIdx.z), order, slens);
+  const int b = seq.b;
   PageWindow<2> pw;
   pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
-  const int length = lengths[b];
+  const int length = order >= 0 ? seq.length : lengths[b];
   const int end = min(start + T, length);
   const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
   const int64_t RS = int64_t(Hkv) * D;
@@ -1056,7 +1065,50 @@ struct PartitionArgs {
   float* maxima;
   int Hq, Hkv, G, hs, splits, T;
   float scale, c;
+  int order = -1;  // batch order of the multi-tile kernels (batch_order)
 };
+
+// Compute units of the current device, queried once per device.
+int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      n = -1;
+    }
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// `order` of ordered_sequence (pd_device.h) for a multi-tile launch over
+// `grid` = (splits, kv heads x slices, batch) at two workgroups per CU:
+// * CUs / (grid.x * grid.y) when the whole grid is resident and rows z and
+//   z + that share CUs;
+// * 0 (longest first) for up to four rounds of workgroups;
+// * -1 (sequence z) when every workgroup has a CU to itself, the batch has one
+//   sequence or more than kMaxOrderedBatch, the CU count is unknown, or the
+//   grid runs more than four rounds.  There the ranking's extra round trip at
+//   the start of every workgroup costs more than the order gains: with 8192
+//   mostly short workgroups (batch 128, lengths up to 4096, D 64, 16 kv heads,
+//   4 fixed partitions) it took the call from 228 to 275 us, and sorting the
+//   batch on the host gained nothing there.
+int batch_order(dim3 grid) {
+  const int B = int(grid.z);
+  if (B < 2 || B > kMaxOrderedBatch) return -1;
+  const int cus = device_cu_count();
+  if (cus <= 0) return -1;
+  const int64_t xy = int64_t(grid.x) * grid.y, n = xy * B;
+  if (n <= cus || n > 8 * int64_t(cus)) return -1;
+  if (n <= 2 * int64_t(cus) && cus % xy == 0) return int(cus / xy);
+  return 0;
+}
 
 template <int D>
 void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
@@ -1080,14 +1132,14 @@ void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionAr
 #define PD_LAUNCH_GP(GPV)                                                                      \
   if constexpr (D == 256)                                                                      \
     hipLaunchKernelGGL((matched_cols_kernel<GPV, kFused, kMode>), grid, dim3(kThreads), 0,      \
-                       stream, a.table, a.lengths, a.q, a.tsb, a.width, a.T, a.qsb, a.qsh,     \
-                       a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,        \
+                       stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb,   \
+                       a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out, \
                        a.maxima, a.Hkv, a.splits, a.scale, a.c);                               \
   else                                                                                         \
     hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused, kMode>), grid, dim3(kThreads), \
-                       0, stream, a.table, a.lengths, a.q, a.tsb, a.width, a.T, a.qsb, a.qsh, \
-                       a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,       \
-                       a.maxima, a.Hkv, a.splits, a.scale, a.c)
+                       0, stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T,      \
+                       a.qsb, a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, \
+                       a.out, a.maxima, a.Hkv, a.splits, a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_GP(1); break;
     case 2: PD_LAUNCH_GP(2); break;
@@ -1154,6 +1206,7 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
     }
     return launch_status(what);
   }
+  a.order = batch_order(grid);
   switch (head_dim * 2 + (fused ? 1 : 0)) {
     case 128: launch_partition_d<64, false>(gp, grid, st, a); break;
     case 129: launch_partition_d<64, true>(gp, grid, st, a); break;
@@ -1271,6 +1324,7 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
                   nullptr, static_cast<uint16_t*>(out), maxima, num_heads, num_kv_heads, G, hs,
                   kSplitMode ? parts : 1, T, float(scale), float(scale * 1.4426950408889634)};
   const dim3 grid(kSplitMode ? parts : 1, num_kv_heads * hs, batch);
+  a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int gp = padded_group(G < 16 ? G : 16);
   constexpr int kMode = kSplitMode ? kSplit : kBase;

@@ -1,0 +1,105 @@
+"""Batch order of the multi-tile kernels, on the GPU.
+
+With more workgroups than CUs, matched_partition_kernel and matched_cols_kernel hand the
+grid's batch rows to the sequences in order of length (ordered_sequence in pd_device.h):
+longest first when the grid runs in two to four rounds, long paired with short on a CU
+when the whole grid is resident; past four rounds the batch keeps its order.  Which workgroup runs an item must not change a bit of the
+result.  Each case runs a batch large enough to switch the ordering on (the mode named
+is the one a 256-CU device takes) and compares every output row, bit for bit, with the
+same sequence run alone (batch 1, where the order is the identity), under the same plan.
+Lengths include zeros, ties and page boundaries; the unused pool holds NaN.
+"""
+import numpy as np
+import pytest
+import torch
+
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X GPU", allow_module_level=True)
+
+from gpu_cases import assert_close_dense, pooled_case, torch_dense
+from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
+from paged_decode.runtime import allocate_resources, paged_decode
+from paged_decode.spec import DecodeSpec
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16)
+
+
+def _lengths(batch, capacity, seed):
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(1, capacity + 1, size=batch)
+    lengths[rng.permutation(batch)[: batch // 8]] = 0
+    ties = rng.permutation(batch)[: batch // 4]
+    lengths[ties] = lengths[ties[0]]                 # a quarter of the batch ties
+    special = [1, 255, 256, 257, capacity - 1, capacity]
+    lengths[:len(special)] = special
+    return lengths.astype(np.int32)
+
+
+def _one(g, b):
+    q, k, v, table, lens = g
+    return q[b:b + 1], k, v, table[b:b + 1], lens[b:b + 1]
+
+
+def _check_rows(full, g, alone):
+    for b in range(full.shape[0]):
+        out = alone(_one(g, b))
+        assert torch.equal(_bits(out[0]), _bits(full[b])), f"sequence {b}"
+
+
+# (dim, hq, hkv, batch, capacity): mode on 256 CUs for one split per sequence
+MATCHED = [
+    (128, 32, 8, 64, 2048),    # 512 workgroups, resident: rows z and z + 32 paired
+    (128, 8, 8, 48, 2048),     # 384 workgroups: rows 16..31 alone on their CU, 32 paired
+    (256, 32, 4, 128, 2048),   # 512 workgroups (matched_cols_kernel): z and z + 64 paired
+    (64, 16, 16, 128, 1024),   # 2048 workgroups: longest first
+]
+
+
+@pytest.mark.parametrize("dim,hq,hkv,batch,capacity", MATCHED)
+def test_matched_rows_do_not_depend_on_the_batch_order(dim, hq, hkv, batch, capacity):
+    lengths = _lengths(batch, capacity, seed=dim + batch)
+    g = pooled_case(lengths, hq, hkv, dim, capacity, pool_pages=batch * capacity // 256 + 64,
+                    seed=batch)
+    res = allocate_matched_resources(DecodeSpec(batch, hq, hkv, dim, capacity), "cuda",
+                                     num_splits=1)
+    assert res.plan.tokens_per_split > res.plan.tile_tokens   # the multi-tile kernels
+    full = matched_decode(*g, resources=res).clone()
+    assert_close_dense(full, torch_dense(*g))
+    single = allocate_matched_resources(DecodeSpec(1, hq, hkv, dim, capacity), "cuda",
+                                        num_splits=1)
+    assert single.plan.tokens_per_split == res.plan.tokens_per_split
+    _check_rows(full, g, lambda c: matched_decode(*c, resources=single))
+
+
+def test_fused_matched_rows_do_not_depend_on_the_batch_order():
+    dim, hq, hkv, batch, capacity = 256, 16, 4, 64, 2048
+    lengths = _lengths(batch, capacity, seed=7)
+    g = pooled_case(lengths, hq, hkv, dim, capacity, pool_pages=batch * 8 + 64, seed=7)
+    # 2 splits x 4 kv heads x 64 sequences = 512 workgroups, rows z and z + 32 paired
+    res = allocate_matched_resources(DecodeSpec(batch, hq, hkv, dim, capacity), "cuda",
+                                     num_splits=2, fused=True)
+    full = matched_decode(*g, resources=res).clone()
+    single = allocate_matched_resources(DecodeSpec(1, hq, hkv, dim, capacity), "cuda",
+                                        num_splits=2)
+    _check_rows(full, g, lambda c: matched_decode(*c, resources=single))
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+@pytest.mark.parametrize("dim,hq,hkv,batch,capacity", [
+    (256, 32, 4, 128, 2048),   # base: 512 resident workgroups; splitk: 1024, longest first
+    (64, 16, 16, 128, 2048),   # base: 2048 workgroups, longest first; splitk: 4096, as given
+    (128, 32, 8, 40, 2048),    # base: 320 workgroups, rows 8..31 alone on their CU
+])
+def test_paged_rows_do_not_depend_on_the_batch_order(backend, dim, hq, hkv, batch, capacity):
+    lengths = _lengths(batch, capacity, seed=batch + hkv)
+    g = pooled_case(lengths, hq, hkv, dim, capacity, pool_pages=batch * capacity // 256 + 64,
+                    seed=hkv)
+    res = allocate_resources(DecodeSpec(batch, hq, hkv, dim, capacity), "cuda", backend)
+    full = paged_decode(*g, resources=res, backend=backend).clone()
+    assert_close_dense(full, torch_dense(*g))
+    single = allocate_resources(DecodeSpec(1, hq, hkv, dim, capacity), "cuda", backend)
+    _check_rows(full, g, lambda c: paged_decode(*c, resources=single, backend=backend))
