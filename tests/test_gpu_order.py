@@ -103,3 +103,44 @@ def test_paged_rows_do_not_depend_on_the_batch_order(backend, dim, hq, hkv, batc
     assert_close_dense(full, torch_dense(*g))
     single = allocate_resources(DecodeSpec(1, hq, hkv, dim, capacity), "cuda", backend)
     _check_rows(full, g, lambda c: paged_decode(*c, resources=single, backend=backend))
+
+
+CAPTURE_FIRST = r"""
+import sys
+sys.path[:0] = {paths!r}
+import torch
+from gpu_cases import pooled_case
+from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
+from paged_decode.spec import DecodeSpec
+import numpy as np
+lengths = np.random.default_rng(1).integers(0, 2049, size=64).astype(np.int32)
+g = pooled_case(lengths, 32, 8, 128, 2048, pool_pages=600, seed=1)
+res = allocate_matched_resources(DecodeSpec(64, 32, 8, 128, 2048), "cuda", num_splits=1)
+stream = torch.cuda.Stream()
+stream.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=stream):    # the library's first launch in this process
+    out = matched_decode(*g, resources=res)
+graph.replay()
+torch.cuda.synchronize()
+captured = out.clone()
+eager = matched_decode(*g, resources=res).clone()
+assert torch.equal(captured.view(torch.int16), eager.view(torch.int16))
+print("capture-first ok")
+"""
+
+
+def test_first_launch_of_the_process_under_graph_capture():
+    """The launcher queries the CU count on its first ordered launch; in a fresh process
+    whose first library call is captured into a graph, the capture must succeed and its
+    replay equal the eager call."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    paths = [here, root, os.path.join(root, "paged-decode-lab_amd")]
+    res = subprocess.run([sys.executable, "-c", CAPTURE_FIRST.format(paths=paths)],
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr[-3000:]
+    assert "capture-first ok" in res.stdout
