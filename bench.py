@@ -357,6 +357,8 @@ def profile_launches(torch, which, calls=50):
     written), used to scale FETCH_SIZE / WRITE_SIZE.  headline: partition and
     merge at the headline shape.  sweep: partition and merge of the bandwidth sweep.
     long: partition and merge at D256 GQA 4:1, B=1, context 131072 (KV from HBM).
+    edge: paged_decode's hip_base and hip_splitk on the edge-coverage batches (B=128,
+    a quarter of the lengths 0, the rest U[1, 4096]; D 64 MHA 16/16, D 256 GQA 32/4).
     """
     import numpy as np
     src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device="cuda")
@@ -390,6 +392,21 @@ def profile_launches(torch, which, calls=50):
             case["merge"]()
         torch.cuda.synchronize()
         del case
+    if "edge" in which:
+        from paged_decode.runtime import allocate_resources, paged_decode
+        from paged_decode.spec import DecodeSpec
+        rng4 = np.random.default_rng(4)
+        c4 = [0 if i % 4 == 0 else int(x) for i, x in enumerate(rng4.integers(1, 4097, size=128))]
+        for hq, hkv, dim in ((16, 16, 64), (32, 4, 256)):
+            q, k, v, table, lens = make_inputs(torch, 128, hq, hkv, dim, 4096, c4, 64)
+            spec = DecodeSpec(128, hq, hkv, dim, 4096)
+            for backend in ("hip_base", "hip_splitk"):
+                res = allocate_resources(spec, "cuda", backend)
+                for _ in range(10):
+                    paged_decode(q, k, v, table, lens, resources=res, backend=backend)
+                torch.cuda.synchronize()
+                del res
+            del q, k, v, table, lens
     torch.cuda.empty_cache()
     print(json.dumps({"profiled": which}))
 
@@ -403,7 +420,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the extra measurements")
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU run")
-    ap.add_argument("--profile", default=None, metavar="headline,sweep,long",
+    ap.add_argument("--profile", default=None, metavar="headline,sweep,long,edge",
                     help="only make eager launches for rocprofv3 (calibration copy + cases)")
     ap.add_argument("--require-idle-gpu", action="store_true",
                     help="refuse to run (before any GPU work) if amd-smi lists other processes")
