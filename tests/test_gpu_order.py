@@ -56,6 +56,8 @@ MATCHED = [
     (128, 8, 8, 48, 2048),     # 384 workgroups: rows 16..31 alone on their CU, 32 paired
     (256, 32, 4, 128, 2048),   # 512 workgroups (matched_cols_kernel): z and z + 64 paired
     (64, 16, 16, 128, 1024),   # 2048 workgroups: longest first
+    (128, 8, 8, 256, 512),     # 2048 workgroups, the largest batch that is ranked
+    (128, 8, 8, 257, 512),     # 2056 workgroups, one sequence too many: as given
 ]
 
 
@@ -72,6 +74,21 @@ def test_matched_rows_do_not_depend_on_the_batch_order(dim, hq, hkv, batch, capa
     single = allocate_matched_resources(DecodeSpec(1, hq, hkv, dim, capacity), "cuda",
                                         num_splits=1)
     assert single.plan.tokens_per_split == res.plan.tokens_per_split
+    _check_rows(full, g, lambda c: matched_decode(*c, resources=single))
+
+
+def test_two_sequences_over_many_splits():
+    """64 splits x 4 kv heads x 2 sequences = 512 workgroups: rows 0 and 1 share CUs."""
+    dim, hq, hkv, capacity = 256, 16, 4, 8192
+    lengths = np.array([8192, 3000], dtype=np.int32)
+    g = pooled_case(lengths, hq, hkv, dim, capacity, pool_pages=96, seed=2)
+    res = allocate_matched_resources(DecodeSpec(2, hq, hkv, dim, capacity), "cuda",
+                                     num_splits=64)
+    assert res.plan.tokens_per_split > res.plan.tile_tokens
+    full = matched_decode(*g, resources=res).clone()
+    assert_close_dense(full, torch_dense(*g))
+    single = allocate_matched_resources(DecodeSpec(1, hq, hkv, dim, capacity), "cuda",
+                                        num_splits=64)
     _check_rows(full, g, lambda c: matched_decode(*c, resources=single))
 
 
