@@ -73,6 +73,36 @@ struct MatchedShared {
 // Hkv * hs), so the base and fixed-split protocols also cover G > 16.
 constexpr int kMatched = 0, kBase = 1, kSplit = 2;
 
+// A partition without tokens, written directly: the values the full epilogue
+// derives from the untouched state (acc 0, running maximum -inf, denominator
+// 0), without its LDS exchange and barriers.  Matched: partial +0, LSE -inf;
+// base: output +0 (kernels.py:40); fixed split: acc +0, m -inf, l 0.  Plans
+// sized for a table capacity far above the live lengths have mostly such
+// partitions.  Not for the fused protocol, whose workgroups must count
+// themselves.
+template <int D, int kMode>
+__device__ __forceinline__ void write_empty_partition(int tid, int b, int Hq, int qb, int Gs,
+                                                      int splits, int p, float* partials,
+                                                      float* lse_out, uint16_t* out,
+                                                      float* maxima) {
+  for (int i = tid; i < Gs * D; i += kThreads) {
+    const int64_t row = int64_t(b) * Hq + qb + i / D;
+    if constexpr (kMode == kBase)
+      out[row * D + i % D] = 0;
+    else
+      partials[(row * splits + p) * D + i % D] = 0.f;
+  }
+  if (kMode != kBase && tid < Gs) {
+    const int64_t orow = (int64_t(b) * Hq + qb + tid) * splits + p;
+    if constexpr (kMode == kSplit) {
+      maxima[orow] = -INFINITY;
+      lse_out[orow] = 0.f;
+    } else {
+      lse_out[orow] = -INFINITY;
+    }
+  }
+}
+
 template <int D, int GP, bool kFused, int kMode>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
@@ -112,6 +142,13 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   const int length = order >= 0 ? seq.length : lengths[b];
   const int end = min(start + T, length);
   const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+  if constexpr (!kFused) {
+    if (count == 0) {
+      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, p, partials, lse_out, out,
+                                      maxima);
+      return;
+    }
+  }
   const int64_t RS = int64_t(Hkv) * D;
 
   // MFMA B operand of QK: the GQA group's query rows.
@@ -494,6 +531,13 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   const int length = order >= 0 ? seq.length : lengths[b];
   const int end = min(start + T, length);
   const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+  if constexpr (!kFused) {
+    if (count == 0) {
+      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, p, partials, lse_out, out,
+                                      maxima);
+      return;
+    }
+  }
   const int64_t RS = int64_t(Hkv) * D;
 
   bf16x8_t qf[C::kCH];
