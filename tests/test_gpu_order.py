@@ -161,3 +161,26 @@ def test_first_launch_of_the_process_under_graph_capture():
                          capture_output=True, text=True, timeout=300)
     assert res.returncode == 0, res.stderr[-3000:]
     assert "capture-first ok" in res.stdout
+
+
+@pytest.mark.parametrize("backend", ["matched", "hip_base", "hip_splitk"])
+def test_strided_query_rows_in_an_ordered_batch(backend):
+    """Q as a strided view (head stride 2D, row stride 2 Hq D) in an ordered batch gives the
+    same bits as contiguous Q: the permuted row index addresses Q through its strides."""
+    dim, hq, hkv, batch, capacity = 128, 32, 8, 64, 2048
+    lengths = _lengths(batch, capacity, seed=11)
+    q, k, v, table, lens = pooled_case(lengths, hq, hkv, dim, capacity,
+                                       pool_pages=batch * 8 + 64, seed=11)
+    wide = torch.zeros((batch, hq, 2 * dim), dtype=q.dtype, device=q.device)
+    wide[..., :dim] = q
+    strided = wide[..., :dim]
+    assert not strided.is_contiguous()
+    spec = DecodeSpec(batch, hq, hkv, dim, capacity)
+    if backend == "matched":
+        res = allocate_matched_resources(spec, "cuda", num_splits=1)
+        call = lambda qq: matched_decode(qq, k, v, table, lens, resources=res).clone()
+    else:
+        res = allocate_resources(spec, "cuda", backend)
+        call = lambda qq: paged_decode(qq, k, v, table, lens, resources=res,
+                                       backend=backend).clone()
+    assert torch.equal(_bits(call(strided)), _bits(call(q)))
