@@ -236,28 +236,49 @@ struct Matched {
 };
 
 // V rows sit in LDS unpadded (kPitch = 2D bytes), with the 16-byte pieces of
-// each row permuted: piece p of row r is stored at position p ^ vswz(r).  A
-// transposed read (ds_read_b64_tr_b16) addresses 4 consecutive rows at the
-// same two pieces; with vswz(r) = 2 (r % 4) those land on 8 different piece
-// positions modulo 8, i.e. 128 distinct bytes: all banks, no conflict.
-__device__ __forceinline__ int vswz(int row) { return 2 * (row & 3); }
+// each row permuted: piece p of row r is stored at position p ^ vswz(r).  The
+// LDS serves 32 lanes of a ds_read_b64_tr_b16 per clock, 256 bytes over 64
+// four-byte banks; each lane's 8 bytes are two pieces' halves of one row, and
+// each row's 4 lanes read two adjacent pieces (32 bytes).  The 32 lanes must
+// therefore land on 8 distinct 32-byte bank groups.  Which 8 rows they read
+// depends on the kernel:
+// * row groups (matched_partition_kernel): lanes 0-15 read rows 0-3 of a
+//   16-row group, lanes 16-31 rows 4-7;
+// * column split (matched_tile_kernel, matched_cols_kernel): lanes 0-15 read
+//   rows 0-3 of a 32-token k-step and lanes 16-31 rows 8-11 (rows 4-7 and
+//   12-15 in the second read of the step, which takes the same swizzle).
+// Rows of 2D >= 256 bytes start on bank 0, so the swizzle alone spreads them:
+// bits 0-1 of the row pick one of 4 pairs of pieces, and bit 2 (row groups)
+// or bit 3 (column split) one of two 128-byte halves.  Rows of 128 bytes
+// (D = 64) alternate between the two halves by their own address (bit 0),
+// so the swizzle spreads the rows of one half over its 4 pairs of pieces.
+template <int D, bool kColSplit>
+__device__ __forceinline__ int vswz(int row) {
+  if constexpr (D >= 128)
+    return 2 * (row & 3) + 8 * ((row >> (kColSplit ? 3 : 2)) & 1);
+  else if constexpr (kColSplit)
+    return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1));
+  else
+    return 2 * ((row >> 1) & 3);
+}
 
 // Source byte offset (tile-relative) of the 16 bytes that DMA copy i of
 // wavefront w places at LDS position 16 * (64 i + lane) of its rows.
-template <int D, int GP>
+template <int D, int GP, bool kColSplit>
 __device__ __forceinline__ int v_copy_offset(int i, int lane, int w, int RS) {
   using C = Matched<D, GP>;
   const int slot = 64 * i + lane;
   const int row = slot / C::kPieces, pos = slot % C::kPieces;
-  return ((w * C::kTW + row) * RS + 8 * (pos ^ vswz(row))) * 2;
+  return ((w * C::kTW + row) * RS + 8 * (pos ^ vswz<D, kColSplit>(row))) * 2;
 }
 
 // Byte offset within a V row of this lane's 8 bytes of a transposed read of
 // the 16 columns from col0 (a multiple of 16): lane l % 4 = b reads columns
-// col0 + 4b .. +3, in rows r with r % 4 = rmod.
-__device__ __forceinline__ int v_read_offset(int col0, int lane, int rmod) {
+// col0 + 4b .. +3 of a row whose index within its 16-row group is `row`.
+template <int D, bool kColSplit>
+__device__ __forceinline__ int v_read_offset(int col0, int lane, int row) {
   const int b = lane & 3;
-  return 16 * (((col0 >> 3) + (b >> 1)) ^ (2 * rmod)) + 8 * (b & 1);
+  return 16 * (((col0 >> 3) + (b >> 1)) ^ vswz<D, kColSplit>(row)) + 8 * (b & 1);
 }
 
 template <int D, int GP>

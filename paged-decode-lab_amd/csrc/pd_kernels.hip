@@ -167,7 +167,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP>(i, lane, w, int(RS));
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, false>(i, lane, w, int(RS));
   // This lane's transposed-read row within its wavefront's LDS rows (rows
   // 4qg + qh/4 of each 16-row group, so row % 4 = qh / 4).
   const int trb = w * C::kSlot + (4 * qg + (qh >> 2)) * C::kPitch;
@@ -305,7 +305,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
     for (int g = 0; g < C::kNG; g += 2) {
 #pragma unroll
       for (int j = 0; j < C::kNB; ++j) {
-        const int col = v_read_offset(16 * j, lane, qh >> 2);
+        const int col = v_read_offset<D, false>(16 * j, lane, 4 * qg + (qh >> 2));
         const short4_t lo = lds_read_tr(base + 16 * g * C::kPitch + col);
         const short4_t hi = lds_read_tr(base + 16 * (g + 1) * C::kPitch + col);
         const bf16x8_t bv = __builtin_bit_cast(
@@ -551,7 +551,7 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP>(i, lane, w, int(RS));
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, true>(i, lane, w, int(RS));
 
   floatx4_t acc[P::kNBW];  // O[head 4*qg + r][64w + 16j + qh]
 #pragma unroll
@@ -690,7 +690,8 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       short4_t lo[P::kNBW], hi[P::kNBW];
 #pragma unroll
       for (int j = 0; j < P::kNBW; ++j) {
-        const uint32_t vj = vb + v_read_offset(w * P::kCols + 16 * j, lane, qh >> 2);
+        const uint32_t vj =
+            vb + v_read_offset<D, true>(w * P::kCols + 16 * j, lane, 8 * (qg & 1) + (qh >> 2));
         lo[j] = lds_read_tr_at<kOff>(vj);
         hi[j] = lds_read_tr_at<kOff + 4 * C::kPitch>(vj);
       }
@@ -894,7 +895,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   const int kl = kline_offset(lane, int(RS)) + w * C::kTW * int(RS) * 2;
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP>(i, lane, w, int(RS));
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, true>(i, lane, w, int(RS));
 
   KTile<D, GP> R;
   {
@@ -973,7 +974,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     const char* hi_row = vs + (t_hi / C::kTW) * C::kSlot + (t_hi % C::kTW) * C::kPitch;
 #pragma unroll
     for (int j = 0; j < P::kNBW; ++j) {
-      const int cb = v_read_offset(w * P::kCols + 16 * j, lane, qh >> 2);
+      const int cb = v_read_offset<D, true>(w * P::kCols + 16 * j, lane, 8 * (qg & 1) + (qh >> 2));
       const short4_t lo = lds_read_tr(lo_row + cb);
       const short4_t hi = lds_read_tr(hi_row + cb);
       const bf16x8_t bv = __builtin_bit_cast(

@@ -76,44 +76,73 @@ def test_operand_layout_loads_touch_half_lines_and_whole_line_loads_whole_ones()
         assert len({line_of(a) for a in operand[start:start + 8]}) == 8
 
 
-def vswz(row):
-    return 2 * (row & 3)
+def vswz(dim, col_split, row):
+    if dim >= 128:
+        return 2 * (row & 3) + 8 * ((row >> (3 if col_split else 2)) & 1)
+    if col_split:
+        return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1))
+    return 2 * ((row >> 1) & 3)
+
+
+def v_read_offset(dim, col_split, col0, lane, row):
+    b = lane & 3
+    return 16 * (((col0 >> 3) + (b >> 1)) ^ vswz(dim, col_split, row)) + 8 * (b & 1)
+
+
+def read_row(col_split, lane, step, second):
+    """Row (within the wavefront's LDS rows) that `lane` reads in a transposed read:
+    row groups: rows 4(L/16) + (L%16)/4 of 16-row group `step`; column split: rows
+    8(L/16) + (L%16)/4 (+4 in the second read) of 32-token k-step `step`."""
+    c = (lane & 15) >> 2
+    if col_split:
+        return 32 * step + 8 * (lane >> 4) + c + (4 if second else 0)
+    return 16 * step + 4 * (lane >> 4) + c
 
 
 @pytest.mark.parametrize("dim", [64, 128, 256])
-def test_v_rows_swizzle_round_trips_and_transposed_reads_are_conflict_free(dim):
+@pytest.mark.parametrize("col_split", [False, True])
+def test_v_rows_swizzle_round_trips_and_transposed_reads_are_conflict_free(dim, col_split):
     """pd_device.h stores V rows in LDS unpadded, 16-byte piece p of row r at position
     p ^ vswz(r) (v_copy_offset), and reads them back with v_read_offset.  Every copy
-    lane fills one distinct position, every transposed read finds the logical columns
-    it asks for, and the 16 lanes of a read hit 128 distinct bytes (all banks)."""
+    lane fills one distinct position and every transposed read finds the logical columns
+    it asks for.  The LDS serves 32 lanes of a read per clock over 64 four-byte banks
+    (256 bytes); the 32 lanes of each half-wavefront hit 256 distinct bytes, for the
+    row-group reads of matched_partition_kernel and the column-split reads of the tile
+    and D=256 kernels.  (The previous 4-row swizzle gave 2-way conflicts here, which
+    SQ_LDS_BANK_CONFLICT showed on MI355X.)"""
     pieces = dim // 8
     pitch = 16 * pieces
-    rows = 16384 // dim // 4               # rows per wavefront
-    copies = rows * pitch // 1024
-    # DMA: LDS position 16 * (64 i + lane) <- global (row, piece pos ^ vswz(row))
+    tile = 16384 // dim
+    tw = tile // 4                         # rows per wavefront
+    copies = tw * pitch // 1024
     stored = {}
     for i in range(copies):
         for lane in range(64):
             slot = 64 * i + lane
             row, pos = divmod(slot, pieces)
-            stored[(row, pos)] = (row, pos ^ vswz(row))
-    assert len(stored) == rows * pieces
-    assert sorted(stored.values()) == [(r, p) for r in range(rows) for p in range(pieces)]
+            stored[(row, pos)] = (row, pos ^ vswz(dim, col_split, row))
+    assert len(stored) == tw * pieces
+    assert sorted(stored.values()) == [(r, p) for r in range(tw) for p in range(pieces)]
 
-    def v_read_offset(col0, lane, rmod):
-        b = lane & 3
-        return 16 * (((col0 >> 3) + (b >> 1)) ^ (2 * rmod)) + 8 * (b & 1)
+    def address(row):
+        """Byte address of `row` of the tile: wavefront row // tw's slot, then the row."""
+        return (row // tw) * tw * pitch + (row % tw) * pitch
 
-    for first_row in range(0, rows, 4):
-        for col0 in range(0, dim, 16):
-            banks = set()
-            for lane in range(16):
-                c, b = lane >> 2, lane & 3
-                row = first_row + c
-                off = v_read_offset(col0, lane, row % 4)
-                pos, within = divmod(off, 16)
-                # the logical piece stored there holds columns col0 + 4b .. + 3
-                assert stored[(row, pos)] == (row, (col0 + 4 * b) // 8)
-                assert within == 8 * (b & 1)
-                banks.add((row * pitch + off) % 128)
-            assert len(banks) == 16             # 16 x 8 bytes = 128 distinct bytes
+    steps = (tile // 32) if col_split else (tw // 16)
+    for step in range(steps):
+        for second in ((False, True) if col_split else (False,)):
+            cols = range(0, dim, 16)
+            for col0 in cols:
+                for half in (0, 32):
+                    chunks = set()
+                    for lane in range(half, half + 32):
+                        row = read_row(col_split, lane, step, second)
+                        local = row % tw if col_split else row
+                        off = v_read_offset(dim, col_split, col0, lane, local % 16)
+                        pos, within = divmod(off, 16)
+                        b = lane & 3
+                        assert stored[(local, pos)] == (local, (col0 + 4 * b) // 8)
+                        assert within == 8 * (b & 1)
+                        base = address(row) if col_split else row * pitch
+                        chunks.add(((base + off) % 256) // 8)
+                    assert len(chunks) == 32, (step, second, col0, half)
