@@ -110,6 +110,7 @@ def test_fused_matched_rows_do_not_depend_on_the_batch_order():
     (256, 32, 4, 128, 2048),   # base: 512 resident workgroups; splitk: 1024, longest first
     (64, 16, 16, 128, 2048),   # base: 2048 workgroups, longest first; splitk: 4096, as given
     (128, 32, 8, 40, 2048),    # base: 320 workgroups, rows 8..31 alone on their CU
+    (128, 64, 2, 128, 1024),   # 32-head groups in two 16-head slices: 512 workgroups
 ])
 def test_paged_rows_do_not_depend_on_the_batch_order(backend, dim, hq, hkv, batch, capacity):
     lengths = _lengths(batch, capacity, seed=batch + hkv)
