@@ -168,8 +168,8 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   int voff[C::kDma];
 #pragma unroll
   for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, false>(i, lane, w, int(RS));
-  // This lane's transposed-read row within its wavefront's LDS rows (rows
-  // 4qg + qh/4 of each 16-row group, so row % 4 = qh / 4).
+  // This lane's transposed-read row within its wavefront's LDS rows: row
+  // 4qg + qh/4 of each 16-row group (the row v_read_offset swizzles by).
   const int trb = w * C::kSlot + (4 * qg + (qh >> 2)) * C::kPitch;
 
   floatx4_t acc[C::kNB];   // O[head 4*qg + r][16j + qh]

@@ -1,4 +1,4 @@
-"""Lane arithmetic of the single-tile kernel's whole-line K loads, on the CPU.
+"""Lane arithmetic of the K whole-line loads and the V-row LDS swizzle, on the CPU.
 
 pd_device.h loads each 16-row group of K as whole 128-byte lines (kline_offset:
 lane S gets row 8sh + S/8, 16-byte chunk S%8 of line h), then lines_to_mfma
@@ -9,6 +9,8 @@ runs the same index arithmetic on NumPy lanes and checks the result against the
 operand layout the QK MFMA reads (lane 16g + r: row r, chunk 4ch + g), for every
 head dim.  On the GPU the kernel's outputs are bit-identical to loads made
 directly in the operand layout (tests/test_gpu_matched.py and the paged tests).
+The V-row swizzle test at the end checks the LDS copy/read round trip and the
+bank spread of the transposed reads.
 """
 import numpy as np
 import pytest
