@@ -39,7 +39,7 @@ enum pd_status { PD_OK = 0, PD_EINVAL = 1, PD_ELAUNCH = 2 };
 
 #define PD_PAGE_SIZE 256      /* spec.py:6 */
 #define PD_PARTITION_SIZE 1024 /* spec.py:7 */
-#define PD_ABI_VERSION 2
+#define PD_ABI_VERSION 3
 
 /* Split-KV plan; field meanings follow SplitKVPlan (splitkv_plan.py:15-23). */
 typedef struct pd_plan {
@@ -94,8 +94,10 @@ int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 
 /* Stable LSE merge; replaces _lse_merge (matched_splitkv.py:101-127) as
  * launched by matched_decode (:147-149).  Writes out bf16 [batch, num_heads,
- * head_dim].  lse_lanes is the plan's lane count (a power of two <= splits'
- * next power of two); it only changes float32 summation order. */
+ * head_dim].  lse_lanes is the plan's lane count, a power of two in [1, 64]
+ * no larger than the next power of two of splits.  It sets the float32
+ * summation order of the log-sum, as in the reference: lane j sums splits
+ * j, j + lse_lanes, ... in order, then a halving tree adds the lanes. */
 int pd_lse_merge(const float* partials, const float* lse, void* out,
                  int32_t batch, int32_t num_heads, int32_t head_dim, int32_t splits,
                  int32_t lse_lanes, pd_stream_t stream);
@@ -108,7 +110,8 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
  * all zero before the first call; every completed call leaves it all zero
  * again, so the launch can be replayed from a graph without a reset.  Calls
  * that share `counters` must not run concurrently.  Writes partials, lse and
- * out bf16 [batch, num_heads, head_dim]. */
+ * out bf16 [batch, num_heads, head_dim].  The merge sums with the plan's
+ * lse_lanes, min(next_pow2(splits), 32 if head_dim % 128 == 0 else 16). */
 int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                       const void* k, const void* v,
                       const int32_t* table, int64_t table_stride_b, int32_t table_width,
@@ -168,13 +171,17 @@ int pd_store_kv(const void* key, int64_t key_stride, const void* value, int64_t 
  * 256-slot pages; replaces the index_copy_ of PagedHybridCache.update
  * (src/paged_decode/hybrid.py:63-72).  Element (b, h, s, d) goes to page
  * table[b, positions[s] / 256], slot positions[s] % 256, kv head h.  `positions`
- * is int64 [steps]; a negative position or table entry, or a page index at or
- * past table_width, skips the row.  head_dim in {64, 128, 256}; strides in
- * elements, multiples of 8; pointers 16-byte aligned. */
+ * is int64 [steps]; k_pages and v_pages hold num_pages pages each.  A negative
+ * position, a page index at or past table_width, or a table entry outside
+ * [0, num_pages) skips the row (the reference's index_copy_ rejects such an
+ * index; here nothing is written outside the pool).  head_dim in
+ * {64, 128, 256}; strides in elements, multiples of 8; pointers 16-byte
+ * aligned. */
 int pd_store_kv_pages(const void* key, int64_t key_stride_b, int64_t key_stride_h,
                       int64_t key_stride_s, const void* value, int64_t value_stride_b,
                       int64_t value_stride_h, int64_t value_stride_s, void* k_pages,
-                      void* v_pages, const int32_t* table, int64_t table_stride_b,
+                      void* v_pages, int64_t num_pages, const int32_t* table,
+                      int64_t table_stride_b,
                       int32_t table_width, const int64_t* positions, int32_t batch,
                       int32_t num_kv_heads, int32_t steps, int32_t head_dim, pd_stream_t stream);
 

@@ -114,15 +114,29 @@ __device__ __forceinline__ void buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, int
 // Shared by the standalone merge kernel and the fused decode so that both give
 // bit-identical outputs.
 //
+// The plan's LSE lane count for a split count and head dim:
+// min(next_pow2(splits), 32 if D % 128 == 0 else 16) (splitkv_plan.py:52-56).
+__device__ __host__ __forceinline__ int plan_lse_lanes(int splits, int D) {
+  int lanes = 1;
+  while (lanes < splits) lanes <<= 1;
+  const int cap = D % 128 == 0 ? 32 : 16;
+  return lanes < cap ? lanes : cap;
+}
+
 // Merge weights of one (b, h) row, computed by one full wavefront: lane owns
 // splits `lane` and `lane + 64` (splits <= 128).  M = max lse (-inf -> 0),
 // S = sum exp(lse - M), L = ln S + M (+inf when S == 0), w_p = exp(lse_p - L)
 // (matched_splitkv.py:107-120; an all-empty row gets w = 0 everywhere).  The
 // two loads are unconditional buffer loads (zero past the row, replaced by
 // -inf), so they issue without a branch and queue behind earlier loads.
+// S is summed in the reference's float32 order for `lanes` (a power of two,
+// 1..64): lane j < lanes adds e_j, e_{j+lanes}, e_{j+2 lanes}, ... in that
+// order (:114-118), then a halving tree over the lanes adds lane j + half to
+// lane j (:119), here an xor butterfly (float addition commutes exactly).
+// Terms past the last split are exact zeros, so they are not added.
 template <bool kCoherent>
-__device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lane,
-                                            float& w0, float& w1) {
+__device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lanes,
+                                            int lane, float& w0, float& w1) {
   const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(lrow, splits * 4);
   float a[1], c[1];
   buffer_load_f32<1, kCoherent>(rsrc, lane * 4, a);
@@ -131,7 +145,15 @@ __device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int 
   const float v1 = lane + 64 < splits ? c[0] : -INFINITY;
   float mx = wave_max(fmaxf(v0, v1));
   if (mx == -INFINITY) mx = 0.f;
-  const float total = wave_sum(exp_fast(v0 - mx) + exp_fast(v1 - mx));
+  const float e0 = exp_fast(v0 - mx), e1 = exp_fast(v1 - mx);
+  float s = e0;
+  const int terms = (splits + lanes - 1) / lanes;
+  for (int t = 1; t < terms; ++t) {
+    const int off = t * lanes;  // lanes j < `lanes` read split j + off < 128
+    s += __shfl(off < 64 ? e0 : e1, (lane + off) & 63);
+  }
+  for (int m = lanes >> 1; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+  const float total = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 0));
   const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
   w0 = exp_fast(v0 - logsum);
   w1 = exp_fast(v1 - logsum);
@@ -389,6 +411,16 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt field");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// s_waitcnt vmcnt(0): every vector-memory load AND store this wavefront has
+// issued has completed (on gfx9-family GPUs stores are counted in vmcnt too).
+// A device-scope (sc1) store has then been written through to the coherence
+// point, so a workgroup on another XCD that reads the line with a
+// device-scope load sees it.  A barrier or a workgroup-scope fence does not
+// wait for other wavefronts' stores: each wavefront waits for its own.
+__device__ __forceinline__ void wait_memory() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Waits for every outstanding LDS read (lgkmcnt(0)) and makes the values

@@ -428,14 +428,18 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
 
   if constexpr (kFused) {
     // Split-completion count.  Every partial and LSE value exchanged between
-    // workgroups is written and read with device-scope (sc1) accesses.  The
-    // barrier waits until this workgroup's stores have completed before thread
-    // 0 increments the counter, and the last workgroup issues its loads only
-    // after its increment returned splits - 1, i.e. after every other
-    // workgroup's stores completed.  No cache-wide writeback or invalidate is
-    // needed, so the KV tiles other calls keep in L2 stay resident.
+    // workgroups is written and read with device-scope (sc1) accesses.  Each
+    // wavefront waits until its own stores have completed (vmcnt(0): written
+    // through to the coherence point), then the barrier orders all four
+    // wavefronts' completed stores before thread 0 increments the counter.
+    // The last workgroup issues its loads only after its increment returned
+    // splits - 1, i.e. after every other workgroup's stores completed, and
+    // those loads are device-scope, so they are served from the coherence
+    // point rather than from a line this XCD's caches may hold from an
+    // earlier call.  No cache-wide writeback or invalidate is needed, so the
+    // KV tiles other calls keep in L2 stay resident.
     int* counter = counters + int64_t(b) * Hkv + kh;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    wait_memory();
     __syncthreads();
     if (tid == 0)
       sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -450,7 +454,10 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
       float w0 = 0.f, w1 = 0.f, acc[kV];
       merge_splits<kV, true>(
           partials + (row0 + hh) * splits * D, D, lane * kV, splits,
-          [&] { lse_weights<true>(lse_out + (row0 + hh) * splits, splits, lane, w0, w1); },
+          [&] {
+            lse_weights<true>(lse_out + (row0 + hh) * splits, splits, plan_lse_lanes(splits, D),
+                              lane, w0, w1);
+          },
           [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
       uint16_t* dst = out + (row0 + hh) * D + lane * kV;
 #pragma unroll
@@ -806,7 +813,7 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     // Split-completion count and the last workgroup's merge, exactly as in
     // matched_partition_kernel.
     int* counter = counters + int64_t(b) * Hkv + kh;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    wait_memory();
     __syncthreads();
     if (tid == 0)
       sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -819,7 +826,10 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       float w0 = 0.f, w1 = 0.f, mrg[kV];
       merge_splits<kV, true>(
           partials + (row0 + hh) * splits * D, D, lane * kV, splits,
-          [&] { lse_weights<true>(lse_out + (row0 + hh) * splits, splits, lane, w0, w1); },
+          [&] {
+            lse_weights<true>(lse_out + (row0 + hh) * splits, splits, plan_lse_lanes(splits, D),
+                              lane, w0, w1);
+          },
           [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, mrg);
       uint16_t* dst = out + (row0 + hh) * D + lane * kV;
 #pragma unroll
@@ -1014,14 +1024,14 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 template <int D, int kBatch>
 __global__ void __launch_bounds__(64)
 lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ lse,
-                 uint16_t* __restrict__ out, int splits) {
+                 uint16_t* __restrict__ out, int splits, int lanes) {
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x;
   const int dd = blockIdx.y * 64 + lane;
   float w0 = 0.f, w1 = 0.f, acc[1];
   merge_splits<1, false, kBatch>(
       partials + row * splits * D, D, dd, splits,
-      [&] { lse_weights<false>(lse + row * splits, splits, lane, w0, w1); },
+      [&] { lse_weights<false>(lse + row * splits, splits, lanes, lane, w0, w1); },
       [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
   out[row * D + dd] = uint16_t(bf16_bits(acc[0]));
 }
@@ -1302,8 +1312,10 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
   if (!pd::valid_head_dim(head_dim))
     return pd::fail(PD_EINVAL, "custom decode supports head_dim 64, 128, or 256");
   if (splits < 1 || splits > 128) return pd::fail(PD_EINVAL, "splits must be in [1,128]");
-  if (lse_lanes < 1 || (lse_lanes & (lse_lanes - 1)))
-    return pd::fail(PD_EINVAL, "lse_lanes must be a power of two");
+  if (lse_lanes < 1 || lse_lanes > 64 || (lse_lanes & (lse_lanes - 1)))
+    return pd::fail(PD_EINVAL, "lse_lanes must be a power of two in [1, 64]");
+  if (lse_lanes > 1 && lse_lanes / 2 >= splits)
+    return pd::fail(PD_EINVAL, "lse_lanes must not exceed the next power of two of splits");
   if (!partials || !lse || !out) return pd::fail(PD_EINVAL, "null tensor pointer");
   if (!aligned16(partials)) return pd::fail(PD_EINVAL, "partials must be 16-byte aligned");
   const int64_t rows = int64_t(batch) * num_heads;
@@ -1314,10 +1326,10 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
 #define PD_LAUNCH_MERGE(DV)                                                                    \
   if (splits > 64)                                                                             \
     hipLaunchKernelGGL((lse_merge_kernel<DV, 128>), grid, dim3(64), 0, st, partials, lse, o,   \
-                       splits);                                                                \
+                       splits, lse_lanes);                                                     \
   else                                                                                         \
     hipLaunchKernelGGL((lse_merge_kernel<DV, 64>), grid, dim3(64), 0, st, partials, lse, o,    \
-                       splits)
+                       splits, lse_lanes)
   switch (head_dim) {
     case 64: PD_LAUNCH_MERGE(64); break;
     case 128: PD_LAUNCH_MERGE(128); break;

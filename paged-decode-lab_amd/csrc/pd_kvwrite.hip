@@ -43,13 +43,14 @@ store_slots_kernel(const uint16_t* __restrict__ key, int64_t key_stride,
 }
 
 // key[b, h, s, :] (strides ksb, ksh, kss; d contiguous) goes to the page slot
-// table[b, pos[s] / 256] * 256 + pos[s] % 256, kv head h.  A negative table
-// entry or position, or a page index at or past the row's width, skips it.
+// table[b, pos[s] / 256] * 256 + pos[s] % 256, kv head h.  A negative
+// position, a page index at or past the row's width, or a table entry outside
+// [0, num_pages) skips it, so no row is written outside the page pool.
 __global__ void __launch_bounds__(kThreads)
 store_pages_kernel(const uint16_t* __restrict__ key, int64_t ksb, int64_t ksh, int64_t kss,
                    const uint16_t* __restrict__ value, int64_t vsb, int64_t vsh, int64_t vss,
                    uint16_t* __restrict__ k_pages, uint16_t* __restrict__ v_pages,
-                   const int32_t* __restrict__ table, int64_t tsb, int width,
+                   int64_t num_pages, const int32_t* __restrict__ table, int64_t tsb, int width,
                    const int64_t* __restrict__ positions, int batch, int hkv, int steps,
                    int pieces_per_row) {
   const int64_t piece = int64_t(blockIdx.x) * kThreads + threadIdx.x;
@@ -64,7 +65,7 @@ store_pages_kernel(const uint16_t* __restrict__ key, int64_t ksb, int64_t ksh, i
   const int64_t pos = positions[s];
   if (pos < 0 || (pos >> 8) >= width) return;
   const int32_t page = table[int64_t(b) * tsb + (pos >> 8)];
-  if (page < 0) return;
+  if (page < 0 || page >= num_pages) return;
   const int D = pieces_per_row * 8;
   const int64_t dst = ((int64_t(page) * 256 + (pos & 255)) * hkv + h) * D + 8 * c;
   const u32x4_t kx = *reinterpret_cast<const u32x4_t*>(key + b * ksb + h * ksh + s * kss + 8 * c);
@@ -116,7 +117,8 @@ extern "C" int pd_store_kv(const void* key, int64_t key_stride, const void* valu
 extern "C" int pd_store_kv_pages(const void* key, int64_t key_stride_b, int64_t key_stride_h,
                                  int64_t key_stride_s, const void* value, int64_t value_stride_b,
                                  int64_t value_stride_h, int64_t value_stride_s, void* k_pages,
-                                 void* v_pages, const int32_t* table, int64_t table_stride_b,
+                                 void* v_pages, int64_t num_pages, const int32_t* table,
+                                 int64_t table_stride_b,
                                  int32_t table_width, const int64_t* positions, int32_t batch,
                                  int32_t num_kv_heads, int32_t steps, int32_t head_dim,
                                  pd_stream_t stream) {
@@ -129,6 +131,7 @@ extern "C" int pd_store_kv_pages(const void* key, int64_t key_stride_b, int64_t 
   if (!key || !value || !k_pages || !v_pages || !table || !positions)
     return pd::fail(PD_EINVAL, "null tensor pointer");
   if (table_width < 1) return pd::fail(PD_EINVAL, "table width must be positive");
+  if (num_pages < 1) return pd::fail(PD_EINVAL, "the page pool must hold at least one page");
   const int64_t strides[6] = {key_stride_b, key_stride_h, key_stride_s,
                               value_stride_b, value_stride_h, value_stride_s};
   for (int64_t st : strides)
@@ -144,7 +147,8 @@ extern "C" int pd_store_kv_pages(const void* key, int64_t key_stride_b, int64_t 
                      reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(key),
                      key_stride_b, key_stride_h, key_stride_s, static_cast<const uint16_t*>(value),
                      value_stride_b, value_stride_h, value_stride_s,
-                     static_cast<uint16_t*>(k_pages), static_cast<uint16_t*>(v_pages), table,
-                     table_stride_b, table_width, positions, batch, num_kv_heads, steps, pieces);
+                     static_cast<uint16_t*>(k_pages), static_cast<uint16_t*>(v_pages), num_pages,
+                     table, table_stride_b, table_width, positions, batch, num_kv_heads, steps,
+                     pieces);
   return launch_status("pd_store_kv_pages");
 }

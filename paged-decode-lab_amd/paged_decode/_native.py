@@ -41,8 +41,8 @@ SIGNATURES = {
                        _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_ml_merge": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
     "pd_store_kv": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _vp],
-    "pd_store_kv_pages": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i32,
-                          _vp, _i32, _i32, _i32, _i32, _vp],
+    "pd_store_kv_pages": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64,
+                          _i32, _vp, _i32, _i32, _i32, _i32, _vp],
 }
 
 _lib = None
@@ -159,6 +159,7 @@ def store_kv_pages(key, value, k_pages, v_pages, tables, positions):
     check(lib().pd_store_kv_pages(key.data_ptr(), key.stride(0), key.stride(1), key.stride(2),
                                   value.data_ptr(), value.stride(0), value.stride(1),
                                   value.stride(2), k_pages.data_ptr(), v_pages.data_ptr(),
-                                  tables.data_ptr(), tables.stride(0), tables.shape[1],
+                                  k_pages.shape[0], tables.data_ptr(), tables.stride(0),
+                                  tables.shape[1],
                                   positions.data_ptr(), b, hkv, steps, d,
                                   stream_handle(key.device)))

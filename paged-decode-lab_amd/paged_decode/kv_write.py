@@ -35,8 +35,9 @@ def store_kvcache(key, value, k_cache, v_cache, slot_mapping):
     _require(key.dtype == torch.bfloat16 and k_cache.dtype == torch.bfloat16 and
              value.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16,
              "BF16 key/value and caches required")
-    _require(all(t.device == key.device for t in (value, k_cache, v_cache, slot_mapping)),
-             "all tensors must be on one device")
+    _require(key.is_cuda and all(t.device == key.device
+                                 for t in (value, k_cache, v_cache, slot_mapping)),
+             "all tensors must be on one CUDA device")
     _native.store_kv(key, value, k_cache, v_cache, slot_mapping)
 
 
@@ -59,4 +60,7 @@ def write_pages(key, value, k_pages, v_pages, tables, positions):
     _require(key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16 and
              k_pages.dtype == torch.bfloat16 and v_pages.dtype == torch.bfloat16,
              "BF16 key/value and pages required")
+    _require(key.is_cuda and all(t.device == key.device
+                                 for t in (value, k_pages, v_pages, tables, positions)),
+             "key, value, pages, tables and positions must be on one CUDA device")
     _native.store_kv_pages(key, value, k_pages, v_pages, tables, positions)

@@ -49,11 +49,23 @@ def validate_device_metadata(table, lengths, num_pages, max_context_len):
     """Debug check: deliberately synchronizes; NEVER call in capture/hot path."""
     if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
         raise RuntimeError("metadata content validation cannot run during graph capture")
-    table = table.detach().to("cpu", torch.int32).contiguous()
-    lengths = lengths.detach().to("cpu", torch.int32).contiguous()
     if table.dim() != 2 or lengths.dim() != 1 or table.shape[0] != lengths.shape[0]:
         raise ValueError("metadata batch dimensions differ")
-    _native.validate_metadata(table, lengths, int(num_pages), int(max_context_len))
+    # reference.py:14-15: integral dtypes only (no float truncation, no bool).
+    for x in (table, lengths):
+        if x.dtype.is_floating_point or x.dtype.is_complex or x.dtype == torch.bool:
+            raise ValueError("metadata must be integral")
+    _native.validate_metadata(_host_int32(table), _host_int32(lengths), int(num_pages),
+                              int(max_context_len))
+
+
+def _host_int32(x):
+    """Host int32 copy; wider values saturate to [-1, 2^31 - 1] instead of wrapping, so a
+    negative or out-of-range length or live page entry is still rejected after narrowing."""
+    x = x.detach().to("cpu")
+    if x.dtype != torch.int32:
+        x = x.to(torch.int64).clamp(-1, 2 ** 31 - 1).to(torch.int32)
+    return x.contiguous()
 
 
 def _aligned(t):

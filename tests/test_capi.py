@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert names == sorted(_native.SIGNATURES), names
     for name in names:
         assert getattr(lib, name) is not None
-    assert lib.pd_abi_version() == 2
+    assert lib.pd_abi_version() == 3
 
 
 def test_error_reporting_and_validation_without_launching():
@@ -72,3 +72,46 @@ def test_validate_device_metadata_accepts_cpu_tensors_and_rejects_bad_rows():
         validate_device_metadata(table, torch.tensor([300, 300], dtype=torch.int32), 3, 512)
     with pytest.raises(ValueError, match="batch"):
         validate_device_metadata(table, torch.tensor([1], dtype=torch.int32), 3, 512)
+
+
+def test_validate_device_metadata_rejects_non_integral_and_wide_values():
+    # reference.py:14-15: float or bool metadata is rejected, not truncated.
+    from paged_decode.runtime import validate_device_metadata
+    table = torch.tensor([[0, 1]], dtype=torch.int32)
+    with pytest.raises(ValueError, match="integral"):
+        validate_device_metadata(table.float(), torch.tensor([300], dtype=torch.int32), 2, 512)
+    with pytest.raises(ValueError, match="integral"):
+        validate_device_metadata(table, torch.tensor([1.5]), 2, 512)
+    with pytest.raises(ValueError, match="integral"):
+        validate_device_metadata(table, torch.tensor([True]), 2, 512)
+    # int64 values past int32 saturate instead of wrapping: 2^32 + 5 would wrap to 5.
+    with pytest.raises(ValueError, match="capacity"):
+        validate_device_metadata(table, torch.tensor([2 ** 32 + 5], dtype=torch.int64), 2, 512)
+    with pytest.raises(ValueError, match="capacity"):
+        validate_device_metadata(table, torch.tensor([-(2 ** 32) + 5], dtype=torch.int64), 2, 512)
+    # A live page entry of 2^32 would wrap to page 0.
+    wide = torch.tensor([[2 ** 32, 1]], dtype=torch.int64)
+    with pytest.raises(ValueError, match="live page"):
+        validate_device_metadata(wide, torch.tensor([300], dtype=torch.int64), 2, 512)
+    validate_device_metadata(table.long(), torch.tensor([300], dtype=torch.int64), 2, 512)
+
+
+def test_kv_writes_reject_host_tensors_before_launching():
+    from paged_decode.kv_write import store_kvcache, write_pages
+    key = torch.zeros((1, 2, 3, 64), dtype=torch.bfloat16)
+    pages = torch.zeros((2, 256, 2, 64), dtype=torch.bfloat16)
+    tables = torch.zeros((1, 2), dtype=torch.int32)
+    positions = torch.arange(3, dtype=torch.int64)
+    with pytest.raises(ValueError, match="CUDA device"):
+        write_pages(key, key.clone(), pages, pages.clone(), tables, positions)
+    rows = torch.zeros((3, 2, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="CUDA device"):
+        store_kvcache(rows, rows.clone(), pages, pages.clone(), torch.zeros(3, dtype=torch.int32))
+
+
+def test_lse_merge_lane_count_is_validated():
+    lib = _native.lib()
+    null = ctypes.c_void_p(0)
+    for lanes, splits in ((3, 36), (128, 128), (64, 8), (0, 4)):
+        status = lib.pd_lse_merge(null, null, null, 1, 4, 256, splits, lanes, null)
+        assert status == _native.PD_EINVAL and b"lse_lanes" in lib.pd_last_error(), (lanes, splits)
