@@ -121,6 +121,29 @@ int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                       int32_t splits, int32_t tokens_per_split, int32_t tile_tokens,
                       double scale, pd_stream_t stream);
 
+/* Bytes of the static device scratch of pd_matched_decode_noalloc. */
+#define PD_NOALLOC_SCRATCH_BYTES (16 << 20)
+
+/* Allocation-free matched split-KV decode.  This entry point has no
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory or pass a workspace (code under hipGraph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, output and
+ * results (bit for bit) as pd_matched_decode without its partials, lse and
+ * counters: the split workspace lives in a static device array of
+ * PD_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, so
+ * batch * num_heads * splits * (head_dim + 1) * 4 bytes (plus 256 for
+ * alignment) must fit in it, or PD_EINVAL is returned.  It calls no
+ * hipMalloc, hipFree or allocating library routine.  Every call on one GPU
+ * shares that GPU's scratch, so calls that overlap on one GPU (two streams,
+ * two threads) race; calls ordered on one stream do not. */
+int pd_matched_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                              const void* k, const void* v,
+                              const int32_t* table, int64_t table_stride_b, int32_t table_width,
+                              const int32_t* lengths, void* out,
+                              int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t splits, int32_t tokens_per_split,
+                              int32_t tile_tokens, double scale, pd_stream_t stream);
+
 /* Base decode: FP32 online softmax over the whole context with FP32
  * probabilities, out = acc / denom (0 for an empty row), for every query head.
  * One workgroup per (kv head, sequence) serves the kv head's query heads (16 at

@@ -29,6 +29,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 #include <type_traits>
 
 #include "pd_device.h"
@@ -1304,10 +1305,13 @@ extern "C" int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_st
                          tile_tokens, scale, stream);
 }
 
-extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, int32_t batch,
-                            int32_t num_heads, int32_t head_dim, int32_t splits,
-                            int32_t lse_lanes, pd_stream_t stream) {
-  pd::clear_error();
+namespace {
+
+// Validation and launch of lse_merge_kernel, shared by pd_lse_merge and
+// pd_matched_decode_noalloc.
+int merge_entry(const char* what, const float* partials, const float* lse, void* out,
+                int32_t batch, int32_t num_heads, int32_t head_dim, int32_t splits,
+                int32_t lse_lanes, pd_stream_t stream) {
   if (batch <= 0 || num_heads <= 0) return pd::fail(PD_EINVAL, "batch and heads must be positive");
   if (!pd::valid_head_dim(head_dim))
     return pd::fail(PD_EINVAL, "custom decode supports head_dim 64, 128, or 256");
@@ -1336,7 +1340,97 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
     default: PD_LAUNCH_MERGE(256); break;
   }
 #undef PD_LAUNCH_MERGE
-  return launch_status("pd_lse_merge");
+  return launch_status(what);
+}
+
+}  // namespace
+
+extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, int32_t batch,
+                            int32_t num_heads, int32_t head_dim, int32_t splits,
+                            int32_t lse_lanes, pd_stream_t stream) {
+  pd::clear_error();
+  return merge_entry("pd_lse_merge", partials, lse, out, batch, num_heads, head_dim, splits,
+                     lse_lanes, stream);
+}
+
+// ------------------------------------------------ allocation-free decode
+// The split workspace of pd_matched_decode_noalloc lives in this file-scope
+// device array: partials f32 [batch, num_heads, splits, head_dim] from byte 0,
+// then lse f32 [batch, num_heads, splits] from the next 256-byte boundary.
+// Every GPU the library runs on holds its own copy until the process ends.  In
+// host code `pd_scratch` names a host-side stand-in, never the device memory:
+// the device address comes from hipGetSymbolAddress, once per device, with that
+// device current.
+static __device__ __align__(256) unsigned char pd_scratch[PD_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// Device address of pd_scratch on the current device, looked up on the first
+// call per device; nullptr (with pd_last_error set) if the lookup fails.
+void* scratch_address() {
+  static std::atomic<void*> cache[kMaxDevices];
+  static std::mutex mu;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    pd::fail(PD_ELAUNCH, "no current HIP device (or device index past %d)", kMaxDevices - 1);
+    return nullptr;
+  }
+  void* ptr = cache[dev].load(std::memory_order_acquire);
+  if (ptr) return ptr;
+  std::lock_guard<std::mutex> lock(mu);
+  ptr = cache[dev].load(std::memory_order_relaxed);
+  if (!ptr) {
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(pd_scratch));
+    if (err != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      pd::fail(PD_ELAUNCH, "hipGetSymbolAddress(pd_scratch) failed on device %d: %s", dev,
+               hipGetErrorString(err));
+      return nullptr;
+    }
+    cache[dev].store(ptr, std::memory_order_release);
+  }
+  return ptr;
+}
+
+}  // namespace
+
+extern "C" int pd_matched_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                         const void* k, const void* v, const int32_t* table,
+                                         int64_t table_stride_b, int32_t table_width,
+                                         const int32_t* lengths, void* out, int32_t batch,
+                                         int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t splits,
+                                         int32_t tokens_per_split, int32_t tile_tokens,
+                                         double scale, pd_stream_t stream) {
+  pd::clear_error();
+  if (batch <= 0 || num_heads <= 0 || splits < 1 || splits > 128 ||
+      !pd::valid_head_dim(head_dim))
+    return pd::fail(PD_EINVAL, "batch, heads, head_dim (64/128/256) and splits (1..128) must "
+                               "be valid");
+  const int64_t rows = int64_t(batch) * num_heads * splits;
+  const int64_t lse_offset = (rows * head_dim * 4 + 255) / 256 * 256;
+  const int64_t need = lse_offset + rows * 4;
+  if (need > int64_t(PD_NOALLOC_SCRATCH_BYTES))
+    return pd::fail(PD_EINVAL,
+                    "split workspace of %lld bytes (batch * num_heads * splits * (head_dim + 1) "
+                    "floats) exceeds the %lld-byte static scratch of pd_matched_decode_noalloc",
+                    static_cast<long long>(need),
+                    static_cast<long long>(PD_NOALLOC_SCRATCH_BYTES));
+  if (!out) return pd::fail(PD_EINVAL, "invalid output buffer");
+  auto* base = static_cast<unsigned char*>(scratch_address());
+  if (!base) return PD_ELAUNCH;
+  auto* partials = reinterpret_cast<float*>(base);
+  auto* lse = reinterpret_cast<float*>(base + lse_offset);
+  if (int st = partition_entry("pd_matched_decode_noalloc", false, q, q_stride_b, q_stride_h, k,
+                               v, table, table_stride_b, table_width, lengths, partials, lse,
+                               nullptr, nullptr, batch, num_heads, num_kv_heads, head_dim,
+                               splits, tokens_per_split, tile_tokens, scale, stream))
+    return st;
+  return merge_entry("pd_matched_decode_noalloc", partials, lse, out, batch, num_heads,
+                     head_dim, splits, plan_lse_lanes(splits, head_dim), stream);
 }
 
 namespace {

@@ -35,6 +35,8 @@ SIGNATURES = {
     "pd_lse_merge": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
     "pd_matched_decode": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                           _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
+    "pd_matched_decode_noalloc": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp,
+                                  _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_base": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i32,
                 _dbl, _vp],
     "pd_split_fixed": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp,
@@ -113,6 +115,17 @@ def matched_decode(q, k, v, tables, lengths, partials, lse, counters, out, num_k
                                   counters.data_ptr(), out.data_ptr(), b, h, num_kv_heads, d,
                                   splits, tokens_per_split, tile_tokens, scale,
                                   stream_handle(q.device)))
+
+
+def matched_decode_noalloc(q, k, v, tables, lengths, out, num_kv_heads, splits,
+                           tokens_per_split, tile_tokens, scale):
+    """pd_matched_decode with the split workspace in the library's static device scratch."""
+    b, h, d = q.shape
+    check(lib().pd_matched_decode_noalloc(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                                          v.data_ptr(), tables.data_ptr(), tables.stride(0),
+                                          tables.shape[1], lengths.data_ptr(), out.data_ptr(), b,
+                                          h, num_kv_heads, d, splits, tokens_per_split,
+                                          tile_tokens, scale, stream_handle(q.device)))
 
 
 def lse_merge(partials, lse, out, lse_lanes):

@@ -115,3 +115,13 @@ def test_lse_merge_lane_count_is_validated():
     for lanes, splits in ((3, 36), (128, 128), (64, 8), (0, 4)):
         status = lib.pd_lse_merge(null, null, null, 1, 4, 256, splits, lanes, null)
         assert status == _native.PD_EINVAL and b"lse_lanes" in lib.pd_last_error(), (lanes, splits)
+
+
+def test_noalloc_rejects_workspaces_past_its_static_scratch():
+    # batch 64 x 32 heads x 32 splits x 257 floats = 67 MB > 16 MiB: rejected before any
+    # device call (the scratch address is looked up only for calls that fit).
+    lib = _native.lib()
+    null = ctypes.c_void_p(0)
+    status = lib.pd_matched_decode_noalloc(null, 0, 0, null, null, null, 0, 128, null, null,
+                                           64, 32, 8, 256, 32, 1024, 64, 0.0625, null)
+    assert status == _native.PD_EINVAL and b"static scratch" in lib.pd_last_error()

@@ -1,0 +1,107 @@
+"""pd_matched_decode_noalloc against pd_matched_decode, through the C ABI.
+
+The allocation-free entry point keeps its split workspace in the library's
+static device scratch.  Its output must equal pd_matched_decode's (which takes
+the workspace as arguments) bit for bit, on consecutive calls of different
+sizes that share the scratch, eagerly and replayed from a hipGraph.
+"""
+import pytest
+import torch
+
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X GPU", allow_module_level=True)
+
+from cases import make_case, poison_tails
+from gpu_cases import to_gpu
+from paged_decode import _native
+from paged_decode.matched_splitkv import allocate_matched_resources
+from paged_decode.spec import DecodeSpec
+
+pytestmark = pytest.mark.gpu
+
+
+def reference_call(g, spec, num_splits=0):
+    """pd_matched_decode with its own workspace; returns (out, plan)."""
+    res = allocate_matched_resources(spec, "cuda", num_splits=num_splits, fused=True)
+    q, k, v, table, lens = g
+    plan = res.plan
+    _native.matched_decode(q, k, v, table, lens, res.partials, res.lse, res.counters, res.out,
+                           spec.num_kv_heads, plan.splits, plan.tokens_per_split,
+                           plan.tile_tokens, spec.head_dim ** -0.5)
+    return res.out.clone(), plan
+
+
+def noalloc_call(g, spec, plan, out):
+    q, k, v, table, lens = g
+    _native.matched_decode_noalloc(q, k, v, table, lens, out, spec.num_kv_heads, plan.splits,
+                                   plan.tokens_per_split, plan.tile_tokens,
+                                   spec.head_dim ** -0.5)
+
+
+CASES = [
+    # (lengths, Hq, Hkv, D, capacity, explicit splits): the benchmark's D256 GQA shape
+    # with four sequences, then a smaller one (fewer rows, fewer splits, D 128).
+    ([2064, 0, 1000, 1], 16, 4, 256, 2112, 0),
+    ([257, 0], 8, 2, 128, 600, 0),
+]
+
+
+def test_two_calls_in_a_row_match_pd_matched_decode():
+    outs = []
+    for lengths, hq, hkv, dim, cap, splits in CASES:
+        print(f"noalloc case B={len(lengths)} Hq={hq} Hkv={hkv} D={dim} cap={cap}", flush=True)
+        case = make_case(lengths, hq, hkv, dim, seed=len(lengths), capacity=cap)
+        poison_tails(*case[1:3], case[3], case[4])
+        g = to_gpu(case)
+        spec = DecodeSpec(len(lengths), hq, hkv, dim, cap)
+        expected, plan = reference_call(g, spec, splits)
+        out = torch.full_like(expected, float("nan"))
+        noalloc_call(g, spec, plan, out)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), \
+            f"B={len(lengths)} D={dim}: differs from pd_matched_decode"
+        assert not out[lengths.index(0)].any(), "a zero-length row is not exactly zero"
+        outs.append(out)
+    # The first call's output is untouched by the second call, which reused the scratch.
+    assert outs[0].isfinite().all()
+
+
+def test_graph_replay_equals_eager():
+    lengths, hq, hkv, dim, cap, _ = CASES[0]
+    spec = DecodeSpec(len(lengths), hq, hkv, dim, cap)
+    case = make_case(lengths, hq, hkv, dim, seed=3, capacity=cap)
+    g = to_gpu(case)
+    expected, plan = reference_call(g, spec)
+    out = torch.empty_like(expected)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        noalloc_call(g, spec, plan, out)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        noalloc_call(g, spec, plan, out)
+    for replay in range(3):
+        out.zero_()
+        # Eager work on the same scratch between replays (a different, smaller call).
+        small = CASES[1]
+        sspec = DecodeSpec(len(small[0]), *small[1:5])
+        sg = to_gpu(make_case(small[0], *small[1:4], seed=replay, capacity=small[4]))
+        sexp, splan = reference_call(sg, sspec)
+        sout = torch.empty_like(sexp)
+        noalloc_call(sg, sspec, splan, sout)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(sout.view(torch.int16), sexp.view(torch.int16))
+        assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), f"replay {replay}"
+
+
+def test_oversized_workspace_is_rejected():
+    q = torch.zeros((64, 32, 256), device="cuda", dtype=torch.bfloat16)
+    kv = torch.zeros((1, 256, 8, 256), device="cuda", dtype=torch.bfloat16)
+    table = torch.zeros((64, 128), device="cuda", dtype=torch.int32)
+    lens = torch.zeros((64,), device="cuda", dtype=torch.int32)
+    out = torch.empty_like(q)
+    # 64 * 32 * 32 splits * 257 floats = 67 MB > 16 MiB.
+    with pytest.raises(ValueError, match="static scratch"):
+        _native.matched_decode_noalloc(q, kv, kv, table, lens, out, 8, 32, 1024, 64, 0.0625)
