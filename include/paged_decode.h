@@ -102,16 +102,23 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
                  int32_t batch, int32_t num_heads, int32_t head_dim, int32_t splits,
                  int32_t lse_lanes, pd_stream_t stream);
 
-/* Matched split-KV decode in one launch: the partition of pd_partition plus,
- * in the last workgroup to finish each (sequence, kv head), the LSE merge of
- * pd_lse_merge for that GQA group (bit-identical to pd_partition followed by
+/* int32 counters per (sequence, kv head) in pd_matched_decode's `counters`. */
+#define PD_FUSED_COUNTERS_PER_GROUP 128
+
+/* Matched split-KV decode in one launch: the partition of pd_partition plus
+ * the LSE merge of pd_lse_merge (bit-identical to pd_partition followed by
  * pd_lse_merge).  Replaces the two launches of matched_decode
- * (matched_splitkv.py:142-149).  `counters` is int32 [batch * num_kv_heads],
- * all zero before the first call; every completed call leaves it all zero
- * again, so the launch can be replayed from a graph without a reset.  Calls
- * that share `counters` must not run concurrently.  Writes partials, lse and
- * out bf16 [batch, num_heads, head_dim].  The merge sums with the plan's
- * lse_lanes, min(next_pow2(splits), 32 if head_dim % 128 == 0 else 16). */
+ * (matched_splitkv.py:142-149).  With splits of one tile (tokens_per_split ==
+ * tile_tokens) the merge of each GQA group is shared by the last wavefront to
+ * finish each quarter of the head_dim columns; otherwise the last workgroup of
+ * each (sequence, kv head) merges the whole group.  `counters` is int32
+ * [batch * num_kv_heads * PD_FUSED_COUNTERS_PER_GROUP] (four counters per
+ * group, each on a 128-byte line), all zero before the first call; every completed
+ * call leaves it all zero again, so the launch can be replayed from a graph
+ * without a reset.  Calls that share `counters` must not run concurrently.
+ * Writes partials, lse and out bf16 [batch, num_heads, head_dim].  The merge
+ * sums with the plan's lse_lanes, min(next_pow2(splits), 32 if
+ * head_dim % 128 == 0 else 16). */
 int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                       const void* k, const void* v,
                       const int32_t* table, int64_t table_stride_b, int32_t table_width,

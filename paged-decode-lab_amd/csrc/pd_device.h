@@ -80,6 +80,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
+// Cache-policy operand of the buffer builtins for device-scope coherent
+// accesses: the sc1 bit (bit 4; bit 0 is sc0, bit 1 nt).
+constexpr int kCoherentAux = 16;
+
 // E consecutive floats at byte offset `off`; kCoherent sets the sc1 cache
 // policy bit (device-scope coherent, so a line another XCD wrote is re-read).
 // The builtins' results are bit-cast as whole vectors to float vectors before
@@ -88,7 +92,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 template <int E, bool kCoherent>
 __device__ __forceinline__ void buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, int off,
                                                 float (&x)[E]) {
-  constexpr int aux = kCoherent ? 16 : 0;
+  constexpr int aux = kCoherent ? kCoherentAux : 0;
   if constexpr (E == 1) {
     x[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, aux));
   } else if constexpr (E == 2) {
@@ -134,15 +138,24 @@ __device__ __host__ __forceinline__ int plan_lse_lanes(int splits, int D) {
 // order (:114-118), then a halving tree over the lanes adds lane j + half to
 // lane j (:119), here an xor butterfly (float addition commutes exactly).
 // Terms past the last split are exact zeros, so they are not added.
+// The two LSE loads of lse_weights (a row of `bytes` bytes; zero past it), so
+// that a caller can issue several rows' loads before any is needed.
 template <bool kCoherent>
-__device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lanes,
-                                            int lane, float& w0, float& w1) {
-  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(lrow, splits * 4);
-  float a[1], c[1];
-  buffer_load_f32<1, kCoherent>(rsrc, lane * 4, a);
-  buffer_load_f32<1, kCoherent>(rsrc, (lane + 64) * 4, c);
-  const float v0 = lane < splits ? a[0] : -INFINITY;
-  const float v1 = lane + 64 < splits ? c[0] : -INFINITY;
+__device__ __forceinline__ void lse_load(const float* __restrict__ lrow, int bytes, int lane,
+                                         float& a, float& c) {
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(lrow, bytes);
+  float x[1], y[1];
+  buffer_load_f32<1, kCoherent>(rsrc, lane * 4, x);
+  buffer_load_f32<1, kCoherent>(rsrc, (lane + 64) * 4, y);
+  a = x[0];
+  c = y[0];
+}
+
+// lse_weights on the values lse_load returned for the row.
+__device__ __forceinline__ void lse_weights_of(float a, float c, int splits, int lanes, int lane,
+                                               float& w0, float& w1) {
+  const float v0 = lane < splits ? a : -INFINITY;
+  const float v1 = lane + 64 < splits ? c : -INFINITY;
   float mx = wave_max(fmaxf(v0, v1));
   if (mx == -INFINITY) mx = 0.f;
   const float e0 = exp_fast(v0 - mx), e1 = exp_fast(v1 - mx);
@@ -157,6 +170,14 @@ __device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int 
   const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
   w0 = exp_fast(v0 - logsum);
   w1 = exp_fast(v1 - logsum);
+}
+
+template <bool kCoherent>
+__device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lanes,
+                                            int lane, float& w0, float& w1) {
+  float a, c;
+  lse_load<kCoherent>(lrow, splits * 4, lane, a, c);
+  lse_weights_of(a, c, splits, lanes, lane, w0, w1);
 }
 
 // acc[e] = fma(w_p, partial_p[e], acc[e]) for p = 0, 1, ..., splits-1 in order
@@ -213,6 +234,101 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
   for (int s0 = kBatch; s0 < splits; s0 += kBatch) {
     load(s0);
     accumulate(s0);
+  }
+}
+
+// One wavefront merges columns [c0, c0 + C) (C a multiple of 4) of the G <= GP
+// query heads of a GQA group over all `splits` splits, with the arithmetic of
+// lse_merge_kernel: merge weights per head from lse_weights, then
+// acc = fma(w_p, partial_p, acc) in split order.  `pg` and `lg` are the
+// group's first rows of partials [G][splits][D] and lse [G][splits]; `og` its
+// first output row [G][D].
+// Lane l owns chunks l, l + 64, ... (kNC of them) of 4 consecutive columns;
+// chunk i is head i / (C/4), columns c0 + 4 (i % (C/4)), so one 16-byte load
+// per split and chunk.  Batches of kBatch splits are issued at once (kBatch *
+// kNC stays below the 63 loads a wavefront can have in flight), before the
+// weights are computed.  A head's weights reach the lanes through `wsh`, this
+// wavefront's 128 * GP floats of LDS: lse_weights leaves w_p in lane p % 64,
+// which writes it to wsh[128 h + p], and each lane reads its head's weights
+// four splits at a time.  Loads past the last split read past the buffer
+// (zero) and have weight 0, so they leave acc unchanged.  kCoherent reads with
+// device-scope loads (values that other workgroups wrote).
+template <int GP, int kNC, int kBatch, bool kCoherent>
+__device__ __forceinline__ void merge_group_chunks(const float* __restrict__ pg,
+                                                   const float* __restrict__ lg,
+                                                   uint16_t* __restrict__ og, int G, int splits,
+                                                   int D, int lanes, int c0, int C,
+                                                   float* __restrict__ wsh, int lane) {
+  static_assert(kBatch % 4 == 0 && kBatch * kNC <= 48, "batch of loads in flight");
+  const int cpr = C / 4;  // chunks per head
+  const int bytes = G * splits * D * 4;
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(pg, bytes);
+  int hd[kNC], off[kNC];
+  bool live[kNC];
+  float acc[kNC][4];
+#pragma unroll
+  for (int i = 0; i < kNC; ++i) {
+    const int chunk = lane + 64 * i;
+    live[i] = chunk < G * cpr;
+    hd[i] = live[i] ? chunk / cpr : 0;
+    off[i] = ((hd[i] * splits) * D + c0 + 4 * (chunk % cpr)) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[i][e] = 0.f;
+  }
+  float x[kBatch][kNC][4];
+  auto load = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+      for (int i = 0; i < kNC; ++i)
+        buffer_load_f32<4, kCoherent>(rs, s0 + j < splits ? off[i] + (s0 + j) * D * 4 : bytes,
+                                      x[j][i]);
+  };
+  auto accumulate = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < kBatch; j += 4)
+#pragma unroll
+      for (int i = 0; i < kNC; ++i) {
+        // Splits from 128 on do not exist (x = 0 there); their weights are read
+        // from splits 124..127, which are finite.
+        const int p4 = s0 + j < 128 ? s0 + j : 124;
+        const floatx4_t w4 = *reinterpret_cast<const floatx4_t*>(wsh + 128 * hd[i] + p4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][e] = fmaf(w4[u], x[j + u][i][e], acc[i][e]);
+      }
+  };
+  load(0);
+  // Every head's LSE loads go out with the first batch (rows past the group
+  // read as empty), so all of them arrive in one round trip.
+  float la[GP], lc[GP];
+#pragma unroll
+  for (int h = 0; h < GP; ++h)
+    lse_load<kCoherent>(lg + int64_t(h < G ? h : 0) * splits, h < G ? splits * 4 : 0, lane, la[h],
+                        lc[h]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int h = 0; h < GP; ++h) {
+    if (h >= G) break;
+    float w0, w1;
+    lse_weights_of(la[h], lc[h], splits, lanes, lane, w0, w1);
+    wsh[128 * h + lane] = w0;
+    wsh[128 * h + 64 + lane] = w1;
+  }
+  accumulate(0);
+  for (int s0 = kBatch; s0 < splits; s0 += kBatch) {
+    load(s0);
+    accumulate(s0);
+  }
+#pragma unroll
+  for (int i = 0; i < kNC; ++i) {
+    if (!live[i]) continue;
+    const int chunk = lane + 64 * i;
+    uint16_t* dst = og + int64_t(hd[i]) * D + c0 + 4 * (chunk % cpr);
+    *reinterpret_cast<u32x2_t*>(dst) =
+        u32x2_t{bf16_bits(acc[i][0]) | (bf16_bits(acc[i][1]) << 16),
+                bf16_bits(acc[i][2]) | (bf16_bits(acc[i][3]) << 16)};
   }
 }
 

@@ -74,6 +74,14 @@ struct MatchedShared {
 // Hkv * hs), so the base and fixed-split protocols also cover G > 16.
 constexpr int kMatched = 0, kBase = 1, kSplit = 2;
 
+// Split counters of the fused launch: four per (sequence, kv head), one per
+// column slice of the single-tile kernel (the multi-tile kernels use the
+// first), each on a 128-byte line of its own, so that the atomics of
+// different slices do not queue on one line.
+constexpr int kCounterStride = 32;
+constexpr int kCountersPerGroup = 4 * kCounterStride;
+static_assert(kCountersPerGroup == PD_FUSED_COUNTERS_PER_GROUP, "C ABI counter layout");
+
 // A partition without tokens, written directly: the values the full epilogue
 // derives from the untouched state (acc 0, running maximum -inf, denominator
 // 0), without its LDS exchange and barriers.  Matched: partial +0, LSE -inf;
@@ -439,7 +447,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
     // point rather than from a line this XCD's caches may hold from an
     // earlier call.  No cache-wide writeback or invalidate is needed, so the
     // KV tiles other calls keep in L2 stay resident.
-    int* counter = counters + int64_t(b) * Hkv + kh;
+    int* counter = counters + (int64_t(b) * Hkv + kh) * kCountersPerGroup;  // the first slot
     wait_memory();
     __syncthreads();
     if (tid == 0)
@@ -813,7 +821,7 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   if constexpr (kFused) {
     // Split-completion count and the last workgroup's merge, exactly as in
     // matched_partition_kernel.
-    int* counter = counters + int64_t(b) * Hkv + kh;
+    int* counter = counters + (int64_t(b) * Hkv + kh) * kCountersPerGroup;  // the first slot
     wait_memory();
     __syncthreads();
     if (tid == 0)
@@ -853,14 +861,35 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 // of the 16-token grouping at D=256.  Scores, maxima, probabilities,
 // denominators and LSEs are bit-identical to matched_partition_kernel's; the
 // partial differs only in the fp32 summation order of P V.
+//
+// kFused = true also merges, in the same launch, with the work of the merge
+// spread over the column slices the wavefronts already own.  Wavefront w of
+// every split writes its columns [w*D/4, (w+1)*D/4) of the partials and the
+// group's LSEs with device-scope stores, waits for its own stores to
+// complete, and increments counters[(b * Hkv + kh) * 4 + w].  The wavefront
+// whose increment returns splits - 1 is the last for its slice: every split's
+// slice and LSEs are then complete, and it merges that slice for the whole
+// GQA group (merge_group_column, device-scope loads) and resets the counter
+// to 0.  So four wavefronts, usually on four CUs, share a group's merge, each
+// reading a quarter of its partials, with no workgroup barrier and no cache
+// writeback or invalidate.  The output is bit-identical to lse_merge_kernel's.
 
+// Shape of the fused merge of one column slice (D/4 columns of G <= GP heads):
+// kNC 4-column chunks per lane, kBatch splits per batch of loads.
 template <int D, int GP>
+struct FusedMerge {
+  static constexpr int kNC = GP * D / 1024 > 1 ? GP * D / 1024 : 1;
+  static constexpr int kBatch = 48 / kNC;
+};
+
+template <int D, int GP, bool kFused>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
                     const uint16_t* __restrict__ q, int tsb, int width, int qsb, int qsh, int G,
                     int Hq, int splits, const uint16_t* __restrict__ k,
                     const uint16_t* __restrict__ v, float* __restrict__ partials,
-                    float* __restrict__ lse_out, int Hkv, float scale, float c) {
+                    float* __restrict__ lse_out, int Hkv, float scale, float c,
+                    int* __restrict__ counters, uint16_t* __restrict__ out) {
   using C = Matched<D, GP>;
   using P = TileP<D>;
   constexpr int TILE = C::kTile;
@@ -868,6 +897,8 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   __shared__ float lsum[4][16];
   __shared__ __attribute__((aligned(16))) char vs[4 * C::kSlot];
   __shared__ __attribute__((aligned(16))) char ps[16 * P::kPitch];
+  // Fused merge: each wavefront's merge weights, [GP][128] floats.
+  __shared__ __attribute__((aligned(16))) float wsm[kFused ? 4 * 128 * GP : 4];
 
   const int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -885,12 +916,42 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   // wait for two memory round trips (length, then table) instead of one.
   pw.settle();
 
+  // Fused protocol, after this wavefront's slice and LSEs were stored with
+  // device-scope stores: count the slice, and merge it if it was the last.
+  auto count_and_merge = [&]() {
+    wait_memory();
+    int* counter = counters + (int64_t(b) * Hkv + kh) * kCountersPerGroup + w * kCounterStride;
+    int old = 0;
+    if (lane == 0)
+      old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readlane(old, 0);
+    if (old != splits - 1) return;
+    const int64_t grow = int64_t(b) * Hq + kh * G;  // first query head of the group
+    using M = FusedMerge<D, GP>;
+    merge_group_chunks<GP, M::kNC, M::kBatch, true>(
+        partials + grow * splits * D, lse_out + grow * splits, out + grow * D, G, splits, D,
+        plan_lse_lanes(splits, D), w * P::kCols, P::kCols, wsm + w * 128 * GP, lane);
+    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+
   if (end <= start) {
     // Empty split: partial 0 (acc 0 times rcp(1)) and LSE -inf, as the
     // general kernel writes for count == 0.
-    for (int i = tid; i < G * D; i += kThreads)
-      partials[(row0 + int64_t(i / D) * splits) * D + i % D] = 0.f;
-    if (tid < G) lse_out[row0 + int64_t(tid) * splits] = -INFINITY;
+    if constexpr (kFused) {
+      // Each wavefront publishes its own column slice and LSEs.
+      if (lane < P::kCols)
+        for (int h = 0; h < G; ++h)
+          __hip_atomic_store(partials + (row0 + int64_t(h) * splits) * D + w * P::kCols + lane,
+                             0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane < G)
+        __hip_atomic_store(lse_out + row0 + int64_t(lane) * splits, -INFINITY, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      count_and_merge();
+    } else {
+      for (int i = tid; i < G * D; i += kThreads)
+        partials[(row0 + int64_t(i / D) * splits) * D + i % D] = 0.f;
+      if (tid < G) lse_out[row0 + int64_t(tid) * splits] = -INFINITY;
+    }
     return;
   }
 
@@ -1004,13 +1065,43 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     const float safe = den > 0.f ? den : 1.f;
     const float inv = rcp_fast(safe);
     float* dst = partials + (row0 + int64_t(h) * splits) * D + w * P::kCols + qh;
-#pragma unroll
-    for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = acc[j][r] * inv;
-    if (w == 0 && qh == 0) {
+    const bool lse_lane = kFused ? qh == 0 : (w == 0 && qh == 0);
+    float lv = 0.f;
+    if (lse_lane) {
       const float mh = fmaxf(fmaxf(wmax[0][h], wmax[1][h]), fmaxf(wmax[2][h], wmax[3][h]));
-      lse_out[row0 + int64_t(h) * splits] =
-          den > 0.f ? fmaf(mh, scale, ln_fast(safe)) : -INFINITY;
+      lv = den > 0.f ? fmaf(mh, scale, ln_fast(safe)) : -INFINITY;
     }
+    if constexpr (kFused) {
+      // The slice goes to LDS as [head][column], then out with one 16-byte
+      // store per lane and 4 columns (below).  Every wavefront stores the
+      // group's LSEs (the same bits), so each slice's count covers them; the
+      // stores are device-scope (sc1): written through to the coherence point,
+      // so the merging wavefront on another XCD reads them without any cache
+      // writeback.
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j) wsm[w * 128 * GP + h * P::kCols + 16 * j + qh] = acc[j][r] * inv;
+      if (lse_lane)
+        __hip_atomic_store(lse_out + row0 + int64_t(h) * splits, lv, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = acc[j][r] * inv;
+      if (lse_lane) lse_out[row0 + int64_t(h) * splits] = lv;
+    }
+  }
+  if constexpr (kFused) {
+    // Lane l stores chunk l (+64, ...): head c / (kCols/4), 4 columns, 16 bytes.
+    constexpr int kChunks = P::kCols / 4;
+    const float* stage = wsm + w * 128 * GP;
+    const int64_t grow = int64_t(b) * Hq + kh * G;
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(partials + grow * splits * D, G * splits * D * 4);
+    for (int ch = lane; ch < G * kChunks; ch += 64) {
+      const int h = ch / kChunks, c4 = 4 * (ch % kChunks);
+      const u32x4_t val = *reinterpret_cast<const u32x4_t*>(stage + h * P::kCols + c4);
+      __builtin_amdgcn_raw_buffer_store_b128(val, rs, ((h * splits + p) * D + w * P::kCols + c4) * 4,
+                                             0, kCoherentAux);
+    }
+    count_and_merge();
   }
 }
 
@@ -1166,12 +1257,12 @@ int batch_order(dim3 grid) {
   return 0;
 }
 
-template <int D>
+template <int D, bool kFused>
 void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
-#define PD_LAUNCH_TILE(GPV)                                                                   \
-  hipLaunchKernelGGL((matched_tile_kernel<D, GPV>), grid, dim3(kThreads), 0, stream, a.table, \
-                     a.lengths, a.q, a.tsb, a.width, a.qsb, a.qsh, a.G, a.Hq, a.splits, a.k,  \
-                     a.v, a.partials, a.lse, a.Hkv, a.scale, a.c)
+#define PD_LAUNCH_TILE(GPV)                                                                    \
+  hipLaunchKernelGGL((matched_tile_kernel<D, GPV, kFused>), grid, dim3(kThreads), 0, stream,    \
+                     a.table, a.lengths, a.q, a.tsb, a.width, a.qsb, a.qsh, a.G, a.Hq, a.splits, \
+                     a.k, a.v, a.partials, a.lse, a.Hkv, a.scale, a.c, a.counters, a.out)
   switch (gp) {
     case 1: PD_LAUNCH_TILE(1); break;
     case 2: PD_LAUNCH_TILE(2); break;
@@ -1254,11 +1345,14 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
   const dim3 grid(splits, num_kv_heads, batch);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int gp = padded_group(G);
-  if (!fused && tokens_per_split == tile_tokens) {
-    switch (head_dim) {
-      case 64: launch_tile_d<64>(gp, grid, st, a); break;
-      case 128: launch_tile_d<128>(gp, grid, st, a); break;
-      default: launch_tile_d<256>(gp, grid, st, a); break;
+  if (tokens_per_split == tile_tokens) {
+    switch (head_dim * 2 + (fused ? 1 : 0)) {
+      case 128: launch_tile_d<64, false>(gp, grid, st, a); break;
+      case 129: launch_tile_d<64, true>(gp, grid, st, a); break;
+      case 256: launch_tile_d<128, false>(gp, grid, st, a); break;
+      case 257: launch_tile_d<128, true>(gp, grid, st, a); break;
+      case 512: launch_tile_d<256, false>(gp, grid, st, a); break;
+      default: launch_tile_d<256, true>(gp, grid, st, a); break;
     }
     return launch_status(what);
   }

@@ -22,6 +22,12 @@ from . import _native
 from .runtime import _validate
 from .splitkv_plan import make_splitkv_plan
 
+# int32 split counters per (sequence, kv head) of the fused launch
+# (PD_FUSED_COUNTERS_PER_GROUP): one per wavefront column slice of the
+# single-tile kernel, each on a 128-byte line of its own (the multi-tile
+# kernels use the first).
+COUNTERS_PER_GROUP = 128
+
 
 @dataclass
 class MatchedResources:
@@ -46,7 +52,8 @@ def allocate_matched_resources(spec, device, *, num_splits=0, fused=False):
                     dtype=torch.bfloat16),
         torch.empty((*shape, spec.head_dim), device=device, dtype=torch.float32),
         torch.empty(shape, device=device, dtype=torch.float32),
-        torch.zeros((spec.max_batch * spec.num_kv_heads,), device=device, dtype=torch.int32)
+        torch.zeros((spec.max_batch * spec.num_kv_heads * COUNTERS_PER_GROUP,), device=device,
+                    dtype=torch.int32)
         if fused else None)
 
 
@@ -64,7 +71,8 @@ def _check_matched(q, tables, resources, scale):
             raise ValueError("invalid matched workspace")
     counters = resources.counters
     if counters is not None and (
-            counters.shape != (spec.max_batch * spec.num_kv_heads,) or counters.device != q.device
+            counters.shape != (spec.max_batch * spec.num_kv_heads * COUNTERS_PER_GROUP,)
+            or counters.device != q.device
             or counters.dtype != torch.int32 or not counters.is_contiguous()):
         raise ValueError("invalid matched workspace")
 
