@@ -2,7 +2,7 @@
 import numpy as np
 import torch
 
-from parity import assert_parity
+from parity import assert_parity, record
 
 
 def to_gpu(case, device="cuda"):
@@ -42,9 +42,14 @@ def torch_dense(q, k, v, tables, lengths, scale=None):
     return result
 
 
-def assert_close_dense(actual, expected):
+def assert_close_dense(actual, expected, where=""):
+    """The reference's dense gate (2e-2, tests/test_gpu.py:44-48); max-abs and RMSE are
+    recorded for the run's parity summary."""
     assert torch.isfinite(actual).all()
     torch.testing.assert_close(actual.float(), expected.float(), atol=2e-2, rtol=2e-2)
+    diff = actual.float() - expected.float()
+    record(where, max_abs_vs_dense=float(diff.abs().max()) if diff.numel() else 0.0,
+           rmse_vs_dense=float(diff.square().mean().sqrt()) if diff.numel() else 0.0)
 
 
 def pooled_case(lengths, hq, hkv, dim, capacity, pool_pages, seed, device="cuda"):

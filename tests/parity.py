@@ -19,12 +19,25 @@ The 2^-18 term covers float32 accumulation-order noise on outputs that are
 close to zero.  Planted protocol mistakes (forward tile walk, no bf16(p)) fail
 this gate (tests/test_oracle_matched.py::test_parity_gate_rejects_protocol_mistakes).
 """
+import os
+
 import numpy as np
 
 from oracle.numerics import bf16_ulp_distance
 
 NOISE_FLOOR = 2.0 ** -18
 MAX_FRACTION_BEYOND_ONE_ULP = 1e-2
+
+
+# (test id, label, statistics) of every check that passed, for the summary that
+# conftest.py prints at the end of the run.
+RECORDS = []
+
+
+def record(where="", **stats):
+    """Keeps the statistics of a passed check under the running test's id."""
+    test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
+    RECORDS.append((test, where, stats))
 
 
 def bf16_ulp_of(x):
@@ -61,4 +74,6 @@ def assert_parity(actual, expected, where="", ambiguity=None):
     if stats["beyond_one_ulp"] > MAX_FRACTION_BEYOND_ONE_ULP:
         raise AssertionError(f"{where}: too many outputs beyond one bf16 ulp ({summary})")
     print(f"parity {where}: {summary}")
+    record(where, max_ulps=stats["max_ulps"], beyond_one_ulp=stats["beyond_one_ulp"],
+           one_ulp=stats["one_ulp"], max_abs_vs_oracle=stats["max_abs"])
     return stats
