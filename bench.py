@@ -211,15 +211,15 @@ import json, os, sys, time
 sys.path.insert(0, {root!r})
 import numpy as np
 from oracle import reference as R
-rng = np.random.default_rng(20261105)
-ctx, hq, hkv, dim, budget = {ctx}, 16, 4, 256, {budget}
-width = (ctx + 255) // 256
-table = rng.permutation(width).reshape(1, width).astype(np.int32)
+rng = np.random.default_rng({seed})
+lens = np.array({lengths!r}, dtype=np.int32)
+batch, hq, hkv, dim, budget = len(lens), {hq}, {hkv}, {dim}, {budget}
+width = (max({capacity}, 1) + 255) // 256
+table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
 bf = lambda x: ((x.view(np.uint32).astype(np.uint64) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
-k = bf(rng.normal(size=(width, 256, hkv, dim)).astype(np.float32))
+k = bf(rng.normal(size=(batch * width, 256, hkv, dim)).astype(np.float32))
 v = bf(rng.normal(size=k.shape).astype(np.float32))
-q = bf(rng.normal(size=(1, hq, dim)).astype(np.float32))
-lens = np.array([ctx], dtype=np.int32)
+q = bf(rng.normal(size=(batch, hq, dim)).astype(np.float32))
 R.streaming_reference(q, k, v, table, lens, split=True)          # warmup
 times, t_end = [], time.perf_counter() + budget
 while len(times) < 5 or time.perf_counter() < t_end:
@@ -230,12 +230,23 @@ times.sort()
 print(json.dumps(dict(us=times[len(times) // 2] * 1e6, calls=len(times))))
 """
 
+# CPU-baseline workloads: name -> (lengths, Hq, Hkv, D, table capacity, seed).
+CPU_WORKLOADS = {
+    "ctx_2064": ([2064], 16, 4, 256, 2112, 20261105),
+    "ctx_528": ([528], 16, 4, 256, 528, 20261105),
+    "cpu_reference_b4": ([0, 1, 257, 1000], 8, 2, 128, 1000, 7),
+}
 
-def cpu_baseline(ctx, threads, budget):
+
+def cpu_baseline(workload, threads, budget):
+    """Median time of the NumPy restatement of the reference CPU path (split mode) on one
+    workload, in a child process limited to ``threads`` BLAS/OpenMP threads."""
+    lengths, hq, hkv, dim, capacity, seed = CPU_WORKLOADS[workload]
     env = dict(os.environ)
     env["OPENBLAS_NUM_THREADS"] = str(threads)
     env["OMP_NUM_THREADS"] = str(threads)
-    code = CPU_SNIPPET.format(root=ROOT, ctx=ctx, budget=budget)
+    code = CPU_SNIPPET.format(root=ROOT, seed=seed, lengths=list(lengths), hq=hq, hkv=hkv,
+                              dim=dim, capacity=capacity, budget=budget)
     res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
                          timeout=600)
     if res.returncode:
@@ -534,19 +545,32 @@ def main():
     if not args.no_cpu:
         # The box's CPU share for one GPU is 16 threads, whatever os.cpu_count() reports.
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
-        one = cpu_baseline(ctx, 1, args.cpu_budget)
-        allc = cpu_baseline(ctx, threads, args.cpu_budget)
+        one = cpu_baseline("ctx_2064", 1, args.cpu_budget)
+        allc = cpu_baseline("ctx_2064", threads, args.cpu_budget)
         progress(f"cpu baseline: {one['us']:.0f} us (1 thread), {allc['us']:.0f} us (all)")
         best = min((one, 1), (allc, threads), key=lambda x: x[0]["us"])
+        others = {}
+        for name in ("ctx_528", "cpu_reference_b4"):
+            lengths, hq, hkv, dim, _, _ = CPU_WORKLOADS[name]
+            nb = algorithmic_bytes(lengths, len(lengths), hq, hkv, dim)
+            row = {"workload": f"B={len(lengths)} Hq={hq} Hkv={hkv} D={dim} lengths {lengths}"}
+            for label, n in (("one_thread", 1), ("all_threads", threads)):
+                r = cpu_baseline(name, n, args.cpu_budget / 2)
+                row[f"{label}_us_per_call"] = round(r["us"], 1)
+                row[f"{label}_tbps"] = round(nb / r["us"] / 1e6, 6)
+            others[name] = row
+        progress("cpu baseline of context 528 and the B=4 CPU reference case done")
         cpu = {"value": round(nbytes / best[0]["us"] / 1e6, 6), "unit": "TB/s",
                "cores": best[1], "kind": "port",
                "us_per_call": round(best[0]["us"], 1),
                "one_thread_us_per_call": round(one["us"], 1),
                "all_threads_us_per_call": round(allc["us"], 1),
+               "threads_all": threads,
                "host_cpus": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
                "sample": (f"NumPy restatement of the reference CPU path (streaming_reference, "
                           f"1024-token partitions, 64-token tiles, FP32) on the same B=1 Hq=16 Hkv=4 D=256 shape, "
-                          f"median of {allc['calls']} calls in ~{args.cpu_budget:.0f} s")}
+                          f"median of {allc['calls']} calls in ~{args.cpu_budget:.0f} s"),
+               "other_workloads": others}
 
     line = {
         "metric": "paged-decode µs/call + achieved HBM TB/s (% peak), D256 GQA ctx 2064",

@@ -277,9 +277,13 @@ class DecodeStepGraph:
         torch.cuda.current_stream(dev).wait_stream(side)
         torch.cuda.synchronize(dev)
         del saved
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            self.logits = runner._forward(self.tokens, self.position)
+        # Capture begins outside inference mode: torch registers its generators' graph
+        # state when a capture begins, and tensors made in inference mode could not be
+        # updated by later captures made outside it.
+        with torch.inference_mode(False):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self.logits = runner._forward(self.tokens, self.position)
         self.graph = graph
 
     def run(self, token, position):

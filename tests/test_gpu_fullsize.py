@@ -1,8 +1,9 @@
 """The benchmark workloads at their full sizes, on the GPU.
 
 Bandwidth sweep: batch 64, Hq 32, Hkv 8, D 128, lengths U[1, 32768] from a seed, every
-sequence's pages scattered over a pool of 40,000 pages per cache (21 GB each, so element
-offsets pass 2^32).  Edge coverage: batch 128, a quarter of the sequences empty, the
+sequence's pages scattered over the workload's 200 GB pool: 190,734 pages of 512 KiB per
+cache (100 GB each, so element offsets pass 2^37), or the largest pool that fits the
+device's free memory.  Edge coverage: batch 128, a quarter of the sequences empty, the
 rest U[1, 4096] with page and partition boundaries, D 64 MHA 16/16 and D 256 GQA 32/4.
 
 The CPU oracle cannot walk every sequence of these batches in seconds, so the checks are
@@ -32,7 +33,22 @@ from paged_decode.spec import DecodeSpec
 
 pytestmark = pytest.mark.gpu
 
-SWEEP = dict(batch=64, hq=32, hkv=8, dim=128, capacity=32768, pool_pages=40000)
+SWEEP = dict(batch=64, hq=32, hkv=8, dim=128, capacity=32768, pool_pages=190734)
+PAGE_BYTES = 256 * 8 * 128 * 2
+
+
+def _sweep_pool_pages():
+    """The 200 GB pool (K and V), capped at 80% of the free device memory."""
+    free, _ = torch.cuda.mem_get_info()
+    pages = min(SWEEP["pool_pages"], int(0.8 * free) // (2 * PAGE_BYTES))
+    print(f"bandwidth-sweep pool: {pages} pages per cache ({2 * pages * PAGE_BYTES / 1e9:.1f} GB)")
+    return pages
+
+
+@pytest.fixture(autouse=True)
+def _release_pool():
+    yield
+    torch.cuda.empty_cache()
 
 
 def _bits(t):
@@ -113,7 +129,7 @@ def _check_graph_replay(call, q, k, v, table, lens):
 def test_bandwidth_sweep_matched_full_size():
     lengths = _sweep_lengths()
     g = pooled_case(lengths, SWEEP["hq"], SWEEP["hkv"], SWEEP["dim"], SWEEP["capacity"],
-                    SWEEP["pool_pages"], seed=64)
+                    _sweep_pool_pages(), seed=64)
     spec = DecodeSpec(SWEEP["batch"], SWEEP["hq"], SWEEP["hkv"], SWEEP["dim"], SWEEP["capacity"])
     res = allocate_matched_resources(spec, "cuda")
     assert res.plan.splits == 1 and res.plan.tokens_per_split == 32768
@@ -139,7 +155,7 @@ def test_bandwidth_sweep_matched_full_size():
 def test_bandwidth_sweep_paged_backends_full_size(backend):
     lengths = _sweep_lengths()
     g = pooled_case(lengths, SWEEP["hq"], SWEEP["hkv"], SWEEP["dim"], SWEEP["capacity"],
-                    SWEEP["pool_pages"], seed=65)
+                    _sweep_pool_pages(), seed=65)
     spec = DecodeSpec(SWEEP["batch"], SWEEP["hq"], SWEEP["hkv"], SWEEP["dim"], SWEEP["capacity"])
     res = allocate_resources(spec, "cuda", backend)
 
