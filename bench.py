@@ -290,6 +290,7 @@ def context_sweep(torch, contexts=(8192, 32768, 131072)):
         # 128 unrolled calls per graph, as for the headline: a graph replay carries a
         # launch cost of its own that a short unroll would spread over too few calls.
         us = graph_time_us(torch, case["full"], 256, unroll=128)
+        fused_us = graph_time_us(torch, case["fused"], 256, unroll=128)
         part_us = graph_time_us(torch, case["partition"], 256, unroll=128)
         nbytes = algorithmic_bytes([ctx], 1, 16, 4, 256)
         pbytes = algorithmic_bytes([ctx], 1, 16, 4, 256, with_output=False)
@@ -297,6 +298,8 @@ def context_sweep(torch, contexts=(8192, 32768, 131072)):
         out[f"ctx_{ctx}"] = {"plan": f"{p.splits}x{p.tokens_per_split}",
                              "us_per_call": round(us, 2), "tbps": round(nbytes / us / 1e6, 3),
                              "pct_peak": round(100 * nbytes / us / 1e6 / PEAK_TBPS, 1),
+                             "fused_us_per_call": round(fused_us, 2),
+                             "fused_pct_peak": round(100 * nbytes / fused_us / 1e6 / PEAK_TBPS, 1),
                              "partition_us": round(part_us, 2),
                              "partition_pct_peak": round(100 * pbytes / part_us / 1e6 / PEAK_TBPS, 1)}
         del case
@@ -524,9 +527,11 @@ def main():
                                           "tbps": round(nbytes / f_us / 1e6, 3)}
         c528 = matched_case(torch, 1, 16, 4, 256, 528, [528], 20261105)
         u528 = graph_time_us(torch, c528["full"], args.steps)
+        f528 = graph_time_us(torch, c528["fused"], args.steps)
         b528 = algorithmic_bytes([528], 1, 16, 4, 256)
         extra["ctx_528"] = {"plan": f"{c528['plan'].splits}x{c528['plan'].tokens_per_split}",
-                            "us_per_call": round(u528, 3), "tbps": round(b528 / u528 / 1e6, 3)}
+                            "us_per_call": round(u528, 3), "tbps": round(b528 / u528 / 1e6, 3),
+                            "fused_us_per_call": round(f528, 3)}
         del c528
         progress("reference protocol, 1024-token partitions and context 528 done")
         extra["context_sweep_d256_gqa4"] = context_sweep(torch)

@@ -39,7 +39,7 @@ enum pd_status { PD_OK = 0, PD_EINVAL = 1, PD_ELAUNCH = 2 };
 
 #define PD_PAGE_SIZE 256      /* spec.py:6 */
 #define PD_PARTITION_SIZE 1024 /* spec.py:7 */
-#define PD_ABI_VERSION 3
+#define PD_ABI_VERSION 4
 
 /* Split-KV plan; field meanings follow SplitKVPlan (splitkv_plan.py:15-23). */
 typedef struct pd_plan {
@@ -102,6 +102,17 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
                  int32_t batch, int32_t num_heads, int32_t head_dim, int32_t splits,
                  int32_t lse_lanes, pd_stream_t stream);
 
+/* Probes how the current device deals the workgroups of a launch to its XCDs
+ * and records it for pd_matched_decode.  This entry point has no counterpart
+ * in the reference (its GPUs have one L2).  It launches one small kernel on the
+ * default stream and waits for it, so it must not be called while a stream is
+ * being captured.  *xcds receives the XCD count when workgroup i of a launch
+ * runs on XCD i % count (the MI355X dispatch order), else -1.  From then on,
+ * pd_matched_decode on this device keeps all splits of each (sequence, kv head)
+ * on one XCD for single-tile plans, so their partials and merge stay in that
+ * XCD's L2 (see pd_matched_decode). */
+int pd_probe_xcds(int32_t* xcds);
+
 /* int32 counters per (sequence, kv head) in pd_matched_decode's `counters`. */
 #define PD_FUSED_COUNTERS_PER_GROUP 128
 
@@ -118,7 +129,16 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
  * without a reset.  Calls that share `counters` must not run concurrently.
  * Writes partials, lse and out bf16 [batch, num_heads, head_dim].  The merge
  * sums with the plan's lse_lanes, min(next_pow2(splits), 32 if
- * head_dim % 128 == 0 else 16). */
+ * head_dim % 128 == 0 else 16).
+ * Where the merge runs: on a device that pd_probe_xcds found to deal
+ * workgroups round-robin to its XCDs, single-tile plans run a one-dimensional
+ * grid that puts every split of (sequence b, kv head kh), group
+ * g = b * num_kv_heads + kh, on XCD g % xcds; partials, counters and merge then
+ * stay in that XCD's L2 (plain stores, loads that skip the CU's L1).  A
+ * workgroup that finds itself on another XCD adds 1 to
+ * counters[g * PD_FUSED_COUNTERS_PER_GROUP + 1], which is otherwise always 0.
+ * Elsewhere the partials are published with device-scope stores and read
+ * with device-scope loads, so the merge may run on any XCD. */
 int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                       const void* k, const void* v,
                       const int32_t* table, int64_t table_stride_b, int32_t table_width,

@@ -80,19 +80,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
-// Cache-policy operand of the buffer builtins for device-scope coherent
-// accesses: the sc1 bit (bit 4; bit 0 is sc0, bit 1 nt).
+// Cache-policy operands of the buffer builtins (bit 0 is sc0, bit 1 nt, bit 4
+// sc1).  kCoherentAux (sc1): device-scope coherent accesses, written through to
+// / re-read from the coherence point beyond the XCDs' L2s, so a line another
+// XCD wrote is seen.  kL2Aux (sc0): a load that misses the CU's L1 and is
+// served by its XCD's L2, which every CU of that XCD writes through to; enough
+// for values another workgroup of the same XCD stored.
 constexpr int kCoherentAux = 16;
+constexpr int kL2Aux = 1;
 
-// E consecutive floats at byte offset `off`; kCoherent sets the sc1 cache
-// policy bit (device-scope coherent, so a line another XCD wrote is re-read).
+// E consecutive floats at byte offset `off`, with cache policy kAux.
 // The builtins' results are bit-cast as whole vectors to float vectors before
 // any element is read: reading elements of their integer vector results
 // directly made this compiler emit a single dword load for the whole vector.
-template <int E, bool kCoherent>
+template <int E, int kAux>
 __device__ __forceinline__ void buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, int off,
                                                 float (&x)[E]) {
-  constexpr int aux = kCoherent ? kCoherentAux : 0;
+  constexpr int aux = kAux;
   if constexpr (E == 1) {
     x[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, aux));
   } else if constexpr (E == 2) {
@@ -140,13 +144,13 @@ __device__ __host__ __forceinline__ int plan_lse_lanes(int splits, int D) {
 // Terms past the last split are exact zeros, so they are not added.
 // The two LSE loads of lse_weights (a row of `bytes` bytes; zero past it), so
 // that a caller can issue several rows' loads before any is needed.
-template <bool kCoherent>
+template <int kAux>
 __device__ __forceinline__ void lse_load(const float* __restrict__ lrow, int bytes, int lane,
                                          float& a, float& c) {
   const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(lrow, bytes);
   float x[1], y[1];
-  buffer_load_f32<1, kCoherent>(rsrc, lane * 4, x);
-  buffer_load_f32<1, kCoherent>(rsrc, (lane + 64) * 4, y);
+  buffer_load_f32<1, kAux>(rsrc, lane * 4, x);
+  buffer_load_f32<1, kAux>(rsrc, (lane + 64) * 4, y);
   a = x[0];
   c = y[0];
 }
@@ -172,11 +176,11 @@ __device__ __forceinline__ void lse_weights_of(float a, float c, int splits, int
   w1 = exp_fast(v1 - logsum);
 }
 
-template <bool kCoherent>
+template <int kAux>
 __device__ __forceinline__ void lse_weights(const float* __restrict__ lrow, int splits, int lanes,
                                             int lane, float& w0, float& w1) {
   float a, c;
-  lse_load<kCoherent>(lrow, splits * 4, lane, a, c);
+  lse_load<kAux>(lrow, splits * 4, lane, a, c);
   lse_weights_of(a, c, splits, lanes, lane, w0, w1);
 }
 
@@ -204,7 +208,7 @@ struct MergeBatch {
   static constexpr int value = E == 1 ? 64 : (E == 2 ? 48 : (E == 4 ? 40 : (E == 8 ? 16 : 8)));
 };
 
-template <int E, bool kCoherent, int kBatch = MergeBatch<E>::value, typename PrepareFn,
+template <int E, int kAux, int kBatch = MergeBatch<E>::value, typename PrepareFn,
           typename WeightFn>
 __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int D, int dd,
                                              int splits, PrepareFn prepare, WeightFn weight,
@@ -217,7 +221,7 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
   auto load = [&](int s0) {
 #pragma unroll
     for (int j = 0; j < kBatch; ++j)
-      buffer_load_f32<E, kCoherent>(rsrc, ((s0 + j) * D + dd) * 4, x[j]);
+      buffer_load_f32<E, kAux>(rsrc, ((s0 + j) * D + dd) * 4, x[j]);
   };
   auto accumulate = [&](int s0) {
 #pragma unroll
@@ -251,9 +255,10 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
 // wavefront's 128 * GP floats of LDS: lse_weights leaves w_p in lane p % 64,
 // which writes it to wsh[128 h + p], and each lane reads its head's weights
 // four splits at a time.  Loads past the last split read past the buffer
-// (zero) and have weight 0, so they leave acc unchanged.  kCoherent reads with
-// device-scope loads (values that other workgroups wrote).
-template <int GP, int kNC, int kBatch, bool kCoherent>
+// (zero) and have weight 0, so they leave acc unchanged.  kAux is the cache
+// policy of the loads: kCoherentAux for values workgroups on other XCDs wrote,
+// kL2Aux for values workgroups of this XCD wrote.
+template <int GP, int kNC, int kBatch, int kAux>
 __device__ __forceinline__ void merge_group_chunks(const float* __restrict__ pg,
                                                    const float* __restrict__ lg,
                                                    uint16_t* __restrict__ og, int G, int splits,
@@ -281,7 +286,7 @@ __device__ __forceinline__ void merge_group_chunks(const float* __restrict__ pg,
     for (int j = 0; j < kBatch; ++j)
 #pragma unroll
       for (int i = 0; i < kNC; ++i)
-        buffer_load_f32<4, kCoherent>(rs, s0 + j < splits ? off[i] + (s0 + j) * D * 4 : bytes,
+        buffer_load_f32<4, kAux>(rs, s0 + j < splits ? off[i] + (s0 + j) * D * 4 : bytes,
                                       x[j][i]);
   };
   auto accumulate = [&](int s0) {
@@ -305,7 +310,7 @@ __device__ __forceinline__ void merge_group_chunks(const float* __restrict__ pg,
   float la[GP], lc[GP];
 #pragma unroll
   for (int h = 0; h < GP; ++h)
-    lse_load<kCoherent>(lg + int64_t(h < G ? h : 0) * splits, h < G ? splits * 4 : 0, lane, la[h],
+    lse_load<kAux>(lg + int64_t(h < G ? h : 0) * splits, h < G ? splits * 4 : 0, lane, la[h],
                         lc[h]);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

@@ -79,6 +79,12 @@ constexpr int kMatched = 0, kBase = 1, kSplit = 2;
 // first), each on a 128-byte line of its own, so that the atomics of
 // different slices do not queue on one line.
 constexpr int kCounterStride = 32;
+// Fused modes of the single-tile kernel: none (partition only), coherent (the
+// merge may run on another XCD: device-scope stores and loads), XCD-local (all
+// of a group's workgroups on one XCD: plain stores, loads served by its L2).
+constexpr int kFuseNone = 0, kFuseCoherent = 1, kFuseXcd = 2;
+// Hardware register holding the XCD (XCC) index of the executing wavefront.
+constexpr int kHwRegXccId = 20;
 constexpr int kCountersPerGroup = 4 * kCounterStride;
 static_assert(kCountersPerGroup == PD_FUSED_COUNTERS_PER_GROUP, "C ABI counter layout");
 
@@ -461,10 +467,10 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
     constexpr int kV = D / 64;
     for (int hh = __builtin_amdgcn_readfirstlane(w); hh < G; hh += 4) {
       float w0 = 0.f, w1 = 0.f, acc[kV];
-      merge_splits<kV, true>(
+      merge_splits<kV, kCoherentAux>(
           partials + (row0 + hh) * splits * D, D, lane * kV, splits,
           [&] {
-            lse_weights<true>(lse_out + (row0 + hh) * splits, splits, plan_lse_lanes(splits, D),
+            lse_weights<kCoherentAux>(lse_out + (row0 + hh) * splits, splits, plan_lse_lanes(splits, D),
                               lane, w0, w1);
           },
           [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
@@ -833,10 +839,10 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     constexpr int kV = D / 64;
     for (int hh = __builtin_amdgcn_readfirstlane(w); hh < G; hh += 4) {
       float w0 = 0.f, w1 = 0.f, mrg[kV];
-      merge_splits<kV, true>(
+      merge_splits<kV, kCoherentAux>(
           partials + (row0 + hh) * splits * D, D, lane * kV, splits,
           [&] {
-            lse_weights<true>(lse_out + (row0 + hh) * splits, splits, plan_lse_lanes(splits, D),
+            lse_weights<kCoherentAux>(lse_out + (row0 + hh) * splits, splits, plan_lse_lanes(splits, D),
                               lane, w0, w1);
           },
           [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, mrg);
@@ -882,17 +888,23 @@ struct FusedMerge {
   static constexpr int kBatch = 48 / kNC;
 };
 
-template <int D, int GP, bool kFused>
+template <int D, int GP, int kFuse>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
                     const uint16_t* __restrict__ q, int tsb, int width, int qsb, int qsh, int G,
                     int Hq, int splits, const uint16_t* __restrict__ k,
                     const uint16_t* __restrict__ v, float* __restrict__ partials,
                     float* __restrict__ lse_out, int Hkv, float scale, float c,
-                    int* __restrict__ counters, uint16_t* __restrict__ out) {
+                    int* __restrict__ counters, uint16_t* __restrict__ out, int xcds,
+                    int groups) {
   using C = Matched<D, GP>;
   using P = TileP<D>;
   constexpr int TILE = C::kTile;
+  constexpr bool kFused = kFuse != kFuseNone;
+  // Cache policy of the published slices and of the merging loads.
+  constexpr int kPubAux = kFuse == kFuseXcd ? 0 : kCoherentAux;
+  constexpr int kMergeAux = kFuse == kFuseXcd ? kL2Aux : kCoherentAux;
+  constexpr int kScope = kFuse == kFuseXcd ? __HIP_MEMORY_SCOPE_WORKGROUP : __HIP_MEMORY_SCOPE_AGENT;
   __shared__ float wmax[4][16];
   __shared__ float lsum[4][16];
   __shared__ __attribute__((aligned(16))) char vs[4 * C::kSlot];
@@ -900,7 +912,26 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   // Fused merge: each wavefront's merge weights, [GP][128] floats.
   __shared__ __attribute__((aligned(16))) float wsm[kFused ? 4 * 128 * GP : 4];
 
-  const int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  if constexpr (kFuse == kFuseXcd) {
+    // One-dimensional grid dealt round-robin to the XCDs: workgroup i runs on
+    // XCD i % xcds.  Group g = (b, kh) belongs to XCD g % xcds, whose
+    // workgroups take its splits in turn, so all of a group's partials, its
+    // counters and its merge stay in that XCD's L2.
+    const int i = blockIdx.x, x = i % xcds, slot = i / xcds;
+    const int g = x + xcds * (slot / splits);
+    if (g >= groups) return;
+    p = slot % splits;
+    kh = g % Hkv;
+    b = g / Hkv;
+    // The mapping relies on the dispatch order; a workgroup on another XCD
+    // counts itself in an otherwise unused word of the group's counter line,
+    // which the host-side checks read (it is never set on a correctly placed
+    // launch).
+    if ((__builtin_amdgcn_s_getreg((15 << 11) | kHwRegXccId) & 0xf) != x && threadIdx.x == 0)
+      __hip_atomic_fetch_add(counters + int64_t(g) * kCountersPerGroup + 1, 1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = lane & 15, qg = lane >> 4;
@@ -922,16 +953,15 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     wait_memory();
     int* counter = counters + (int64_t(b) * Hkv + kh) * kCountersPerGroup + w * kCounterStride;
     int old = 0;
-    if (lane == 0)
-      old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, kScope);
     old = __builtin_amdgcn_readlane(old, 0);
     if (old != splits - 1) return;
     const int64_t grow = int64_t(b) * Hq + kh * G;  // first query head of the group
     using M = FusedMerge<D, GP>;
-    merge_group_chunks<GP, M::kNC, M::kBatch, true>(
+    merge_group_chunks<GP, M::kNC, M::kBatch, kMergeAux>(
         partials + grow * splits * D, lse_out + grow * splits, out + grow * D, G, splits, D,
         plan_lse_lanes(splits, D), w * P::kCols, P::kCols, wsm + w * 128 * GP, lane);
-    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, kScope);
   };
 
   if (end <= start) {
@@ -942,10 +972,10 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       if (lane < P::kCols)
         for (int h = 0; h < G; ++h)
           __hip_atomic_store(partials + (row0 + int64_t(h) * splits) * D + w * P::kCols + lane,
-                             0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                             0.f, __ATOMIC_RELAXED, kScope);
       if (lane < G)
         __hip_atomic_store(lse_out + row0 + int64_t(lane) * splits, -INFINITY, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+                           kScope);
       count_and_merge();
     } else {
       for (int i = tid; i < G * D; i += kThreads)
@@ -1081,8 +1111,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 #pragma unroll
       for (int j = 0; j < P::kNBW; ++j) wsm[w * 128 * GP + h * P::kCols + 16 * j + qh] = acc[j][r] * inv;
       if (lse_lane)
-        __hip_atomic_store(lse_out + row0 + int64_t(h) * splits, lv, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(lse_out + row0 + int64_t(h) * splits, lv, __ATOMIC_RELAXED, kScope);
     } else {
 #pragma unroll
       for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = acc[j][r] * inv;
@@ -1099,7 +1128,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       const int h = ch / kChunks, c4 = 4 * (ch % kChunks);
       const u32x4_t val = *reinterpret_cast<const u32x4_t*>(stage + h * P::kCols + c4);
       __builtin_amdgcn_raw_buffer_store_b128(val, rs, ((h * splits + p) * D + w * P::kCols + c4) * 4,
-                                             0, kCoherentAux);
+                                             0, kPubAux);
     }
     count_and_merge();
   }
@@ -1121,9 +1150,9 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
   const int lane = threadIdx.x;
   const int dd = blockIdx.y * 64 + lane;
   float w0 = 0.f, w1 = 0.f, acc[1];
-  merge_splits<1, false, kBatch>(
+  merge_splits<1, 0, kBatch>(
       partials + row * splits * D, D, dd, splits,
-      [&] { lse_weights<false>(lse + row * splits, splits, lanes, lane, w0, w1); },
+      [&] { lse_weights<0>(lse + row * splits, splits, lanes, lane, w0, w1); },
       [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
   out[row * D + dd] = uint16_t(bf16_bits(acc[0]));
 }
@@ -1234,6 +1263,20 @@ int device_cu_count() {
   return n;
 }
 
+// XCD layout of each device, set by pd_probe_xcds: the number of XCDs when
+// workgroup i of a launch runs on XCD i % xcds, -1 when the dispatch does not
+// follow that order, 0 when not probed.
+std::atomic<int> g_xcd_layout[64];
+
+int xcd_layout() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return g_xcd_layout[dev].load(std::memory_order_relaxed);
+}
+
 // `order` of ordered_sequence (pd_device.h) for a multi-tile launch over
 // `grid` = (splits, kv heads x slices, batch) at two workgroups per CU:
 // * CUs / (grid.x * grid.y) when the whole grid is resident and rows z and
@@ -1257,12 +1300,14 @@ int batch_order(dim3 grid) {
   return 0;
 }
 
-template <int D, bool kFused>
-void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
+template <int D, int kFuse>
+void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a, int xcds,
+                   int groups) {
 #define PD_LAUNCH_TILE(GPV)                                                                    \
-  hipLaunchKernelGGL((matched_tile_kernel<D, GPV, kFused>), grid, dim3(kThreads), 0, stream,    \
+  hipLaunchKernelGGL((matched_tile_kernel<D, GPV, kFuse>), grid, dim3(kThreads), 0, stream,     \
                      a.table, a.lengths, a.q, a.tsb, a.width, a.qsb, a.qsh, a.G, a.Hq, a.splits, \
-                     a.k, a.v, a.partials, a.lse, a.Hkv, a.scale, a.c, a.counters, a.out)
+                     a.k, a.v, a.partials, a.lse, a.Hkv, a.scale, a.c, a.counters, a.out, xcds, \
+                     groups)
   switch (gp) {
     case 1: PD_LAUNCH_TILE(1); break;
     case 2: PD_LAUNCH_TILE(2); break;
@@ -1346,13 +1391,30 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int gp = padded_group(G);
   if (tokens_per_split == tile_tokens) {
-    switch (head_dim * 2 + (fused ? 1 : 0)) {
-      case 128: launch_tile_d<64, false>(gp, grid, st, a); break;
-      case 129: launch_tile_d<64, true>(gp, grid, st, a); break;
-      case 256: launch_tile_d<128, false>(gp, grid, st, a); break;
-      case 257: launch_tile_d<128, true>(gp, grid, st, a); break;
-      case 512: launch_tile_d<256, false>(gp, grid, st, a); break;
-      default: launch_tile_d<256, true>(gp, grid, st, a); break;
+    // Fused single-tile plans keep each group on one XCD when the dispatch
+    // order of this device is known (pd_probe_xcds); otherwise they publish
+    // their partials at device scope.
+    const int xcds = fused ? xcd_layout() : 0;
+    const int groups = batch * num_kv_heads;
+    int mode = fused ? (xcds > 0 ? kFuseXcd : kFuseCoherent) : kFuseNone;
+    dim3 tgrid = grid;
+    if (mode == kFuseXcd) {
+      const int64_t n = int64_t(xcds) * ((groups + xcds - 1) / xcds) * splits;
+      if (n < (int64_t(1) << 31))
+        tgrid = dim3(unsigned(n));
+      else
+        mode = kFuseCoherent;
+    }
+    switch (head_dim * 4 + mode) {
+      case 256 + kFuseNone: launch_tile_d<64, kFuseNone>(gp, tgrid, st, a, xcds, groups); break;
+      case 256 + kFuseCoherent: launch_tile_d<64, kFuseCoherent>(gp, tgrid, st, a, xcds, groups); break;
+      case 256 + kFuseXcd: launch_tile_d<64, kFuseXcd>(gp, tgrid, st, a, xcds, groups); break;
+      case 512 + kFuseNone: launch_tile_d<128, kFuseNone>(gp, tgrid, st, a, xcds, groups); break;
+      case 512 + kFuseCoherent: launch_tile_d<128, kFuseCoherent>(gp, tgrid, st, a, xcds, groups); break;
+      case 512 + kFuseXcd: launch_tile_d<128, kFuseXcd>(gp, tgrid, st, a, xcds, groups); break;
+      case 1024 + kFuseNone: launch_tile_d<256, kFuseNone>(gp, tgrid, st, a, xcds, groups); break;
+      case 1024 + kFuseCoherent: launch_tile_d<256, kFuseCoherent>(gp, tgrid, st, a, xcds, groups); break;
+      default: launch_tile_d<256, kFuseXcd>(gp, tgrid, st, a, xcds, groups); break;
     }
     return launch_status(what);
   }
@@ -1445,6 +1507,52 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
   pd::clear_error();
   return merge_entry("pd_lse_merge", partials, lse, out, batch, num_heads, head_dim, splits,
                      lse_lanes, stream);
+}
+
+// ------------------------------------------------------------- XCD probe
+// Placement of the workgroups of one launch of kXccProbeGroups workgroups on
+// the device's XCDs, read by pd_probe_xcds.  In host code `pd_xcc_ids` names a
+// host-side stand-in; the device address comes from hipGetSymbolAddress.
+constexpr int kXccProbeGroups = 2048;
+static __device__ int pd_xcc_ids[kXccProbeGroups];
+
+__global__ void __launch_bounds__(64) xcc_probe_kernel(int* __restrict__ ids) {
+  if (threadIdx.x == 0)
+    ids[blockIdx.x] = __builtin_amdgcn_s_getreg((15 << 11) | kHwRegXccId) & 0xf;
+}
+
+extern "C" int pd_probe_xcds(int32_t* xcds) {
+  pd::clear_error();
+  if (!xcds) return pd::fail(PD_EINVAL, "null output pointer");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return pd::fail(PD_ELAUNCH, "no current HIP device (or more than 64)");
+  }
+  void* ids = nullptr;
+  if (hipGetSymbolAddress(&ids, HIP_SYMBOL(pd_xcc_ids)) != hipSuccess || !ids) {
+    const hipError_t err = hipGetLastError();
+    return pd::fail(PD_ELAUNCH, "hipGetSymbolAddress(pd_xcc_ids) failed: %s",
+                    hipGetErrorString(err));
+  }
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(kXccProbeGroups), dim3(64), 0, nullptr,
+                     static_cast<int*>(ids));
+  if (int st = launch_status("pd_probe_xcds")) return st;
+  static int host[kXccProbeGroups];
+  static std::mutex lock;
+  std::lock_guard<std::mutex> guard(lock);
+  if (hipMemcpy(host, ids, sizeof(host), hipMemcpyDeviceToHost) != hipSuccess) {
+    const hipError_t err = hipGetLastError();
+    return pd::fail(PD_ELAUNCH, "pd_probe_xcds copy failed: %s", hipGetErrorString(err));
+  }
+  int n = 1;
+  for (int i = 0; i < kXccProbeGroups; ++i) n = host[i] + 1 > n ? host[i] + 1 : n;
+  bool round_robin = true;
+  for (int i = 0; i < kXccProbeGroups; ++i) round_robin = round_robin && host[i] == i % n;
+  const int layout = round_robin ? n : -1;
+  g_xcd_layout[dev].store(layout, std::memory_order_relaxed);
+  *xcds = layout;
+  return PD_OK;
 }
 
 // ------------------------------------------------ allocation-free decode

@@ -33,6 +33,7 @@ SIGNATURES = {
     "pd_partition": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
                      _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_lse_merge": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
+    "pd_probe_xcds": [ctypes.POINTER(_i32)],
     "pd_matched_decode": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                           _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_matched_decode_noalloc": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp,
@@ -103,6 +104,22 @@ def partition(q, k, v, tables, lengths, partials, lse, num_kv_heads, splits, tok
                              lengths.data_ptr(), partials.data_ptr(), lse.data_ptr(), b, h,
                              num_kv_heads, d, splits,
                              tokens_per_split, tile_tokens, scale, stream_handle(q.device)))
+
+
+_probed = {}
+
+
+def probe_xcds(device):
+    """XCD count of ``device`` when its workgroups are dealt round-robin to its XCDs, else
+    -1 (pd_probe_xcds; once per device, never during stream capture)."""
+    index = torch.device(device).index
+    index = torch.cuda.current_device() if index is None else index
+    if index not in _probed:
+        count = _i32(0)
+        with torch.cuda.device(index):
+            check(lib().pd_probe_xcds(ctypes.byref(count)))
+        _probed[index] = count.value
+    return _probed[index]
 
 
 def matched_decode(q, k, v, tables, lengths, partials, lse, counters, out, num_kv_heads, splits,

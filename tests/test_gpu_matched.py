@@ -158,6 +158,34 @@ def test_fused_decode_matches_two_launches(lengths, hq, hkv, dim, cap, splits):
         assert torch.equal(_bits(res.partials), _bits(two.partials))
 
 
+@pytest.mark.parametrize("lengths,hq,hkv,dim,cap", [
+    ([500, 0, 1300], 12, 3, 128, 2048),          # 9 groups: XCDs hold 2, 1, 1, ... groups
+    ([2064], 16, 4, 256, 2112),                  # the headline: 4 groups on 4 XCDs
+    ([17] * 20, 8, 8, 64, 256)])                 # 160 groups, 1 split each
+def test_xcd_local_fused_decode(lengths, hq, hkv, dim, cap):
+    """Single-tile plans on a device whose workgroups are dealt round-robin to its XCDs run
+    the XCD-local fused launch (every split of a group on one XCD).  Outputs, partials and
+    LSEs equal the two launches bit for bit, and no workgroup reports a placement other
+    than the one the grid assumes (word 1 of each group's counter line stays 0)."""
+    xcds = _native.probe_xcds("cuda")
+    assert xcds == -1 or 1 <= xcds <= 16
+    if xcds < 1:
+        pytest.skip("this device does not deal workgroups round-robin to its XCDs")
+    g = to_gpu(make_case(lengths, hq, hkv, dim, seed=44, capacity=cap))
+    res = allocate_matched_resources(DecodeSpec(len(lengths), hq, hkv, dim, cap), "cuda",
+                                     fused=True)
+    assert res.plan.tokens_per_split == res.plan.tile_tokens
+    two = _two_kernel_resources(res)
+    for _ in range(3):
+        fused = matched_decode(*g, resources=res).clone()
+        split = matched_decode(*g, resources=two).clone()
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(res.counters) == 0
+        assert torch.equal(_bits(fused), _bits(split))
+        assert torch.equal(_bits(res.partials), _bits(two.partials))
+        assert torch.equal(_bits(res.lse), _bits(two.lse))
+
+
 def test_fused_counters_return_to_zero_across_graph_replays():
     case = make_case([2064], 16, 4, 256, seed=3, capacity=2112)
     g = to_gpu(case)
