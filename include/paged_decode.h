@@ -107,7 +107,8 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
  * in the reference (its GPUs have one L2).  It launches one small kernel on the
  * default stream and waits for it, so it must not be called while a stream is
  * being captured.  *xcds receives the XCD count when workgroup i of a launch
- * runs on XCD i % count (the MI355X dispatch order), else -1.  From then on,
+ * runs on XCD (i + c) % count for one offset c per launch (the MI355X
+ * dispatch order; c varies between launches), else -1.  From then on,
  * pd_matched_decode on this device keeps all splits of each (sequence, kv head)
  * on one XCD for single-tile plans, so their partials and merge stay in that
  * XCD's L2 (see pd_matched_decode). */
@@ -132,11 +133,11 @@ int pd_probe_xcds(int32_t* xcds);
  * head_dim % 128 == 0 else 16).
  * Where the merge runs: on a device that pd_probe_xcds found to deal
  * workgroups round-robin to its XCDs, single-tile plans run a one-dimensional
- * grid that puts every split of (sequence b, kv head kh), group
- * g = b * num_kv_heads + kh, on XCD g % xcds; partials, counters and merge then
- * stay in that XCD's L2 (plain stores, loads that skip the CU's L1).  A
- * workgroup that finds itself on another XCD adds 1 to
- * counters[g * PD_FUSED_COUNTERS_PER_GROUP + 1], which is otherwise always 0.
+ * grid in which each workgroup reads the XCD it runs on and takes work of the
+ * groups g = b * num_kv_heads + kh with g % xcds equal to it, so every split of
+ * a group runs on one XCD; partials, counters and merge then stay in that
+ * XCD's L2 (plain stores, loads that skip the CU's L1).  A workgroup on an XCD
+ * index beyond the probed count adds 1 to counters[1], otherwise always 0.
  * Elsewhere the partials are published with device-scope stores and read
  * with device-scope loads, so the merge may run on any XCD. */
 int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,

@@ -914,23 +914,28 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 
   int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   if constexpr (kFuse == kFuseXcd) {
-    // One-dimensional grid dealt round-robin to the XCDs: workgroup i runs on
-    // XCD i % xcds.  Group g = (b, kh) belongs to XCD g % xcds, whose
-    // workgroups take its splits in turn, so all of a group's partials, its
-    // counters and its merge stay in that XCD's L2.
-    const int i = blockIdx.x, x = i % xcds, slot = i / xcds;
+    // One-dimensional grid of xcds * R workgroups.  The dispatcher deals the
+    // workgroups of a launch round-robin to the XCDs from an offset that
+    // varies between launches (workgroup i runs on XCD (i + c) % xcds, the
+    // same c for the whole launch), so each XCD runs exactly R workgroups,
+    // whose i / xcds are 0 .. R-1.  The work is chosen by the XCD the
+    // workgroup actually runs on: group g = (b, kh) belongs to XCD
+    // g % xcds, whose workgroups take its splits in turn, so all of a
+    // group's partials, its counters and its merge stay in that XCD's L2.
+    const int x = __builtin_amdgcn_s_getreg((15 << 11) | kHwRegXccId) & 0xf;
+    const int slot = blockIdx.x / xcds;
     const int g = x + xcds * (slot / splits);
+    if (x >= xcds) {
+      // Not the device pd_probe_xcds saw: counted in an otherwise unused word
+      // (word 1 of group 0's counter line), which the tests require to stay 0.
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(counters + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
     if (g >= groups) return;
     p = slot % splits;
     kh = g % Hkv;
     b = g / Hkv;
-    // The mapping relies on the dispatch order; a workgroup on another XCD
-    // counts itself in an otherwise unused word of the group's counter line,
-    // which the host-side checks read (it is never set on a correctly placed
-    // launch).
-    if ((__builtin_amdgcn_s_getreg((15 << 11) | kHwRegXccId) & 0xf) != x && threadIdx.x == 0)
-      __hip_atomic_fetch_add(counters + int64_t(g) * kCountersPerGroup + 1, 1, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
   }
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1547,8 +1552,10 @@ extern "C" int pd_probe_xcds(int32_t* xcds) {
   }
   int n = 1;
   for (int i = 0; i < kXccProbeGroups; ++i) n = host[i] + 1 > n ? host[i] + 1 : n;
+  // Round-robin from one offset c: host[i] == (i + c) % n for every i.
+  const int c = host[0];
   bool round_robin = true;
-  for (int i = 0; i < kXccProbeGroups; ++i) round_robin = round_robin && host[i] == i % n;
+  for (int i = 0; i < kXccProbeGroups; ++i) round_robin = round_robin && host[i] == (i + c) % n;
   const int layout = round_robin ? n : -1;
   g_xcd_layout[dev].store(layout, std::memory_order_relaxed);
   *xcds = layout;
