@@ -40,15 +40,54 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 __device__ __forceinline__ float ln_fast(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
 __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
+// x of lane L ^ M, for M = 1, 2, 4, 8, 16 or 32, with VALU lane moves (no LDS
+// round trip, unlike ds_bpermute).  Lane layouts checked on gfx950 with an
+// in-bounds probe: DPP quad_perm [1,0,3,2] / [2,3,0,1] give L ^ 1 / L ^ 2;
+// row_shl:n gives lane L + n of the same 16-lane row and row_shr:n lane L - n,
+// so L ^ 4 and L ^ 8 select between the two by the lane bit; for
+// v_permlane16_swap(x, x) the first result holds x[L ^ 16] in the odd 16-lane
+// rows and the second in the even rows, and v_permlane32_swap likewise for
+// the upper / lower 32 lanes.
+template <int M>
+__device__ __forceinline__ float xor_lanes(float x, int lane) {
+  const int v = __float_as_int(x);
+  if constexpr (M == 1) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));
+  } else if constexpr (M == 2) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));
+  } else if constexpr (M == 4 || M == 8) {
+    const int up = __builtin_amdgcn_mov_dpp(v, 0x100 + M, 0xF, 0xF, false);  // row_shl:M
+    const int dn = __builtin_amdgcn_mov_dpp(v, 0x110 + M, 0xF, 0xF, false);  // row_shr:M
+    return __int_as_float((lane & M) ? dn : up);
+  } else if constexpr (M == 16) {
+    const auto a = __builtin_amdgcn_permlane16_swap(unsigned(v), unsigned(v), false, false);
+    return __uint_as_float((lane & 16) ? a[0] : a[1]);
+  } else {
+    static_assert(M == 32, "xor distance");
+    const auto a = __builtin_amdgcn_permlane32_swap(unsigned(v), unsigned(v), false, false);
+    return __uint_as_float((lane & 32) ? a[0] : a[1]);
+  }
+}
+
+// x of lane L ^ m for any m in [0, 64) (wavefront-uniform), one move per set bit.
+__device__ __forceinline__ float xor_lanes_any(float x, int m, int lane) {
+  if (m & 32) x = xor_lanes<32>(x, lane);
+  if (m & 16) x = xor_lanes<16>(x, lane);
+  if (m & 8) x = xor_lanes<8>(x, lane);
+  if (m & 4) x = xor_lanes<4>(x, lane);
+  if (m & 2) x = xor_lanes<2>(x, lane);
+  if (m & 1) x = xor_lanes<1>(x, lane);
   return x;
 }
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
-  return x;
+
+__device__ __forceinline__ float wave_max(float x) {
+  const int lane = __lane_id();
+  x = fmaxf(x, xor_lanes<32>(x, lane));
+  x = fmaxf(x, xor_lanes<16>(x, lane));
+  x = fmaxf(x, xor_lanes<8>(x, lane));
+  x = fmaxf(x, xor_lanes<4>(x, lane));
+  x = fmaxf(x, xor_lanes<2>(x, lane));
+  return fmaxf(x, xor_lanes<1>(x, lane));
 }
 
 // Reductions over the four 16-lane rows of a wavefront (lanes L, L^16, L^32,
@@ -156,6 +195,12 @@ __device__ __forceinline__ void lse_load(const float* __restrict__ lrow, int byt
 }
 
 // lse_weights on the values lse_load returned for the row.
+// Lane j < lanes needs e_{j + t lanes} for t = 1, 2, ...: split j + t lanes is
+// element j + (t lanes & 63) of e0 (t lanes < 64) or e1, and since lanes is a
+// power of two and j < lanes, j + (t lanes & 63) = j ^ (t lanes & 63), so
+// every term is an xor move.  The plan's lane counts (capped at 32 for D 128
+// and 256, 16 for D 64) take an unrolled path; any other power of two a caller
+// passes takes the general loop.
 __device__ __forceinline__ void lse_weights_of(float a, float c, int splits, int lanes, int lane,
                                                float& w0, float& w1) {
   const float v0 = lane < splits ? a : -INFINITY;
@@ -165,11 +210,37 @@ __device__ __forceinline__ void lse_weights_of(float a, float c, int splits, int
   const float e0 = exp_fast(v0 - mx), e1 = exp_fast(v1 - mx);
   float s = e0;
   const int terms = (splits + lanes - 1) / lanes;
-  for (int t = 1; t < terms; ++t) {
-    const int off = t * lanes;  // lanes j < `lanes` read split j + off < 128
-    s += __shfl(off < 64 ? e0 : e1, (lane + off) & 63);
+  if (terms > 1) {
+    // Terms past the last split are exact zeros and are not added.
+    const float e0x32 = xor_lanes<32>(e0, lane), e1x32 = xor_lanes<32>(e1, lane);
+    if (lanes == 32) {
+      s += e0x32;                        // t = 1: splits j + 32
+      if (terms > 2) s += e1;            // t = 2: j + 64
+      if (terms > 3) s += e1x32;         // t = 3: j + 96
+    } else if (lanes != 16) {
+      for (int t = 1; t < terms; ++t) {
+        const int off = t * lanes;
+        s += xor_lanes_any(off < 64 ? e0 : e1, off & 63, lane);
+      }
+    } else {
+      const float e0x16 = xor_lanes<16>(e0, lane), e1x16 = xor_lanes<16>(e1, lane);
+      const float e0x48 = xor_lanes<16>(e0x32, lane), e1x48 = xor_lanes<16>(e1x32, lane);
+      s += e0x16;                        // j + 16
+      if (terms > 2) s += e0x32;         // j + 32
+      if (terms > 3) s += e0x48;         // j + 48
+      if (terms > 4) s += e1;            // j + 64
+      if (terms > 5) s += e1x16;         // j + 80
+      if (terms > 6) s += e1x32;         // j + 96
+      if (terms > 7) s += e1x48;         // j + 112
+    }
   }
-  for (int m = lanes >> 1; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+  // Halving tree: lane j adds lane j ^ m for m = lanes / 2, ..., 1.
+  if (lanes > 32) s += xor_lanes<32>(s, lane);
+  if (lanes > 16) s += xor_lanes<16>(s, lane);
+  if (lanes > 8) s += xor_lanes<8>(s, lane);
+  if (lanes > 4) s += xor_lanes<4>(s, lane);
+  if (lanes > 2) s += xor_lanes<2>(s, lane);
+  if (lanes > 1) s += xor_lanes<1>(s, lane);
   const float total = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 0));
   const float logsum = total > 0.f ? ln_fast(total) + mx : INFINITY;
   w0 = exp_fast(v0 - logsum);
