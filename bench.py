@@ -457,6 +457,58 @@ def profile_launches(torch, which, calls=50):
     print(json.dumps({"profiled": which}))
 
 
+def ab_report(torch, args):
+    """Paired A/B report (paged_decode.evidence) of variants of the headline call: each is
+    timed as 32- and 128-call graphs over shuffled rounds; ratios are per round against
+    the first variant."""
+    from paged_decode import _native, evidence
+    from paged_decode.matched_splitkv import matched_decode
+    ctx = args.ctx
+    case = matched_case(torch, 1, 16, 4, 256, max(2112, ctx), [ctx], 20261105)
+    q, k, v, table, lens = case["tensors"]
+    res, plan, scale = case["res"], case["plan"], 256 ** -0.5
+    known = {"two_launch": case["full"], "fused": case["fused"],
+             "partition": case["partition"], "merge": case["merge"],
+             "noalloc": lambda: _native.matched_decode_noalloc(
+                 q, k, v, table, lens, res.out, 4, plan.splits, plan.tokens_per_split,
+                 plan.tile_tokens, scale)}
+    variants = {}
+    for item in args.ab.split(","):
+        if "=" in item:
+            name, path = item.split("=", 1)
+            other = _native.load_library(os.path.abspath(path))
+
+            def call(other=other):
+                _native.partition(q, k, v, table, lens, res.partials, res.lse, 4, plan.splits,
+                                  plan.tokens_per_split, plan.tile_tokens, scale, library=other)
+                _native.lse_merge(res.partials, res.lse, res.out, plan.lse_lanes, library=other)
+            variants[name] = call
+        elif item in known:
+            variants[item] = known[item]
+        else:
+            raise SystemExit(f"unknown A/B variant {item!r}; known: {sorted(known)} or NAME=PATH")
+    names = list(variants)
+    rows = evidence.paired_timings(torch, variants, rounds=args.ab_rounds)
+    report = evidence.paired_report(rows, names, names[0], args.ab_rounds)
+    report.update(workload=f"matched decode B=1 Hq=16 Hkv=4 D=256 ctx {ctx}, plan "
+                           f"{plan.splits}x{plan.tokens_per_split}",
+                  rows=rows, environment=benchmark_protocol_fingerprint(torch))
+    if args.ab_out:
+        evidence.write_json_exclusive(args.ab_out, report)
+    for name, x in report["variants"].items():
+        t = x["us_per_call"]["128"]
+        r = x["over_baseline"]
+        progress(f"{name}: {t['median']:.3f} us/call (rounds {t['min']:.3f}-{t['max']:.3f}), "
+                 f"x{r['median']:.4f} of {names[0]} ({r['min']:.4f}-{r['max']:.4f}), "
+                 f"t32/t128-1 = {x['unroll_relative_delta']:+.4f}")
+    print(json.dumps({k: v for k, v in report.items() if k != "rows"}))
+
+
+def benchmark_protocol_fingerprint(torch):
+    from paged_decode import benchmark_protocol
+    return benchmark_protocol.fingerprint(torch)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -470,6 +522,12 @@ def main():
                     help="only make eager launches for rocprofv3 (calibration copy + cases)")
     ap.add_argument("--require-idle-gpu", action="store_true",
                     help="refuse to run (before any GPU work) if amd-smi lists other processes")
+    ap.add_argument("--ab", default=None, metavar="V1,V2,...",
+                    help="paired A/B report of variants of the headline call instead of the "
+                         "benchmark: two_launch, fused, noalloc, partition, merge, or NAME=PATH "
+                         "for the two launches through another build of libpaged_decode.so")
+    ap.add_argument("--ab-rounds", type=int, default=5)
+    ap.add_argument("--ab-out", default=None, help="also write the report to this new JSON file")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -484,6 +542,9 @@ def main():
     _native.lib()
     if args.profile:
         profile_launches(torch, args.profile)
+        return
+    if args.ab:
+        ab_report(torch, args)
         return
 
     ctx, capacity = args.ctx, max(2112, args.ctx)

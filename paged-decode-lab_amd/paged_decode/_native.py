@@ -51,27 +51,39 @@ SIGNATURES = {
 _lib = None
 
 
+def load_library(path):
+    """A ctypes handle of a libpaged_decode.so build at ``path``, with the signatures set.
+    Every entry point below takes ``library=`` to run through such a handle instead of
+    the package's own build (an A/B of two builds in one process)."""
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is not built: run `make -C paged-decode-lab_amd/csrc` "
+            "(or __graft_entry__.build()); there is no fallback implementation")
+    handle = ctypes.CDLL(path)
+    for name, argtypes in SIGNATURES.items():
+        try:
+            fn = getattr(handle, name)
+        except AttributeError:
+            if path == LIB_PATH:
+                raise
+            continue  # an older build compared in an A/B run: calls to it raise
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_char_p if name == "pd_last_error" else ctypes.c_int
+    return handle
+
+
 def lib():
     """The loaded library; raises RuntimeError when it has not been built."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(
-                f"{LIB_PATH} is not built: run `make -C paged-decode-lab_amd/csrc` "
-                "(or __graft_entry__.build()); there is no fallback implementation")
-        handle = ctypes.CDLL(LIB_PATH)
-        for name, argtypes in SIGNATURES.items():
-            fn = getattr(handle, name)
-            fn.argtypes = argtypes
-            fn.restype = ctypes.c_char_p if name == "pd_last_error" else ctypes.c_int
-        _lib = handle
+        _lib = load_library(LIB_PATH)
     return _lib
 
 
-def check(status):
+def check(status, library=None):
     if status == PD_OK:
         return
-    message = lib().pd_last_error().decode()
+    message = (library or lib()).pd_last_error().decode()
     if status == PD_EINVAL:
         raise ValueError(message)
     raise RuntimeError(message)
@@ -97,13 +109,14 @@ def stream_handle(device):
 
 
 def partition(q, k, v, tables, lengths, partials, lse, num_kv_heads, splits, tokens_per_split,
-              tile_tokens, scale):
+              tile_tokens, scale, library=None):
     b, h, d = q.shape
-    check(lib().pd_partition(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
-                             tables.data_ptr(), tables.stride(0), tables.shape[1],
-                             lengths.data_ptr(), partials.data_ptr(), lse.data_ptr(), b, h,
-                             num_kv_heads, d, splits,
-                             tokens_per_split, tile_tokens, scale, stream_handle(q.device)))
+    L = library or lib()
+    check(L.pd_partition(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                         tables.data_ptr(), tables.stride(0), tables.shape[1],
+                         lengths.data_ptr(), partials.data_ptr(), lse.data_ptr(), b, h,
+                         num_kv_heads, d, splits,
+                         tokens_per_split, tile_tokens, scale, stream_handle(q.device)), L)
 
 
 _probed = {}
@@ -123,32 +136,35 @@ def probe_xcds(device):
 
 
 def matched_decode(q, k, v, tables, lengths, partials, lse, counters, out, num_kv_heads, splits,
-                   tokens_per_split, tile_tokens, scale):
+                   tokens_per_split, tile_tokens, scale, library=None):
     b, h, d = q.shape
-    check(lib().pd_matched_decode(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
-                                  v.data_ptr(), tables.data_ptr(), tables.stride(0),
-                                  tables.shape[1], lengths.data_ptr(), partials.data_ptr(),
-                                  lse.data_ptr(),
-                                  counters.data_ptr(), out.data_ptr(), b, h, num_kv_heads, d,
-                                  splits, tokens_per_split, tile_tokens, scale,
-                                  stream_handle(q.device)))
+    L = library or lib()
+    check(L.pd_matched_decode(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                              v.data_ptr(), tables.data_ptr(), tables.stride(0),
+                              tables.shape[1], lengths.data_ptr(), partials.data_ptr(),
+                              lse.data_ptr(),
+                              counters.data_ptr(), out.data_ptr(), b, h, num_kv_heads, d,
+                              splits, tokens_per_split, tile_tokens, scale,
+                              stream_handle(q.device)), L)
 
 
 def matched_decode_noalloc(q, k, v, tables, lengths, out, num_kv_heads, splits,
-                           tokens_per_split, tile_tokens, scale):
+                           tokens_per_split, tile_tokens, scale, library=None):
     """pd_matched_decode with the split workspace in the library's static device scratch."""
     b, h, d = q.shape
-    check(lib().pd_matched_decode_noalloc(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
-                                          v.data_ptr(), tables.data_ptr(), tables.stride(0),
-                                          tables.shape[1], lengths.data_ptr(), out.data_ptr(), b,
-                                          h, num_kv_heads, d, splits, tokens_per_split,
-                                          tile_tokens, scale, stream_handle(q.device)))
+    L = library or lib()
+    check(L.pd_matched_decode_noalloc(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                                      v.data_ptr(), tables.data_ptr(), tables.stride(0),
+                                      tables.shape[1], lengths.data_ptr(), out.data_ptr(), b,
+                                      h, num_kv_heads, d, splits, tokens_per_split,
+                                      tile_tokens, scale, stream_handle(q.device)), L)
 
 
-def lse_merge(partials, lse, out, lse_lanes):
+def lse_merge(partials, lse, out, lse_lanes, library=None):
     b, h, splits, d = partials.shape
-    check(lib().pd_lse_merge(partials.data_ptr(), lse.data_ptr(), out.data_ptr(), b, h, d, splits,
-                             lse_lanes, stream_handle(partials.device)))
+    L = library or lib()
+    check(L.pd_lse_merge(partials.data_ptr(), lse.data_ptr(), out.data_ptr(), b, h, d, splits,
+                         lse_lanes, stream_handle(partials.device)), L)
 
 
 def base(q, k, v, tables, lengths, out, num_kv_heads, scale):
