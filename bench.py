@@ -463,8 +463,8 @@ def ab_report(torch, args):
     the first variant."""
     from paged_decode import _native, evidence
     from paged_decode.matched_splitkv import matched_decode
-    ctx = args.ctx
-    case = matched_case(torch, 1, 16, 4, 256, max(2112, ctx), [ctx], 20261105)
+    ctx, batch = args.ctx, args.ab_batch
+    case = matched_case(torch, batch, 16, 4, 256, max(2112, ctx), [ctx] * batch, 20261105)
     q, k, v, table, lens = case["tensors"]
     res, plan, scale = case["res"], case["plan"], 256 ** -0.5
     known = {"two_launch": case["full"], "fused": case["fused"],
@@ -490,7 +490,7 @@ def ab_report(torch, args):
     names = list(variants)
     rows = evidence.paired_timings(torch, variants, rounds=args.ab_rounds)
     report = evidence.paired_report(rows, names, names[0], args.ab_rounds)
-    report.update(workload=f"matched decode B=1 Hq=16 Hkv=4 D=256 ctx {ctx}, plan "
+    report.update(workload=f"matched decode B={batch} Hq=16 Hkv=4 D=256 ctx {ctx}, plan "
                            f"{plan.splits}x{plan.tokens_per_split}",
                   rows=rows, environment=benchmark_protocol_fingerprint(torch))
     if args.ab_out:
@@ -527,6 +527,8 @@ def main():
                          "benchmark: two_launch, fused, noalloc, partition, merge, or NAME=PATH "
                          "for the two launches through another build of libpaged_decode.so")
     ap.add_argument("--ab-rounds", type=int, default=5)
+    ap.add_argument("--ab-batch", type=int, default=1,
+                    help="sequences of the A/B workload (each of --ctx tokens)")
     ap.add_argument("--ab-out", default=None, help="also write the report to this new JSON file")
     args = ap.parse_args()
     if args.gpus != 1:
