@@ -537,7 +537,12 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   __shared__ __attribute__((aligned(16))) char ps[kTerms][16 * P::kPitch];
   __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
 
-  const int p = blockIdx.x;
+  // The fixed-split protocol walks the whole context of its (kv head,
+  // sequence) in one workgroup (grid.x = 1) and writes the (m, l, acc) of each
+  // T-token partition as the walk leaves it, so a sequence's partitions share
+  // one workgroup's start and its K / V pipeline.
+  constexpr bool kWalk = kMode == kSplit;
+  const int p = kWalk ? 0 : int(blockIdx.x);
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
   const int qb = kh * G + 16 * slice;
   const int Gs = min(16, G - 16 * slice);
@@ -551,12 +556,13 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   PageWindow<2> pw;
   pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
   const int length = order >= 0 ? seq.length : lengths[b];
-  const int end = min(start + T, length);
+  const int end = min(kWalk ? splits * T : start + T, length);
   const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
   if constexpr (!kFused) {
     if (count == 0) {
-      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, p, partials, lse_out, out,
-                                      maxima);
+      for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
+        write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
+                                        maxima);
       return;
     }
   }
@@ -732,6 +738,43 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     pv_step(std::integral_constant<int, 1>{});
   };
 
+  // kWalk: after tile ti, the first tile of partition ti / tpp, that
+  // partition is complete: its denominators are summed over the waves and its
+  // (m, l, acc) stored (kernels.py:77-80), and the running state restarts for
+  // the partition before it.  The loads of the next tiles stay in flight.
+  const int tpp = T / TILE;
+  auto flush = [&](int ti) __attribute__((always_inline)) {
+    if (ti % tpp) return;
+    const int part = ti / tpp;
+    const float l = sum_rows(l_own);
+    if (lane < 16) sm.lsum[w][lane] = l;
+    lds_barrier();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * qg + r;
+      if (h >= Gs) break;
+      const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
+      const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + part;
+      const int col = w * P::kCols + qh;
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r];
+      if (w == 0 && qh == 0) {
+        maxima[orow] = m4[r];
+        lse_out[orow] = den;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
+    m_own = -INFINITY;
+    l_own = 0.f;
+  };
+  auto finish_tile = [&](const char* slot, int ti, bool first) __attribute__((always_inline)) {
+    finish(slot, ti, first);
+    if constexpr (kWalk) flush(ti);
+  };
+
   // Reverse tile walk (matched_splitkv.py:71), last tile first; register sets
   // A, B and LDS slots vs0, vs1 alternate.  The first loads, K(ti), V(ti),
   // K(ti - 1), come in the steady-state order, so the vmcnt above is exact
@@ -751,11 +794,11 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       scores(A, ti);
       issue_v(vs1, ti - 1);
       issue_k(A, ti - 2);
-      finish(vs0, ti, first);
+      finish_tile(vs0, ti, first);
       scores(B, ti - 1);
       issue_v(vs0, ti - 2);
       issue_k(B, ti - 3);
-      finish(vs1, ti - 1, false);
+      finish_tile(vs1, ti - 1, false);
       ti -= 2;
       first = false;
     }
@@ -763,22 +806,30 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       scores(A, 2);
       issue_v(vs1, 1);
       issue_k(A, 0);
-      finish(vs0, 2, first);
+      finish_tile(vs0, 2, first);
       scores(B, 1);
       issue_v(vs0, 0);
-      finish(vs1, 1, false);
+      finish_tile(vs1, 1, false);
       scores(A, 0);
-      finish(vs0, 0, false);
+      finish_tile(vs0, 0, false);
     } else if (ti == 1) {
       scores(A, 1);
       issue_v(vs1, 0);
-      finish(vs0, 1, first);
+      finish_tile(vs0, 1, first);
       scores(B, 0);
-      finish(vs1, 0, false);
+      finish_tile(vs1, 0, false);
     } else {
       scores(A, 0);
-      finish(vs0, 0, first);
+      finish_tile(vs0, 0, first);
     }
+  }
+
+  if constexpr (kWalk) {
+    // Partitions past the sequence's last token are empty.
+    for (int pp = (end + T - 1) / T; pp < splits; ++pp)
+      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
+                                      maxima);
+    return;
   }
 
   // ---- epilogue: denominators over the waves; O needs no reduction
@@ -1683,7 +1734,9 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
                   int(tsb), width, lengths, accums, denoms,
                   nullptr, static_cast<uint16_t*>(out), maxima, num_heads, num_kv_heads, G, hs,
                   kSplitMode ? parts : 1, T, float(scale), float(scale * 1.4426950408889634)};
-  const dim3 grid(kSplitMode ? parts : 1, num_kv_heads * hs, batch);
+  // At D = 256 the fixed-split protocol walks each sequence in one workgroup
+  // (matched_cols_kernel); below it, one workgroup runs per partition.
+  const dim3 grid(kSplitMode && head_dim != 256 ? parts : 1, num_kv_heads * hs, batch);
   a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int gp = padded_group(G < 16 ? G : 16);
