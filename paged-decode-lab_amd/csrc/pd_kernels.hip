@@ -139,7 +139,11 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
   __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
 
-  const int p = blockIdx.x;
+  // The fixed-split protocol walks the whole context of its (kv head,
+  // sequence) in one workgroup (grid.x = 1) and writes the (m, l, acc) of each
+  // T-token partition as the walk leaves it (see flush below).
+  constexpr bool kWalk = kMode == kSplit;
+  const int p = kWalk ? 0 : int(blockIdx.x);
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
   const int qb = kh * G + 16 * slice;            // first query head of this workgroup
   const int Gs = min(16, G - 16 * slice);        // query heads of this workgroup
@@ -155,12 +159,13 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   PageWindow<2> pw;
   pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
   const int length = order >= 0 ? seq.length : lengths[b];
-  const int end = min(start + T, length);
+  const int end = min(kWalk ? splits * T : start + T, length);
   const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
   if constexpr (!kFused) {
     if (count == 0) {
-      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, p, partials, lse_out, out,
-                                      maxima);
+      for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
+        write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
+                                        maxima);
       return;
     }
   }
@@ -336,6 +341,65 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
     }
   };
 
+  // O of wavefront w as 16-byte slots: slot (q, j, n) holds the four heads
+  // 4q .. 4q+3 of column 16j + n, i.e. lane 16q + n's acc[j] as it is (one
+  // ds_write_b128 per column block).  Only the row groups q < NQ hold real
+  // heads.
+  constexpr int NQ = GP >= 4 ? GP / 4 : 1;
+  constexpr int kSlots = NQ * C::kNB * 16;
+  static_assert(kSlots * 16 <= C::kSlot, "a wavefront's O fits its V rows");
+
+  // kWalk: after tile ti, the first tile of partition ti / tpp, that
+  // partition is complete.  Each wavefront has read its own V rows of tile ti
+  // (in `slot`), and the next copies into that slot are issued only after
+  // this, so its rows there hold its O; thread t then sums slot t over the
+  // waves (the epilogue's fixed order), the partition's (m, l, acc) are stored
+  // (kernels.py:77-80), and the running state restarts for the partition
+  // before it.  Copies and loads of the next tiles stay in flight.
+  const int tpp = T / TILE;
+  auto flush = [&](char* slot, int ti) __attribute__((always_inline)) {
+    if (ti % tpp) return;
+    const int part = ti / tpp;
+    const float l = sum_rows(l_own);
+    if (lane < 16) sm.lsum[w][lane] = l;
+    if (tid < 16) sm.mfin[tid] = m_own;
+    if (qg < NQ) {
+      floatx4_t* mine = reinterpret_cast<floatx4_t*>(slot + w * C::kSlot) + qg * C::kNB * 16 + qh;
+#pragma unroll
+      for (int j = 0; j < C::kNB; ++j) mine[16 * j] = acc[j];
+    }
+    lds_barrier();
+    for (int sl = tid; sl < kSlots; sl += kThreads) {
+      const int q = sl / (C::kNB * 16), col = sl % (C::kNB * 16);
+      const floatx4_t* o = reinterpret_cast<const floatx4_t*>(slot) + sl;
+      constexpr int kW = C::kSlot / 16;  // floatx4 per wavefront's rows
+      const floatx4_t o0 = o[0], o1 = o[kW], o2 = o[2 * kW], o3 = o[3 * kW];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * q + r;
+        if (h >= Gs) break;
+        const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + part;
+        partials[orow * D + col] = (o0[r] + o1[r]) + (o2[r] + o3[r]);
+        if (col == 0) {
+          maxima[orow] = sm.mfin[h];
+          lse_out[orow] = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
+        }
+      }
+    }
+    lds_barrier();  // every read of the slot is done before copies refill it
+#pragma unroll
+    for (int j = 0; j < C::kNB; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
+    m_own = -INFINITY;
+    l_own = 0.f;
+  };
+  auto step = [&](KTile<D, GP>& R, char* slot, int ti, bool first, int knext)
+                  __attribute__((always_inline)) {
+    process(R, slot, ti, first, knext);
+    if constexpr (kWalk) flush(slot, ti);
+  };
+
   // Reverse tile walk (matched_splitkv.py:71): last tile first.  Two register
   // sets and two LDS slots alternate.  V rows are loaded one tile ahead, into
   // the LDS slot the previous tile's PV has finished reading; K rows two tiles
@@ -348,7 +412,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
     KTile<D, GP> A;
     issue_k(A, 0);
     issue_v(vs0, 0);
-    process(A, vs0, 0, true, -1);
+    step(A, vs0, 0, true, -1);
   } else if (count > 1) {
     KTile<D, GP> A, B;
     int ti = count - 1;
@@ -358,23 +422,31 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
     bool first = true;
     while (ti >= 3) {
       issue_v(vs1, ti - 1);
-      process(A, vs0, ti, first, ti - 2);
+      step(A, vs0, ti, first, ti - 2);
       issue_v(vs0, ti - 2);
-      process(B, vs1, ti - 1, false, ti - 3);
+      step(B, vs1, ti - 1, false, ti - 3);
       ti -= 2;
       first = false;
     }
     if (ti == 2) {
       issue_v(vs1, 1);
-      process(A, vs0, 2, first, 0);
+      step(A, vs0, 2, first, 0);
       issue_v(vs0, 0);
-      process(B, vs1, 1, false, -1);
-      process(A, vs0, 0, false, -1);
+      step(B, vs1, 1, false, -1);
+      step(A, vs0, 0, false, -1);
     } else {  // ti == 1
       issue_v(vs1, 0);
-      process(A, vs0, 1, first, -1);
-      process(B, vs1, 0, false, -1);
+      step(A, vs0, 1, first, -1);
+      step(B, vs1, 0, false, -1);
     }
+  }
+
+  if constexpr (kWalk) {
+    // Partitions past the sequence's last token are empty.
+    for (int pp = (end + T - 1) / T; pp < splits; ++pp)
+      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
+                                      maxima);
+    return;
   }
 
   // ---- epilogue: combine the 4 waves' accumulators and denominators
@@ -382,12 +454,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   if (lane < 16) sm.lsum[w][lane] = l;
   if (tid < 16) sm.mfin[tid] = m_own;
   __syncthreads();  // every wavefront is done with its V rows (aliased by red)
-  // O of wavefront w as 16-byte slots: slot (q, j, n) holds the four heads
-  // 4q .. 4q+3 of column 16j + n, i.e. lane 16q + n's acc[j] as it is (one
-  // ds_write_b128 per column block).  Only the row groups q < NQ hold real
-  // heads.  Waves 0, 1 use vs0 and waves 2, 3 use vs1.
-  constexpr int NQ = GP >= 4 ? GP / 4 : 1;
-  constexpr int kSlots = NQ * C::kNB * 16;
+  // The slots of wavefronts 0, 1 go to vs0 and those of 2, 3 to vs1.
   static_assert(2 * kSlots * 16 <= 4 * C::kSlot, "reduction buffer");
   auto red = [&](int wave) __attribute__((always_inline)) {
     return reinterpret_cast<floatx4_t*>(wave < 2 ? vs0 : vs1) + (wave & 1) * kSlots;
@@ -1734,9 +1801,9 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
                   int(tsb), width, lengths, accums, denoms,
                   nullptr, static_cast<uint16_t*>(out), maxima, num_heads, num_kv_heads, G, hs,
                   kSplitMode ? parts : 1, T, float(scale), float(scale * 1.4426950408889634)};
-  // At D = 256 the fixed-split protocol walks each sequence in one workgroup
-  // (matched_cols_kernel); below it, one workgroup runs per partition.
-  const dim3 grid(kSplitMode && head_dim != 256 ? parts : 1, num_kv_heads * hs, batch);
+  // The fixed-split protocol walks each sequence in one workgroup and writes
+  // every partition of it (grid.x = 1), like the base protocol.
+  const dim3 grid(1, num_kv_heads * hs, batch);
   a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int gp = padded_group(G < 16 ? G : 16);
