@@ -186,3 +186,40 @@ def test_d256_tile_counts_of_the_column_split_kernel(backend):
     torch.cuda.synchronize()
     assert_close_dense(actual, torch_dense(*g))
     assert_within_one_ulp(actual, oracle_for(case, backend, spec), backend)
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (128, 8, 2), (256, 8, 2), (64, 32, 2)])
+@pytest.mark.parametrize("tiles_per_partition", [1, 2, 3, 5])
+def test_fixed_split_walk_partition_sizes(dim, hq, hkv, tiles_per_partition):
+    """pd_split_fixed walks each sequence in one workgroup and writes every partition as
+    the walk leaves it.  Partition sizes of 1, 2, 3 and 5 tiles, lengths at and around
+    partition and page boundaries, the empty partitions past each sequence's end, and
+    NaN-poisoned tails: the (m, l, acc) workspace against oracle/splitk.py, and the merged
+    output at one bf16 ulp."""
+    from paged_decode import _native
+    tile = 16384 // dim
+    part = tiles_per_partition * tile
+    cap = 4 * part + 3 * tile
+    lengths = [0, 1, tile, part - 1, part, part + 1, 2 * part + tile // 2, cap]
+    q, k, v, table, lens = make_case(lengths, hq, hkv, dim, seed=tiles_per_partition,
+                                     capacity=cap)
+    poison_tails(k, v, table, lens)
+    case = (q, k, v, table, lens)
+    g = to_gpu(case)
+    parts = -(-cap // part)
+    maxima = torch.empty((len(lengths), hq, parts), device="cuda")
+    denoms = torch.empty_like(maxima)
+    accums = torch.empty((len(lengths), hq, parts, dim), device="cuda")
+    out = torch.empty((len(lengths), hq, dim), device="cuda", dtype=torch.bfloat16)
+    _native.split_fixed(*g, maxima, denoms, accums, hkv, parts, part, dim ** -0.5)
+    _native.ml_merge(maxima, denoms, accums, out, len(lengths))
+    torch.cuda.synchronize()
+    m_ref, l_ref, a_ref = OS.split_partitions(*case, parts, part_size=part)
+    np.testing.assert_array_equal(np.isinf(to_np(maxima)), np.isinf(m_ref))
+    live = np.isfinite(m_ref)
+    np.testing.assert_allclose(to_np(maxima)[live], m_ref[live], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(to_np(denoms), l_ref, rtol=3e-5, atol=1e-6)
+    np.testing.assert_allclose(to_np(accums), a_ref, rtol=3e-5, atol=3e-5)
+    assert_within_one_ulp(out, OS.ml_merge(m_ref, l_ref, a_ref),
+                          f"D{dim} {hq}/{hkv} {tiles_per_partition}-tile partitions")
+    assert torch.count_nonzero(out[0]) == 0
