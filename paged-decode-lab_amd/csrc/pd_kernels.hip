@@ -118,7 +118,7 @@ __device__ __forceinline__ void write_empty_partition(int tid, int b, int Hq, in
   }
 }
 
-template <int D, int GP, bool kFused, int kMode>
+template <int D, int GP, bool kFused, int kMode, bool kPair = false>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
                          const uint16_t* __restrict__ q, int tsb, int width, int order, int T,
@@ -129,8 +129,18 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
                          int splits, float scale, float c) {
   static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
   static_assert(D < 256, "D = 256 runs matched_cols_kernel");
+  static_assert(!kPair || kMode != kMatched, "kv-head pairs change the tile of the protocol");
   using C = Matched<D, GP>;
   constexpr int TILE = C::kTile;
+  // kPair (base and fixed-split protocols): the workgroup serves kv heads
+  // 2 kh and 2 kh + 1 and their 2 G query heads.  Row R of a tile is token
+  // R / 2 of kv head 2 kh + R % 2: the two heads' rows of a token are 4 D
+  // contiguous bytes, so a tile holds TILE / 2 tokens; query head e G + g
+  // (e = 0, 1) scores only the rows of its own kv head (odd or even), and the
+  // other rows get probability 0.  At D = 64 a head's row is one 128-byte
+  // line, Hkv lines apart from the next token's; the pair reads two adjacent
+  // lines per token.
+  constexpr int TTOK = kPair ? TILE / 2 : TILE;  // tokens per tile
   __shared__ MatchedShared<D, GP> sm;
   // V rows of the tile being computed and of the one being loaded; two arrays
   // (not one) so that the compiler's wait before reading one slot does not
@@ -145,8 +155,9 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   constexpr bool kWalk = kMode == kSplit;
   const int p = kWalk ? 0 : int(blockIdx.x);
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
-  const int qb = kh * G + 16 * slice;            // first query head of this workgroup
-  const int Gs = min(16, G - 16 * slice);        // query heads of this workgroup
+  const int kvh = kPair ? 2 * kh : kh;           // (first) kv head of this workgroup
+  const int qb = kvh * G + 16 * slice;           // first query head of this workgroup
+  const int Gs = min(16, (kPair ? 2 * G : G) - 16 * slice);  // query heads of this workgroup
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = lane & 15, qg = lane >> 4;
@@ -160,7 +171,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
   const int length = order >= 0 ? seq.length : lengths[b];
   const int end = min(kWalk ? splits * T : start + T, length);
-  const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+  const int count = end > start ? (end - start + TTOK - 1) / TTOK : 0;
   if constexpr (!kFused) {
     if (count == 0) {
       for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
@@ -184,10 +195,11 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   // Tile-relative byte offsets: K pieces of this lane, and the source of each
   // 16-byte LDS piece this lane fills (v_copy_offset); rows past the sequence
   // end read past the buffer, i.e. zeros.
-  const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
+  const int koff = (tile_row_elems<D, kPair>(w * C::kTW + qh, int(RS)) + 8 * qg) * 2;
+  constexpr int kGroupRows = kPair ? 8 : 16;  // token rows of a 16-row group
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, false>(i, lane, w, int(RS));
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, false, kPair>(i, lane, w, int(RS));
   // This lane's transposed-read row within its wavefront's LDS rows: row
   // 4qg + qh/4 of each 16-row group (the row v_read_offset swizzles by).
   const int trb = w * C::kSlot + (4 * qg + (qh >> 2)) * C::kPitch;
@@ -203,17 +215,17 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
 
   // Loads of tile ti (0 <= ti < count): K rows into registers, V rows into LDS.
   auto issue_k = [&](KTile<D, GP>& R, int ti) __attribute__((always_inline)) {
-    const int t0 = start + ti * TILE;
-    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
+    const int t0 = start + ti * TTOK;
+    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kvh, D);
 #pragma unroll
     for (int g = 0; g < C::kNG; ++g)
 #pragma unroll
       for (int ch = 0; ch < C::kCH; ++ch)
-        R.k[g][ch] = buffer_load16(buf.k, koff + g * 16 * int(RS) * 2 + 64 * ch);
+        R.k[g][ch] = buffer_load16(buf.k, koff + g * kGroupRows * int(RS) * 2 + 64 * ch);
   };
   auto issue_v = [&](char* slot, int ti) __attribute__((always_inline)) {
-    const int t0 = start + ti * TILE;
-    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
+    const int t0 = start + ti * TTOK;
+    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kvh, D);
 #pragma unroll
     for (int i = 0; i < C::kDma; ++i)
       lds_copy16(buf.v, slot + w * C::kSlot + 1024 * i, voff[i]);
@@ -225,7 +237,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   // rows of tile knext (two tiles ahead of ti in the walk).
   auto process = [&](KTile<D, GP>& R, const char* slot, int ti, bool first, int knext)
                      __attribute__((always_inline)) {
-    const int nvalid = end - (start + ti * TILE);
+    const int nvalid = end - (start + ti * TTOK);
     // ---- scores
     floatx4_t s[C::kNG];
 #pragma unroll
@@ -250,7 +262,16 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[g][r] *= scale;
     }
-    if (nvalid < TILE) {
+    if constexpr (kPair) {
+      // Rows of the other kv head (row parity r & 1), and tokens past the end.
+      const int e = qh >= G ? 1 : 0;
+#pragma unroll
+      for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((r & 1) != e || ((w * C::kTW + 16 * g + 4 * qg + r) >> 1) >= nvalid)
+            s[g][r] = -INFINITY;
+    } else if (nvalid < TILE) {
 #pragma unroll
       for (int g = 0; g < C::kNG; ++g)
 #pragma unroll
@@ -356,7 +377,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   // waves (the epilogue's fixed order), the partition's (m, l, acc) are stored
   // (kernels.py:77-80), and the running state restarts for the partition
   // before it.  Copies and loads of the next tiles stay in flight.
-  const int tpp = T / TILE;
+  const int tpp = T / TTOK;
   auto flush = [&](char* slot, int ti) __attribute__((always_inline)) {
     if (ti % tpp) return;
     const int part = ti / tpp;
@@ -1465,6 +1486,25 @@ void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionAr
 #undef PD_LAUNCH_GP
 }
 
+// The base and fixed-split protocols at D = 64 with kv heads in pairs
+// (matched_partition_kernel's kPair): gp is the padded size of the pair's
+// query heads, 2 G <= 16.
+template <int kMode>
+void launch_pair_d64(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
+#define PD_LAUNCH_PAIR(GPV)                                                                    \
+  hipLaunchKernelGGL((matched_partition_kernel<64, GPV, false, kMode, true>), grid,             \
+                     dim3(kThreads), 0, stream, a.table, a.lengths, a.q, a.tsb, a.width,        \
+                     a.order, a.T, a.qsb, a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse,  \
+                     a.counters, a.out, a.maxima, a.Hkv, a.splits, a.scale, a.c)
+  switch (gp) {
+    case 2: PD_LAUNCH_PAIR(2); break;
+    case 4: PD_LAUNCH_PAIR(4); break;
+    case 8: PD_LAUNCH_PAIR(8); break;
+    default: PD_LAUNCH_PAIR(16); break;
+  }
+#undef PD_LAUNCH_PAIR
+}
+
 int padded_group(int g) {
   int gp = 1;
   while (gp < g) gp <<= 1;
@@ -1802,12 +1842,19 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
                   nullptr, static_cast<uint16_t*>(out), maxima, num_heads, num_kv_heads, G, hs,
                   kSplitMode ? parts : 1, T, float(scale), float(scale * 1.4426950408889634)};
   // The fixed-split protocol walks each sequence in one workgroup and writes
-  // every partition of it (grid.x = 1), like the base protocol.
-  const dim3 grid(1, num_kv_heads * hs, batch);
+  // every partition of it (grid.x = 1), like the base protocol.  At D = 64 a
+  // workgroup serves two adjacent kv heads when their query heads fit one
+  // 16-head group: a token's two 128-byte rows are one contiguous read.
+  const bool pair = head_dim == 64 && num_kv_heads % 2 == 0 && G <= 8;
+  const dim3 grid(1, pair ? num_kv_heads / 2 : num_kv_heads * hs, batch);
   a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int gp = padded_group(G < 16 ? G : 16);
   constexpr int kMode = kSplitMode ? kSplit : kBase;
+  if (pair) {
+    launch_pair_d64<kMode>(padded_group(2 * G), grid, st, a);
+    return launch_status(what);
+  }
+  const int gp = padded_group(G < 16 ? G : 16);
   switch (head_dim) {
     case 64: launch_partition_d<64, false, kMode>(gp, grid, st, a); break;
     case 128: launch_partition_d<128, false, kMode>(gp, grid, st, a); break;
