@@ -476,22 +476,22 @@ __device__ __forceinline__ int vswz(int row) {
     return 2 * ((row >> 1) & 3);
 }
 
-// Element offset (tile-relative) of tile row R: token R, or with kv-head
-// pairs token R / 2 of the pair's kv head R % 2 (the two heads' rows of a
-// token are adjacent, RS = Hkv * D elements per token).
-template <int D, bool kPair>
+// Element offset (tile-relative) of tile row R: token R / H of the
+// workgroup's kv head R % H, for H kv heads per workgroup (their rows of a
+// token are adjacent; RS = Hkv * D elements per token).
+template <int D, int H>
 __device__ __forceinline__ int tile_row_elems(int R, int RS) {
-  return kPair ? (R >> 1) * RS + (R & 1) * D : R * RS;
+  return (R / H) * RS + (R % H) * D;
 }
 
 // Source byte offset (tile-relative) of the 16 bytes that DMA copy i of
 // wavefront w places at LDS position 16 * (64 i + lane) of its rows.
-template <int D, int GP, bool kColSplit, bool kPair = false>
+template <int D, int GP, bool kColSplit, int H = 1>
 __device__ __forceinline__ int v_copy_offset(int i, int lane, int w, int RS) {
   using C = Matched<D, GP>;
   const int slot = 64 * i + lane;
   const int row = slot / C::kPieces, pos = slot % C::kPieces;
-  return (tile_row_elems<D, kPair>(w * C::kTW + row, RS) + 8 * (pos ^ vswz<D, kColSplit>(row))) * 2;
+  return (tile_row_elems<D, H>(w * C::kTW + row, RS) + 8 * (pos ^ vswz<D, kColSplit>(row))) * 2;
 }
 
 // Byte offset within a V row of this lane's 8 bytes of a transposed read of

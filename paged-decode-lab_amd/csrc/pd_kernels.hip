@@ -118,7 +118,7 @@ __device__ __forceinline__ void write_empty_partition(int tid, int b, int Hq, in
   }
 }
 
-template <int D, int GP, bool kFused, int kMode, bool kPair = false>
+template <int D, int GP, bool kFused, int kMode, int kHeads = 1>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
                          const uint16_t* __restrict__ q, int tsb, int width, int order, int T,
@@ -129,18 +129,19 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
                          int splits, float scale, float c) {
   static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
   static_assert(D < 256, "D = 256 runs matched_cols_kernel");
-  static_assert(!kPair || kMode != kMatched, "kv-head pairs change the tile of the protocol");
+  static_assert(kHeads == 1 || kMode != kMatched, "kv-head groups change the tile of the protocol");
+  static_assert(kHeads == 1 || kHeads == 2, "1 or 2 kv heads per workgroup");
   using C = Matched<D, GP>;
   constexpr int TILE = C::kTile;
-  // kPair (base and fixed-split protocols): the workgroup serves kv heads
-  // 2 kh and 2 kh + 1 and their 2 G query heads.  Row R of a tile is token
-  // R / 2 of kv head 2 kh + R % 2: the two heads' rows of a token are 4 D
-  // contiguous bytes, so a tile holds TILE / 2 tokens; query head e G + g
-  // (e = 0, 1) scores only the rows of its own kv head (odd or even), and the
-  // other rows get probability 0.  At D = 64 a head's row is one 128-byte
-  // line, Hkv lines apart from the next token's; the pair reads two adjacent
-  // lines per token.
-  constexpr int TTOK = kPair ? TILE / 2 : TILE;  // tokens per tile
+  // kHeads = H = 2 (base and fixed-split protocols at D = 64): the
+  // workgroup serves kv heads 2 kh and 2 kh + 1 and their 2 G query heads.
+  // Row R of a tile is token R / 2 of kv head 2 kh + R % 2: the two heads'
+  // rows of a token are 4 D contiguous bytes, so a tile holds TILE / 2
+  // tokens; query head e G + g (e = 0, 1) scores only the rows of its own kv
+  // head (R % 2 = e), and the other rows get probability 0.  A head's D = 64
+  // row is one 128-byte line, Hkv lines apart from the next token's; the
+  // pair reads two adjacent lines per token.
+  constexpr int TTOK = TILE / kHeads;  // tokens per tile
   __shared__ MatchedShared<D, GP> sm;
   // V rows of the tile being computed and of the one being loaded; two arrays
   // (not one) so that the compiler's wait before reading one slot does not
@@ -155,9 +156,9 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   constexpr bool kWalk = kMode == kSplit;
   const int p = kWalk ? 0 : int(blockIdx.x);
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
-  const int kvh = kPair ? 2 * kh : kh;           // (first) kv head of this workgroup
+  const int kvh = kHeads * kh;                   // (first) kv head of this workgroup
   const int qb = kvh * G + 16 * slice;           // first query head of this workgroup
-  const int Gs = min(16, (kPair ? 2 * G : G) - 16 * slice);  // query heads of this workgroup
+  const int Gs = min(16, kHeads * G - 16 * slice);  // query heads of this workgroup
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = lane & 15, qg = lane >> 4;
@@ -195,11 +196,11 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
   // Tile-relative byte offsets: K pieces of this lane, and the source of each
   // 16-byte LDS piece this lane fills (v_copy_offset); rows past the sequence
   // end read past the buffer, i.e. zeros.
-  const int koff = (tile_row_elems<D, kPair>(w * C::kTW + qh, int(RS)) + 8 * qg) * 2;
-  constexpr int kGroupRows = kPair ? 8 : 16;  // token rows of a 16-row group
+  const int koff = (tile_row_elems<D, kHeads>(w * C::kTW + qh, int(RS)) + 8 * qg) * 2;
+  constexpr int kGroupRows = 16 / kHeads;  // tokens of a 16-row group
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, false, kPair>(i, lane, w, int(RS));
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, false, kHeads>(i, lane, w, int(RS));
   // This lane's transposed-read row within its wavefront's LDS rows: row
   // 4qg + qh/4 of each 16-row group (the row v_read_offset swizzles by).
   const int trb = w * C::kSlot + (4 * qg + (qh >> 2)) * C::kPitch;
@@ -262,14 +263,15 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[g][r] *= scale;
     }
-    if constexpr (kPair) {
-      // Rows of the other kv head (row parity r & 1), and tokens past the end.
-      const int e = qh >= G ? 1 : 0;
+    if constexpr (kHeads > 1) {
+      // Rows of the other kv heads (R % H = r % H), and tokens past the end;
+      // padding query lanes (qh >= H G) take the last head's rows.
+      const int e = min(qh / G, kHeads - 1);
 #pragma unroll
       for (int g = 0; g < C::kNG; ++g)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if ((r & 1) != e || ((w * C::kTW + 16 * g + 4 * qg + r) >> 1) >= nvalid)
+          if (r % kHeads != e || (w * C::kTW + 16 * g + 4 * qg + r) / kHeads >= nvalid)
             s[g][r] = -INFINITY;
     } else if (nvalid < TILE) {
 #pragma unroll
@@ -1486,13 +1488,13 @@ void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionAr
 #undef PD_LAUNCH_GP
 }
 
-// The base and fixed-split protocols at D = 64 with kv heads in pairs
-// (matched_partition_kernel's kPair): gp is the padded size of the pair's
-// query heads, 2 G <= 16.
-template <int kMode>
-void launch_pair_d64(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
+// The base and fixed-split protocols at D = 64 with kHeads kv heads per
+// workgroup (matched_partition_kernel's kHeads): gp is the padded size of
+// their query heads, kHeads G <= 16.
+template <int kMode, int kHeads>
+void launch_heads_d64(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_PAIR(GPV)                                                                    \
-  hipLaunchKernelGGL((matched_partition_kernel<64, GPV, false, kMode, true>), grid,             \
+  hipLaunchKernelGGL((matched_partition_kernel<64, GPV, false, kMode, kHeads>), grid,           \
                      dim3(kThreads), 0, stream, a.table, a.lengths, a.q, a.tsb, a.width,        \
                      a.order, a.T, a.qsb, a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse,  \
                      a.counters, a.out, a.maxima, a.Hkv, a.splits, a.scale, a.c)
@@ -1509,6 +1511,15 @@ int padded_group(int g) {
   int gp = 1;
   while (gp < g) gp <<= 1;
   return gp;
+}
+
+// kv heads per workgroup of the D = 64 base / fixed-split launch: 2 when
+// the kv head count is even and the pair's query heads fit one 16-head
+// group, else 1.  (4 heads per workgroup, 512-byte runs per token, measured
+// slower: 187.6 against 168.7 us with batch 128 and 16 kv heads, and with 8
+// kv heads the grid of 256 workgroups leaves half of each CU's slots empty.)
+int heads_per_workgroup(int num_kv_heads, int G) {
+  return num_kv_heads % 2 == 0 && 2 * G <= 16 ? 2 : 1;
 }
 
 // Validation and dispatch shared by pd_partition (fused = false) and
@@ -1845,13 +1856,13 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   // every partition of it (grid.x = 1), like the base protocol.  At D = 64 a
   // workgroup serves two adjacent kv heads when their query heads fit one
   // 16-head group: a token's two 128-byte rows are one contiguous read.
-  const bool pair = head_dim == 64 && num_kv_heads % 2 == 0 && G <= 8;
-  const dim3 grid(1, pair ? num_kv_heads / 2 : num_kv_heads * hs, batch);
+  const int heads = head_dim != 64 ? 1 : heads_per_workgroup(num_kv_heads, G);
+  const dim3 grid(1, heads == 2 ? num_kv_heads / 2 : num_kv_heads * hs, batch);
   a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   constexpr int kMode = kSplitMode ? kSplit : kBase;
-  if (pair) {
-    launch_pair_d64<kMode>(padded_group(2 * G), grid, st, a);
+  if (heads == 2) {
+    launch_heads_d64<kMode, 2>(padded_group(2 * G), grid, st, a);
     return launch_status(what);
   }
   const int gp = padded_group(G < 16 ? G : 16);

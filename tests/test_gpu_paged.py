@@ -189,7 +189,7 @@ def test_d256_tile_counts_of_the_column_split_kernel(backend):
 
 
 @pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (128, 8, 2), (256, 8, 2), (64, 32, 2),
-                                         (64, 8, 2), (64, 6, 6)])
+                                         (64, 8, 2), (64, 6, 6), (64, 16, 16), (64, 12, 4)])
 @pytest.mark.parametrize("tiles_per_partition", [1, 2, 3, 5])
 def test_fixed_split_walk_partition_sizes(dim, hq, hkv, tiles_per_partition):
     """pd_split_fixed walks each sequence in one workgroup and writes every partition as
@@ -227,14 +227,15 @@ def test_fixed_split_walk_partition_sizes(dim, hq, hkv, tiles_per_partition):
 
 
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
-@pytest.mark.parametrize("hq,hkv", [(2, 2), (16, 16), (8, 4), (6, 2), (16, 2), (12, 4), (10, 2)])
+@pytest.mark.parametrize("hq,hkv", [(2, 2), (16, 16), (8, 4), (6, 2), (16, 2), (12, 4), (10, 2),
+                                    (4, 4), (16, 4), (3, 3)])
 def test_d64_kv_head_pairs(backend, hq, hkv):
-    """At D=64 with an even kv head count and at most 8 query heads per kv head, one
-    workgroup serves two adjacent kv heads and their 2G query heads (tiles of 128 tokens of
-    both heads).  Group sizes 1 to 8 (padded to 2, 4, 8 and 16 query heads), lengths
-    around the half-page tile boundaries and the 512-token partitions, NaN-poisoned
-    tails."""
-    lengths = [0, 1, 2, 127, 128, 129, 255, 256, 257, 383, 511, 512, 513, 1100]
+    """At D=64 one workgroup serves two adjacent kv heads and their 2G query heads when
+    the kv head count is even and 2G <= 16 (tiles of 128 tokens of both heads); odd kv
+    head counts stay one per workgroup.  Group sizes 1 to 8 (padded to 2, 4, 8 and 16
+    query heads), lengths around the 128-token tile boundaries and the partitions,
+    NaN-poisoned tails."""
+    lengths = [0, 1, 2, 63, 64, 65, 127, 128, 129, 255, 256, 257, 383, 511, 512, 513, 1100]
     q, k, v, table, lens = make_case(lengths, hq, hkv, 64, seed=hq * 31 + hkv, capacity=1100)
     poison_tails(k, v, table, lens)
     case = (q, k, v, table, lens)
