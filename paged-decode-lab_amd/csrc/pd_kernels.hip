@@ -1284,23 +1284,61 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 // One wavefront per (b, h) row and 64-column chunk (grid rows x D/64), one
 // output element per lane, so a row's partials are read by D/64 CUs at once.
 // Every wavefront computes the row's weights itself (the same arithmetic, so
-// the same bits in every chunk) and broadcasts them with readlane: no LDS, no
-// barrier.
-// kBatch: splits loaded per straight-line batch; 128 (one memory round trip
-// for any split count) when there are more than 64 splits, else 64.
-template <int D, int kBatch>
+// the same bits in every chunk) and broadcasts them with readlane.
+// Every load is in flight at once: a wavefront can have at most 63 vector
+// loads outstanding, so one 4-byte load per split and lane would wait a
+// second round trip past about 60 splits.  Instead the 16 lanes of 16-lane
+// row r load the 64 columns of split 4 i + r as 16-byte pieces, four splits
+// per instruction (kMax / 4 instructions, zeros past the last split), and a
+// 4 x 4 transpose across the rows (v_permlane32_swap, then
+// v_permlane16_swap) leaves lane 16 r + j with column 4 j + r of splits
+// 4 i .. 4 i + 3.  The row's LSEs are loaded first, so the weights are
+// computed while the partials arrive.  The chain acc = fma(w_p, partial_p,
+// acc) runs over p = 0 .. kMax - 1 in order (matched_splitkv.py:121-126); the
+// terms past the last split are fma(0, 0, acc), which changes nothing but a
+// -0 into +0.  kMax: 64 for up to 64 splits, else 128.
+template <int D, int kMax>
 __global__ void __launch_bounds__(64)
 lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ lse,
                  uint16_t* __restrict__ out, int splits, int lanes) {
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x;
-  const int dd = blockIdx.y * 64 + lane;
-  float w0 = 0.f, w1 = 0.f, acc[1];
-  merge_splits<1, 0, kBatch>(
-      partials + row * splits * D, D, dd, splits,
-      [&] { lse_weights<0>(lse + row * splits, splits, lanes, lane, w0, w1); },
-      [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
-  out[row * D + dd] = uint16_t(bf16_bits(acc[0]));
+  const int c0 = blockIdx.y * 64;
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(partials + row * splits * D, splits * D * 4);
+  float la, lc;
+  lse_load<0>(lse + row * splits, splits * 4, lane, la, lc);
+  __builtin_amdgcn_sched_barrier(0);
+  const int r = lane >> 4, j = lane & 15;
+  float x[kMax / 4][4];
+#pragma unroll
+  for (int i = 0; i < kMax / 4; ++i)
+    buffer_load_f32<4, 0>(rs, ((4 * i + r) * D + c0 + 4 * j) * 4, x[i]);
+  __builtin_amdgcn_sched_barrier(0);
+  float w0 = 0.f, w1 = 0.f;
+  lse_weights_of(la, lc, splits, lanes, lane, w0, w1);
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMax / 4; ++i) {
+    // x[i][e] of row r is column 4 j + e of split 4 i + r; swap the row and
+    // element bits, bit 1 (rows 0-1 <-> 2-3) then bit 0 (even <-> odd rows).
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i][e]),
+                                                      __float_as_uint(x[i][e + 2]), false, false);
+      x[i][e] = __uint_as_float(t[0]);
+      x[i][e + 2] = __uint_as_float(t[1]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[i][e]),
+                                                      __float_as_uint(x[i][e + 1]), false, false);
+      x[i][e] = __uint_as_float(t[0]);
+      x[i][e + 1] = __uint_as_float(t[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = fmaf(wave_weight(w0, w1, 4 * i + k), x[i][k], acc);
+  }
+  out[row * D + c0 + 4 * j + r] = uint16_t(bf16_bits(acc));
 }
 
 // ------------------------------------------------------------ m/l/acc merge
