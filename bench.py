@@ -405,6 +405,8 @@ def profile_launches(torch, which, calls=50):
     long: partition and merge at D256 GQA 4:1, B=1, context 131072 (KV from HBM).
     edge: paged_decode's hip_base and hip_splitk on the edge-coverage batches (B=128,
     a quarter of the lengths 0, the rest U[1, 4096]; D 64 MHA 16/16, D 256 GQA 32/4).
+    decoder: the 24-layer random-init decoder, prompt 512, 16 greedy decode steps as
+    hipGraph replays (the kernel mix of one decode step).
     """
     import numpy as np
     src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device="cuda")
@@ -453,6 +455,16 @@ def profile_launches(torch, which, calls=50):
                 torch.cuda.synchronize()
                 del res
             del q, k, v, table, lens
+    if "decoder" in which:
+        from paged_decode import hybrid
+        model = hybrid.random_init_model(hybrid.decoder_config(), "cuda", 0)
+        runner = hybrid.HybridRunner(model=model, backend="hip_matched", mode="graph",
+                                     max_context=512 + 16)
+        gen = torch.Generator().manual_seed(512)
+        runner.generate([torch.randint(0, 151936, (512,), generator=gen).tolist()],
+                        output_tokens=16)
+        torch.cuda.synchronize()
+        del runner, model
     torch.cuda.empty_cache()
     print(json.dumps({"profiled": which}))
 
@@ -518,7 +530,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the extra measurements")
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU run")
-    ap.add_argument("--profile", default=None, metavar="headline,sweep,long,edge",
+    ap.add_argument("--profile", default=None, metavar="headline,sweep,long,edge,decoder",
                     help="only make eager launches for rocprofv3 (calibration copy + cases)")
     ap.add_argument("--require-idle-gpu", action="store_true",
                     help="refuse to run (before any GPU work) if amd-smi lists other processes")
