@@ -46,12 +46,12 @@ def test_boundaries_gqa_and_padding(backend, dim, hq, hkv):
 
 
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
-@pytest.mark.parametrize("dim", [64, 256])
-def test_graph_replay_changes_lengths_pages_and_kv(backend, dim):
-    case = make_case([255, 1023, 0], 4, 1, dim, seed=19, capacity=2048)
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (256, 4, 1), (64, 8, 2)])
+def test_graph_replay_changes_lengths_pages_and_kv(backend, dim, hq, hkv):
+    case = make_case([255, 1023, 0], hq, hkv, dim, seed=19, capacity=2048)
     g = to_gpu(case)
     q, k, v, table, lens = g
-    spec = DecodeSpec(3, 4, 1, dim, 2048)
+    spec = DecodeSpec(3, hq, hkv, dim, 2048)
     res = allocate_resources(spec, "cuda", backend)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
