@@ -175,8 +175,11 @@ int pd_matched_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_strid
 /* Base decode: FP32 online softmax over the whole context with FP32
  * probabilities, out = acc / denom (0 for an empty row), for every query head.
  * One workgroup per (kv head, sequence) serves the kv head's query heads (16 at
- * a time), so K/V is read once per kv head.  Replaces _base (kernels.py:10-41)
- * as launched by paged_decode (runtime.py:109).  Writes out rows [0, batch). */
+ * a time), so K/V is read once per kv head; at head_dim 64 with an even
+ * num_kv_heads and at most 8 query heads per kv head, one workgroup serves two
+ * adjacent kv heads (a token's two rows are one contiguous read).  Replaces
+ * _base (kernels.py:10-41) as launched by paged_decode (runtime.py:109).
+ * Writes out rows [0, batch). */
 int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h,
             const void* k, const void* v,
             const int32_t* table, int64_t table_stride_b, int32_t table_width,
@@ -185,8 +188,9 @@ int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h,
             int32_t head_dim, double scale, pd_stream_t stream);
 
 /* Fixed-size split-K partition: unnormalized (m, l, acc) per partition of
- * partition_size tokens, m in scaled units, one workgroup per (partition, kv
- * head, sequence) as for pd_base.  Replaces _split (kernels.py:44-80) as
+ * partition_size tokens, m in scaled units.  The workgroups are pd_base's:
+ * each walks its sequence's context and writes every partition's (m, l, acc)
+ * as it passes, empty partitions included.  Replaces _split (kernels.py:44-80) as
  * launched by paged_decode (runtime.py:111-113).  maxima/denoms f32
  * [batch, num_heads, partitions], accums f32 [batch, num_heads, partitions, D];
  * the row stride of all three is `partitions`; partitions * partition_size
