@@ -469,50 +469,185 @@ def profile_launches(torch, which, calls=50):
     print(json.dumps({"profiled": which}))
 
 
+AB_WORKLOADS = ("headline", "partitions", "edge_d64", "edge_d256", "sweep")
+
+
+def ab_variants_paged(torch, q, k, v, table, lens, spec, backend, libraries):
+    """One call per variant of a paged_decode backend (hip_base: pd_base; hip_splitk:
+    pd_split_fixed + pd_ml_merge) through this build ("current") or another one, each
+    with its own workspace, so that the outputs can be compared bit for bit."""
+    from paged_decode import _native
+    from paged_decode.runtime import allocate_resources
+    scale = spec.head_dim ** -0.5
+    calls, outputs = {}, {}
+    for name, library in libraries.items():
+        res = allocate_resources(spec, "cuda", backend)
+        if backend == "hip_base":
+            def call(res=res, library=library):
+                _native.base(q, k, v, table, lens, res.out, spec.num_kv_heads, scale,
+                             library=library)
+        else:
+            def call(res=res, library=library):
+                _native.split_fixed(q, k, v, table, lens, res.maxima, res.denoms, res.accums,
+                                    spec.num_kv_heads, spec.partitions, 1024, scale,
+                                    library=library)
+                _native.ml_merge(res.maxima, res.denoms, res.accums, res.out, spec.max_batch,
+                                 library=library)
+        calls[name], outputs[name] = call, res.out
+    return calls, outputs
+
+
+def ab_variants_matched(torch, q, k, v, table, lens, spec, splits, part, lanes, libraries):
+    """The matched partition + LSE merge with a fixed plan (splits x part tokens) through
+    this build or another one, each with its own workspace."""
+    from paged_decode import _native
+    scale = spec.head_dim ** -0.5
+    calls, outputs = {}, {}
+    for name, library in libraries.items():
+        shape = (spec.max_batch, spec.num_heads, splits)
+        partials = torch.empty(shape + (spec.head_dim,), device="cuda")
+        lse = torch.empty(shape, device="cuda")
+        out = torch.empty((spec.max_batch, spec.num_heads, spec.head_dim), device="cuda",
+                          dtype=torch.bfloat16)
+
+        def call(partials=partials, lse=lse, out=out, library=library):
+            _native.partition(q, k, v, table, lens, partials, lse, spec.num_kv_heads, splits,
+                              part, 16384 // spec.head_dim, scale, library=library)
+            _native.lse_merge(partials, lse, out, lanes, library=library)
+        calls[name], outputs[name] = call, out
+    return calls, outputs
+
+
 def ab_report(torch, args):
-    """Paired A/B report (paged_decode.evidence) of variants of the headline call: each is
-    timed as 32- and 128-call graphs over shuffled rounds; ratios are per round against
-    the first variant."""
+    """Paired A/B report (paged_decode.evidence) of variants of one workload: each is timed
+    as graphs of two unroll counts over shuffled rounds; ratios are per round against the
+    first variant, and the outputs of every variant are compared bit for bit with the
+    first one's.
+
+    Workloads (--ab-workload):
+    * headline: the matched decode, B=--ab-batch, Hq 16 / Hkv 4 / D 256, --ctx tokens,
+      planner plan; variants two_launch, fused, noalloc, partition, merge, or NAME=PATH
+      (the two launches through another build of libpaged_decode.so);
+    * partitions: the same matched decode with --ab-partition-token splits (the
+      reference's 1024 by default);
+    * edge_d64 / edge_d256: the edge-coverage batches (B=128, a quarter of the lengths 0,
+      the rest U[1, 4096]; D 64 MHA 16/16, D 256 GQA 32/4) through --ab-backend
+      (hip_base or hip_splitk);
+    * sweep: the bandwidth-sweep batch (B=64, Hq 32 / Hkv 8 / D 128, lengths U[1, 32768],
+      pages over a 200 GB pool) through --ab-backend.
+    Outside headline the variants are current (this build) or NAME=PATH."""
+    import numpy as np
     from paged_decode import _native, evidence
     from paged_decode.matched_splitkv import matched_decode
-    ctx, batch = args.ctx, args.ab_batch
-    case = matched_case(torch, batch, 16, 4, 256, max(2112, ctx), [ctx] * batch, 20261105)
-    q, k, v, table, lens = case["tensors"]
-    res, plan, scale = case["res"], case["plan"], 256 ** -0.5
-    known = {"two_launch": case["full"], "fused": case["fused"],
-             "partition": case["partition"], "merge": case["merge"],
-             "noalloc": lambda: _native.matched_decode_noalloc(
-                 q, k, v, table, lens, res.out, 4, plan.splits, plan.tokens_per_split,
-                 plan.tile_tokens, scale)}
-    variants = {}
-    for item in args.ab.split(","):
+    from paged_decode.spec import DecodeSpec
+    workload, ctx, batch = args.ab_workload, args.ctx, args.ab_batch
+    items = args.ab.split(",")
+    libraries = {}
+    for item in items:
         if "=" in item:
             name, path = item.split("=", 1)
-            other = _native.load_library(os.path.abspath(path))
-
-            def call(other=other):
-                _native.partition(q, k, v, table, lens, res.partials, res.lse, 4, plan.splits,
-                                  plan.tokens_per_split, plan.tile_tokens, scale, library=other)
-                _native.lse_merge(res.partials, res.lse, res.out, plan.lse_lanes, library=other)
-            variants[name] = call
-        elif item in known:
-            variants[item] = known[item]
+            libraries[name] = _native.load_library(os.path.abspath(path))
+    unrolls, replays = (32, 128), 20
+    if workload == "headline":
+        case = matched_case(torch, batch, 16, 4, 256, max(2112, ctx), [ctx] * batch, 20261105)
+        q, k, v, table, lens = case["tensors"]
+        res, plan, scale = case["res"], case["plan"], 256 ** -0.5
+        known = {"two_launch": case["full"], "fused": case["fused"],
+                 "partition": case["partition"], "merge": case["merge"],
+                 "noalloc": lambda: _native.matched_decode_noalloc(
+                     q, k, v, table, lens, res.out, 4, plan.splits, plan.tokens_per_split,
+                     plan.tile_tokens, scale)}
+        other, outputs = ab_variants_matched(torch, q, k, v, table, lens, case["spec"],
+                                             plan.splits, plan.tokens_per_split,
+                                             plan.lse_lanes, libraries)
+        variants = {}
+        for item in items:
+            name = item.split("=", 1)[0]
+            if name in libraries:
+                variants[name] = other[name]
+            elif item in known:
+                variants[item] = known[item]
+            else:
+                raise SystemExit(f"unknown A/B variant {item!r}; known: {sorted(known)} or "
+                                 "NAME=PATH")
+        # partition / merge alone leave no output of their own to compare
+        outputs = {n: outputs[n] if n in libraries else
+                   (res.out if n in ("two_launch", "fused", "noalloc") else None)
+                   for n in variants}
+        label = (f"matched decode B={batch} Hq=16 Hkv=4 D=256 ctx {ctx}, plan "
+                 f"{plan.splits}x{plan.tokens_per_split}")
+    else:
+        for item in items:
+            if "=" not in item and item != "current":
+                raise SystemExit(f"unknown A/B variant {item!r} for workload {workload}: "
+                                 "current or NAME=PATH")
+        libraries = {item.split("=", 1)[0]: libraries.get(item.split("=", 1)[0])
+                     for item in items}
+        unrolls, replays = (4, 16), 5
+        if workload == "partitions":
+            part = args.ab_partition
+            cap = max(2112, ctx)
+            spec = DecodeSpec(batch, 16, 4, 256, cap)
+            q, k, v, table, lens = make_inputs(torch, batch, 16, 4, 256, cap, [ctx] * batch,
+                                               20261105)
+            splits = -(-spec.table_width * PAGE // part)
+            lanes = min(1 << (splits - 1).bit_length(), 32)
+            variants, outputs = ab_variants_matched(torch, q, k, v, table, lens, spec, splits,
+                                                    part, lanes, libraries)
+            label = (f"matched partition + merge B={batch} Hq=16 Hkv=4 D=256 ctx {ctx}, "
+                     f"{splits} partitions of {part} tokens")
         else:
-            raise SystemExit(f"unknown A/B variant {item!r}; known: {sorted(known)} or NAME=PATH")
+            if workload == "sweep":
+                lengths = np.random.default_rng(64).integers(1, 32769, size=64).tolist()
+                geometry = (64, 32, 8, 128, 32768)
+                pool = int(100e9 // (PAGE * 8 * 128 * 2))
+            else:
+                rng4 = np.random.default_rng(4)
+                lengths = [0 if i % 4 == 0 else int(x)
+                           for i, x in enumerate(rng4.integers(1, 4097, size=128))]
+                geometry = (128, 16, 16, 64, 4096) if workload == "edge_d64" else \
+                    (128, 32, 4, 256, 4096)
+                pool = None
+            b, hq, hkv, dim, cap = geometry
+            q, k, v, table, lens = make_inputs(torch, b, hq, hkv, dim, cap, lengths, 64, pool)
+            spec = DecodeSpec(b, hq, hkv, dim, cap)
+            if args.ab_backend == "matched":
+                from paged_decode.splitkv_plan import make_splitkv_plan
+                plan = make_splitkv_plan(spec, torch.cuda.get_device_properties(0)
+                                         .multi_processor_count)
+                variants, outputs = ab_variants_matched(
+                    torch, q, k, v, table, lens, spec, plan.splits, plan.tokens_per_split,
+                    plan.lse_lanes, libraries)
+            else:
+                variants, outputs = ab_variants_paged(torch, q, k, v, table, lens, spec,
+                                                      args.ab_backend, libraries)
+            label = (f"{args.ab_backend} B={b} Hq={hq} Hkv={hkv} D={dim}, {workload} lengths")
     names = list(variants)
-    rows = evidence.paired_timings(torch, variants, rounds=args.ab_rounds)
-    report = evidence.paired_report(rows, names, names[0], args.ab_rounds)
-    report.update(workload=f"matched decode B={batch} Hq=16 Hkv=4 D=256 ctx {ctx}, plan "
-                           f"{plan.splits}x{plan.tokens_per_split}",
-                  rows=rows, environment=benchmark_protocol_fingerprint(torch))
+    # Each variant once, its output copied right away (variants may share a buffer).
+    identical, first = {}, None
+    for n in names:
+        variants[n]()
+        torch.cuda.synchronize()
+        out = None if outputs[n] is None else outputs[n].clone()
+        if n == names[0]:
+            first = out
+        identical[n] = (None if out is None or first is None else
+                        bool(torch.equal(out.view(torch.int16), first.view(torch.int16))))
+    rows = evidence.paired_timings(torch, variants, rounds=args.ab_rounds, replays=replays,
+                                   unrolls=unrolls)
+    report = evidence.paired_report(rows, names, names[0], args.ab_rounds, unrolls=unrolls)
+    report.update(workload=label, outputs_identical_to_first=identical, rows=rows,
+                  environment=benchmark_protocol_fingerprint(torch))
     if args.ab_out:
         evidence.write_json_exclusive(args.ab_out, report)
+    top = str(max(unrolls))
     for name, x in report["variants"].items():
-        t = x["us_per_call"]["128"]
+        t = x["us_per_call"][top]
         r = x["over_baseline"]
         progress(f"{name}: {t['median']:.3f} us/call (rounds {t['min']:.3f}-{t['max']:.3f}), "
                  f"x{r['median']:.4f} of {names[0]} ({r['min']:.4f}-{r['max']:.4f}), "
-                 f"t32/t128-1 = {x['unroll_relative_delta']:+.4f}")
+                 f"t{min(unrolls)}/t{top}-1 = {x['unroll_relative_delta']:+.4f}, "
+                 f"output identical: {identical[name]}")
     print(json.dumps({k: v for k, v in report.items() if k != "rows"}))
 
 
@@ -535,13 +670,21 @@ def main():
     ap.add_argument("--require-idle-gpu", action="store_true",
                     help="refuse to run (before any GPU work) if amd-smi lists other processes")
     ap.add_argument("--ab", default=None, metavar="V1,V2,...",
-                    help="paired A/B report of variants of the headline call instead of the "
-                         "benchmark: two_launch, fused, noalloc, partition, merge, or NAME=PATH "
-                         "for the two launches through another build of libpaged_decode.so")
+                    help="paired A/B report instead of the benchmark: for the headline "
+                         "workload two_launch, fused, noalloc, partition, merge; for the others "
+                         "current; for all NAME=PATH (the call through another build of "
+                         "libpaged_decode.so)")
     ap.add_argument("--ab-rounds", type=int, default=5)
     ap.add_argument("--ab-batch", type=int, default=1,
                     help="sequences of the A/B workload (each of --ctx tokens)")
     ap.add_argument("--ab-out", default=None, help="also write the report to this new JSON file")
+    ap.add_argument("--ab-workload", default="headline", choices=AB_WORKLOADS,
+                    help="workload of the A/B report (see ab_report)")
+    ap.add_argument("--ab-backend", default="hip_base",
+                    choices=("hip_base", "hip_splitk", "matched"),
+                    help="backend of the edge_d64 / edge_d256 / sweep A/B workloads")
+    ap.add_argument("--ab-partition", type=int, default=1024,
+                    help="partition tokens of the partitions A/B workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "

@@ -167,28 +167,31 @@ def lse_merge(partials, lse, out, lse_lanes, library=None):
                          lse_lanes, stream_handle(partials.device)), L)
 
 
-def base(q, k, v, tables, lengths, out, num_kv_heads, scale):
+def base(q, k, v, tables, lengths, out, num_kv_heads, scale, library=None):
     b, h, d = q.shape
-    check(lib().pd_base(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
-                        tables.data_ptr(), tables.stride(0), tables.shape[1], lengths.data_ptr(),
-                        out.data_ptr(),
-                        b, h, num_kv_heads, d, scale, stream_handle(q.device)))
+    L = library or lib()
+    check(L.pd_base(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                    tables.data_ptr(), tables.stride(0), tables.shape[1], lengths.data_ptr(),
+                    out.data_ptr(),
+                    b, h, num_kv_heads, d, scale, stream_handle(q.device)), L)
 
 
 def split_fixed(q, k, v, tables, lengths, maxima, denoms, accums, num_kv_heads, partitions,
-                partition_size, scale):
+                partition_size, scale, library=None):
     b, h, d = q.shape
-    check(lib().pd_split_fixed(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
-                               tables.data_ptr(), tables.stride(0), tables.shape[1],
-                               lengths.data_ptr(), maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(), b, h,
-                               num_kv_heads, d, partitions, partition_size, scale,
-                               stream_handle(q.device)))
+    L = library or lib()
+    check(L.pd_split_fixed(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                           tables.data_ptr(), tables.stride(0), tables.shape[1],
+                           lengths.data_ptr(), maxima.data_ptr(), denoms.data_ptr(),
+                           accums.data_ptr(), b, h, num_kv_heads, d, partitions, partition_size,
+                           scale, stream_handle(q.device)), L)
 
 
-def ml_merge(maxima, denoms, accums, out, batch):
+def ml_merge(maxima, denoms, accums, out, batch, library=None):
     _, h, parts, d = accums.shape
-    check(lib().pd_ml_merge(maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(),
-                            out.data_ptr(), batch, h, d, parts, stream_handle(out.device)))
+    L = library or lib()
+    check(L.pd_ml_merge(maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(),
+                        out.data_ptr(), batch, h, d, parts, stream_handle(out.device)), L)
 
 
 def store_kv(key, value, k_cache, v_cache, slot_mapping):
