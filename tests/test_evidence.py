@@ -1,5 +1,6 @@
 """Host-side checks of the paired timing report (paged_decode.evidence), CPU only."""
 import json
+import os
 
 import pytest
 
@@ -49,3 +50,16 @@ def test_summarize():
     s = evidence.summarize([3, 1, 2, 10])
     assert (s["count"], s["median"], s["min"], s["max"], s["p95"]) == (4, 2.5, 1.0, 10.0, 10.0)
     assert evidence.summarize([])["median"] is None
+
+
+def test_bench_ab_refuses_unknown_variants_before_any_gpu_work():
+    """bench.py --ab names its workload's variants (current or NAME=PATH outside the
+    headline) and refuses others before it allocates anything on a GPU."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--ab", "bogus",
+                          "--ab-workload", "edge_d64"], capture_output=True, text=True,
+                         timeout=300, cwd=root)
+    assert res.returncode != 0
+    assert "unknown A/B variant 'bogus'" in res.stderr
