@@ -1026,7 +1026,9 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 template <int D, int GP>
 struct FusedMerge {
   static constexpr int kNC = GP * D / 1024 > 1 ? GP * D / 1024 : 1;
-  static constexpr int kBatch = 48 / kNC;
+  // 20 rather than 24 at kNC = 2 (D 256 with 5-8 query heads): 24 spilled
+  // 20 bytes per lane to scratch there, 20 needs 229 VGPRs and none.
+  static constexpr int kBatch = kNC == 2 ? 20 : 48 / kNC;
 };
 
 template <int D, int GP, int kFuse>

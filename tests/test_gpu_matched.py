@@ -138,7 +138,8 @@ def _bits(t):
     ([2064], 16, 4, 256, 2112, 0), ([528], 16, 4, 256, 528, 0),
     ([0, 1, 257, 1000], 8, 2, 128, 1000, 0), ([0, 0, 0], 8, 2, 64, 2051, 0),
     ([2051, 1, 0, 1025], 32, 4, 256, 4096, 1), ([2051, 1, 0, 1025], 32, 2, 128, 4096, 6),
-    ([3000, 17], 12, 4, 64, 4096, 0), ([4096] * 3, 16, 1, 256, 4096, 0)])
+    ([3000, 17], 12, 4, 64, 4096, 0), ([4096] * 3, 16, 1, 256, 4096, 0),
+    ([2064, 700], 16, 2, 256, 2112, 0), ([900, 0], 10, 2, 256, 1024, 0)])
 def test_fused_decode_matches_two_launches(lengths, hq, hkv, dim, cap, splits):
     """The fused launch runs the partition kernel the two launches run for the same plan
     (the single-tile kernel for splits of one tile, the multi-tile kernel otherwise) and
