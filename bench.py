@@ -474,48 +474,51 @@ AB_WORKLOADS = ("headline", "partitions", "edge_d64", "edge_d256", "sweep")
 
 def ab_variants_paged(torch, q, k, v, table, lens, spec, backend, libraries):
     """One call per variant of a paged_decode backend (hip_base: pd_base; hip_splitk:
-    pd_split_fixed + pd_ml_merge) through this build ("current") or another one, each
-    with its own workspace, so that the outputs can be compared bit for bit."""
+    pd_split_fixed + pd_ml_merge) through this build ("current") or another one.  All
+    variants share one workspace and output, so that they differ in the library only
+    (the placement of a workspace alone moves these times by a few percent)."""
     from paged_decode import _native
     from paged_decode.runtime import allocate_resources
     scale = spec.head_dim ** -0.5
-    calls, outputs = {}, {}
+    res = allocate_resources(spec, "cuda", backend)
+    calls = {}
     for name, library in libraries.items():
-        res = allocate_resources(spec, "cuda", backend)
         if backend == "hip_base":
-            def call(res=res, library=library):
+            def call(library=library):
                 _native.base(q, k, v, table, lens, res.out, spec.num_kv_heads, scale,
                              library=library)
         else:
-            def call(res=res, library=library):
+            def call(library=library):
                 _native.split_fixed(q, k, v, table, lens, res.maxima, res.denoms, res.accums,
                                     spec.num_kv_heads, spec.partitions, 1024, scale,
                                     library=library)
                 _native.ml_merge(res.maxima, res.denoms, res.accums, res.out, spec.max_batch,
                                  library=library)
-        calls[name], outputs[name] = call, res.out
-    return calls, outputs
+        calls[name] = call
+    return calls, {name: res.out for name in libraries}
 
 
-def ab_variants_matched(torch, q, k, v, table, lens, spec, splits, part, lanes, libraries):
+def ab_variants_matched(torch, q, k, v, table, lens, spec, splits, part, lanes, libraries,
+                        workspace=None):
     """The matched partition + LSE merge with a fixed plan (splits x part tokens) through
-    this build or another one, each with its own workspace."""
+    this build or another one; all variants share one workspace (partials, lse, out)."""
     from paged_decode import _native
     scale = spec.head_dim ** -0.5
-    calls, outputs = {}, {}
-    for name, library in libraries.items():
+    if workspace is None:
         shape = (spec.max_batch, spec.num_heads, splits)
-        partials = torch.empty(shape + (spec.head_dim,), device="cuda")
-        lse = torch.empty(shape, device="cuda")
-        out = torch.empty((spec.max_batch, spec.num_heads, spec.head_dim), device="cuda",
-                          dtype=torch.bfloat16)
-
-        def call(partials=partials, lse=lse, out=out, library=library):
+        workspace = (torch.empty(shape + (spec.head_dim,), device="cuda"),
+                     torch.empty(shape, device="cuda"),
+                     torch.empty((spec.max_batch, spec.num_heads, spec.head_dim), device="cuda",
+                                 dtype=torch.bfloat16))
+    partials, lse, out = workspace
+    calls = {}
+    for name, library in libraries.items():
+        def call(library=library):
             _native.partition(q, k, v, table, lens, partials, lse, spec.num_kv_heads, splits,
                               part, 16384 // spec.head_dim, scale, library=library)
             _native.lse_merge(partials, lse, out, lanes, library=library)
-        calls[name], outputs[name] = call, out
-    return calls, outputs
+        calls[name] = call
+    return calls, {name: out for name in libraries}
 
 
 def ab_report(torch, args):
@@ -526,8 +529,9 @@ def ab_report(torch, args):
 
     Workloads (--ab-workload):
     * headline: the matched decode, B=--ab-batch, Hq 16 / Hkv 4 / D 256, --ctx tokens,
-      planner plan; variants two_launch, fused, noalloc, partition, merge, or NAME=PATH
-      (the two launches through another build of libpaged_decode.so);
+      planner plan; variants two_launch, fused, noalloc, partition, merge (through
+      matched_decode), current or NAME=PATH (pd_partition + pd_lse_merge through this
+      or another build of libpaged_decode.so);
     * partitions: the same matched decode with --ab-partition-token splits (the
       reference's 1024 by default);
     * edge_d64 / edge_d256: the edge-coverage batches (B=128, a quarter of the lengths 0,
@@ -535,7 +539,10 @@ def ab_report(torch, args):
       (hip_base or hip_splitk);
     * sweep: the bandwidth-sweep batch (B=64, Hq 32 / Hkv 8 / D 128, lengths U[1, 32768],
       pages over a 200 GB pool) through --ab-backend.
-    Outside headline the variants are current (this build) or NAME=PATH."""
+    Outside headline the variants are current (this build) or NAME=PATH.  Every variant
+    of a report uses the same workspace and output buffers (the placement of a workspace
+    alone moves these times by a few percent), and each variant's output is copied right
+    after its own call for the bit-for-bit comparison."""
     import numpy as np
     from paged_decode import _native, evidence
     from paged_decode.matched_splitkv import matched_decode
@@ -557,13 +564,17 @@ def ab_report(torch, args):
                  "noalloc": lambda: _native.matched_decode_noalloc(
                      q, k, v, table, lens, res.out, 4, plan.splits, plan.tokens_per_split,
                      plan.tile_tokens, scale)}
+        # "current" and NAME=PATH variants run the same calls on the same workspace as
+        # two_launch, so that they differ in the library only.
+        others = dict(libraries, current=None) if "current" in items else libraries
         other, outputs = ab_variants_matched(torch, q, k, v, table, lens, case["spec"],
                                              plan.splits, plan.tokens_per_split,
-                                             plan.lse_lanes, libraries)
+                                             plan.lse_lanes, others,
+                                             workspace=(res.partials, res.lse, res.out))
         variants = {}
         for item in items:
             name = item.split("=", 1)[0]
-            if name in libraries:
+            if name in others:
                 variants[name] = other[name]
             elif item in known:
                 variants[item] = known[item]
@@ -571,7 +582,7 @@ def ab_report(torch, args):
                 raise SystemExit(f"unknown A/B variant {item!r}; known: {sorted(known)} or "
                                  "NAME=PATH")
         # partition / merge alone leave no output of their own to compare
-        outputs = {n: outputs[n] if n in libraries else
+        outputs = {n: outputs[n] if n in others else
                    (res.out if n in ("two_launch", "fused", "noalloc") else None)
                    for n in variants}
         label = (f"matched decode B={batch} Hq=16 Hkv=4 D=256 ctx {ctx}, plan "

@@ -1296,9 +1296,12 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 // v_permlane16_swap) leaves lane 16 r + j with column 4 j + r of splits
 // 4 i .. 4 i + 3.  The row's LSEs are loaded first, so the weights are
 // computed while the partials arrive.  The chain acc = fma(w_p, partial_p,
-// acc) runs over p = 0 .. kMax - 1 in order (matched_splitkv.py:121-126); the
-// terms past the last split are fma(0, 0, acc), which changes nothing but a
-// -0 into +0.  kMax: 64 for up to 64 splits, else 128.
+// acc) runs over p = 0 .. kMax - 1 in order (matched_splitkv.py:121-126), kMax
+// the split count rounded up to a multiple of 16; the terms past the last
+// split are fma(0, 0, acc), which changes nothing but a -0 into +0.  The
+// result is the same as a chain over 64 terms (128 past 64 splits) would give,
+// the first form of this kernel: such a chain ends with zero terms unless the
+// split count is 64 or 128, so a final acc + 0 stands in for them.
 template <int D, int kMax>
 __global__ void __launch_bounds__(64)
 lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ lse,
@@ -1340,6 +1343,7 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc = fmaf(wave_weight(w0, w1, 4 * i + k), x[i][k], acc);
   }
+  if (splits % 64 != 0) acc = acc + 0.f;
   out[row * D + c0 + 4 * j + r] = uint16_t(bf16_bits(acc));
 }
 
@@ -1700,19 +1704,24 @@ int merge_entry(const char* what, const float* partials, const float* lse, void*
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto* o = static_cast<uint16_t*>(out);
   const dim3 grid(unsigned(rows), head_dim / 64);
-#define PD_LAUNCH_MERGE(DV)                                                                    \
-  if (splits > 64)                                                                             \
-    hipLaunchKernelGGL((lse_merge_kernel<DV, 128>), grid, dim3(64), 0, st, partials, lse, o,   \
+#define PD_LAUNCH_MERGE_K(DV, KM)                                                              \
+  case KM / 16:                                                                                \
+    hipLaunchKernelGGL((lse_merge_kernel<DV, KM>), grid, dim3(64), 0, st, partials, lse, o,    \
                        splits, lse_lanes);                                                     \
-  else                                                                                         \
-    hipLaunchKernelGGL((lse_merge_kernel<DV, 64>), grid, dim3(64), 0, st, partials, lse, o,    \
-                       splits, lse_lanes)
+    break
+#define PD_LAUNCH_MERGE(DV)                                                                    \
+  switch ((splits + 15) / 16) {                                                                \
+    PD_LAUNCH_MERGE_K(DV, 16); PD_LAUNCH_MERGE_K(DV, 32); PD_LAUNCH_MERGE_K(DV, 48);           \
+    PD_LAUNCH_MERGE_K(DV, 64); PD_LAUNCH_MERGE_K(DV, 80); PD_LAUNCH_MERGE_K(DV, 96);           \
+    PD_LAUNCH_MERGE_K(DV, 112); default: PD_LAUNCH_MERGE_K(DV, 128);                           \
+  }
   switch (head_dim) {
     case 64: PD_LAUNCH_MERGE(64); break;
     case 128: PD_LAUNCH_MERGE(128); break;
     default: PD_LAUNCH_MERGE(256); break;
   }
 #undef PD_LAUNCH_MERGE
+#undef PD_LAUNCH_MERGE_K
   return launch_status(what);
 }
 
