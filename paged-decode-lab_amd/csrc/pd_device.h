@@ -514,45 +514,57 @@ struct KTile {
 // bytes, half lines whose consecutive lanes address different rows, and one
 // CU streams such loads at about half the rate of loads whose eight
 // consecutive lanes cover one line (38 vs 72 GB/s per CU, measured on
-// MI355X).  So load (h, sh) of a 16-row group gives lane S row 8sh + S/8,
-// 16-byte chunk S%8 of line h (kline_offset), and lines_to_mfma turns the
-// pair sh = 0, 1 into the operand registers of chunks 8h + g and 8h + 4 + g
-// of row r at lane 16g + r, the layout QK's MFMA and the query rows use:
-//   u = load 0 on lanes S%8 < 4, load 1 from lane S - 4 on lanes S%8 >= 4;
-//   v = load 0 from lane S + 4 on lanes S%8 < 4, load 1 on lanes S%8 >= 4
-// (bank-masked DPP moves within 16-lane rows: banks 1 and 3 are the lanes
-// S%8 >= 4), then one ds_bpermute per dword fetches lane 16g + r's value from
-// lane 8r + g (r < 8) or 8(r - 8) + g + 4 (r >= 8) of u and of v.
+// MI355X).  So load (h, sh) of a 16-row group gives lane S = 8k + p row
+// 8sh + k, 16-byte chunk c(S) of line h, with c = p for S < 32 and the
+// chunks rotated by two in the upper half, c = (p - 2) mod 8 for S >= 32
+// (kline_offset; each 8 consecutive lanes still cover one line).  The bank-
+// masked DPP moves within 16-lane rows (banks 1 and 3 are the lanes p >= 4)
+// pair chunks four apart:
+//   u = load 0 on lanes p < 4, load 1 from lane S - 4 on lanes p >= 4;
+//   v = load 0 from lane S + 4 on lanes p < 4, load 1 on lanes p >= 4,
+// and in the upper half, where the rotation puts the higher chunk of a pair
+// first on lanes with p & 2 = 0, u and v are exchanged there.  Lane S then
+// holds chunks c' and c' + 4 of one row, c' < 4; one ds_bpermute per dword
+// fetches lane 16g + r's chunks g and g + 4 of row r from lane
+// 8 (r mod 8) + 4 [r >= 8] + (r mod 8 < 4 ? g : (g + 2) mod 4) (kline_source).
+// The rotation makes the 32 source lanes of each half-wavefront distinct
+// modulo 32: without it rows k and k + 4 sat on lanes 32 apart and every
+// ds_bpermute read had 2-way bank conflicts.
 // The single-tile kernel loads its one tile this way (all of it in flight at
 // once, so the load rate is what counts).  The multi-tile loop keeps loads in
 // the operand layout: there the rearrangement lengthens every tile's chain
 // and one streaming workgroup slowed from 57 to 41 GB/s.
 __device__ __forceinline__ int kline_offset(int lane, int RS) {
-  return ((lane >> 3) * RS + 8 * (lane & 7)) * 2;
+  const int p = lane & 7;
+  const int chunk = lane >= 32 ? ((p - 2) & 7) : p;
+  return ((lane >> 3) * RS + 8 * chunk) * 2;
 }
 __device__ __forceinline__ int kline_source(int lane) {
-  const int r = lane & 15, g = lane >> 4;
-  return 4 * (r < 8 ? 8 * r + g : 8 * (r - 8) + g + 4);
+  const int r = lane & 15, g = lane >> 4, k = r & 7;
+  return 4 * (8 * k + (r >= 8 ? 4 : 0) + (k >= 4 ? ((g + 2) & 3) : g));
 }
-__device__ __forceinline__ void lines_to_mfma(u32x4_t& a, u32x4_t& b, int src) {
+__device__ __forceinline__ void lines_to_mfma(u32x4_t& a, u32x4_t& b, int src, bool exchange) {
   u32x4_t ra, rb;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int u = __builtin_amdgcn_update_dpp(int(a[e]), int(b[e]), 0x114, 0xf, 0xa, false);
     const int v = __builtin_amdgcn_update_dpp(int(b[e]), int(a[e]), 0x104, 0xf, 0x5, false);
-    ra[e] = unsigned(__builtin_amdgcn_ds_bpermute(src, u));
-    rb[e] = unsigned(__builtin_amdgcn_ds_bpermute(src, v));
+    ra[e] = unsigned(__builtin_amdgcn_ds_bpermute(src, exchange ? v : u));
+    rb[e] = unsigned(__builtin_amdgcn_ds_bpermute(src, exchange ? u : v));
   }
   a = ra;
   b = rb;
 }
 
 template <int D, int GP>
-__device__ __forceinline__ void ktile_to_mfma(KTile<D, GP>& R, int src) {
+__device__ __forceinline__ void ktile_to_mfma(KTile<D, GP>& R, int lane) {
+  const int src = kline_source(lane);
+  const bool exchange = lane >= 32 && !(lane & 2);
 #pragma unroll
   for (int g = 0; g < Matched<D, GP>::kNG; ++g)
 #pragma unroll
-    for (int h = 0; h < Matched<D, GP>::kCH / 2; ++h) lines_to_mfma(R.k[g][2 * h], R.k[g][2 * h + 1], src);
+    for (int h = 0; h < Matched<D, GP>::kCH / 2; ++h)
+      lines_to_mfma(R.k[g][2 * h], R.k[g][2 * h + 1], src, exchange);
 }
 
 typedef short short4_t __attribute__((ext_vector_type(4)));

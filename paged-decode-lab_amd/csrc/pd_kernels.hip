@@ -1157,7 +1157,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   // Every K and V load of the tile is issued before the K rearrangement, which
   // waits for K.
   __builtin_amdgcn_sched_barrier(0);
-  ktile_to_mfma(R, kline_source(lane));
+  ktile_to_mfma(R, lane);
 
   // ---- scores of this wavefront's tokens, tile maximum per head
   const int nvalid = end - start;

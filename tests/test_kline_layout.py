@@ -1,13 +1,15 @@
 """Lane arithmetic of the K whole-line loads and the V-row LDS swizzle, on the CPU.
 
 pd_device.h loads each 16-row group of K as whole 128-byte lines (kline_offset:
-lane S gets row 8sh + S/8, 16-byte chunk S%8 of line h), then lines_to_mfma
-turns each pair of loads into the MFMA A-operand registers with two bank-masked
-DPP moves (row_shr:4 on banks 1 and 3, row_shl:4 on banks 0 and 2 of every
-16-lane row) and one ds_bpermute per dword from lane kline_source(L).  This test
-runs the same index arithmetic on NumPy lanes and checks the result against the
-operand layout the QK MFMA reads (lane 16g + r: row r, chunk 4ch + g), for every
-head dim.  On the GPU the kernel's outputs are bit-identical to loads made
+lane S gets row 8sh + S/8, 16-byte chunk S%8 of line h, rotated by two in the
+upper half-wavefront), then lines_to_mfma turns each pair of loads into the
+MFMA A-operand registers with two bank-masked DPP moves (row_shr:4 on banks 1
+and 3, row_shl:4 on banks 0 and 2 of every 16-lane row), an exchange of the
+pair on upper lanes with S & 2 = 0, and one ds_bpermute per dword from lane
+kline_source(L).  This test runs the same index arithmetic on NumPy lanes and
+checks the result against the operand layout the QK MFMA reads (lane 16g + r:
+row r, chunk 4ch + g), for every head dim, and that each half-wavefront's 32
+ds_bpermute sources are distinct modulo 32 (no bank conflicts).  On the GPU the kernel's outputs are bit-identical to loads made
 directly in the operand layout (tests/test_gpu_matched.py and the paged tests).
 The V-row swizzle test at the end checks the LDS copy/read round trip and the
 bank spread of the transposed reads.
@@ -33,9 +35,18 @@ def dpp_row_shift(old, src, shift, bank_mask):
     return out
 
 
+def kline_chunk(lane):
+    p = lane & 7
+    return (p - 2) & 7 if lane >= 32 else p
+
+
 def kline_source(lane):
     r, g = lane & 15, lane >> 4
-    return 4 * (8 * r + g if r < 8 else 8 * (r - 8) + g + 4)
+    k = r & 7
+    return 4 * (8 * k + (4 if r >= 8 else 0) + (((g + 2) & 3) if k >= 4 else g))
+
+
+EXCHANGE = np.array([lane >= 32 and not lane & 2 for lane in LANES])
 
 
 def bpermute(src, byte_index):
@@ -51,16 +62,38 @@ def test_whole_line_loads_rearrange_into_the_operand_layout(dim):
     regs = {}
     for h in range(lines):
         for sh in range(2):                # kline_offset + 128 h, rows + 8 sh
-            regs[(h, sh)] = np.array([label(8 * sh + s // 8, 8 * h + s % 8) for s in LANES])
+            regs[(h, sh)] = np.array([label(8 * sh + s // 8, 8 * h + kline_chunk(int(s)))
+                                      for s in LANES])
     idx = np.array([kline_source(int(lane)) for lane in LANES])
     for h in range(lines):
         a, b = regs[(h, 0)], regs[(h, 1)]
         u = dpp_row_shift(a, b, 4, 0xA)
         v = dpp_row_shift(b, a, -4, 0x5)
+        u, v = np.where(EXCHANGE, v, u), np.where(EXCHANGE, u, v)
         got = {2 * h: bpermute(u, idx), 2 * h + 1: bpermute(v, idx)}
         for ch, reg in got.items():
             want = np.array([label(lane & 15, 4 * ch + (lane >> 4)) for lane in LANES])
             np.testing.assert_array_equal(reg, want)
+
+
+def test_bpermute_sources_are_distinct_modulo_32_in_each_half():
+    """ds_bpermute reads its source lanes through 32 banks; the rotation of the upper
+    half's chunks gives each half-wavefront 32 sources in distinct banks (the
+    unrotated layout put rows k and k + 4 on lanes 32 apart: 16 banks, 2-way)."""
+    src = [kline_source(int(lane)) // 4 for lane in LANES]
+    for half in (range(0, 32), range(32, 64)):
+        assert len({src[lane] % 32 for lane in half}) == 32
+    unrotated = [8 * (lane & 15) + (lane >> 4) if (lane & 15) < 8 else
+                 8 * ((lane & 15) - 8) + (lane >> 4) + 4 for lane in range(64)]
+    assert len({unrotated[lane] % 32 for lane in range(32)}) == 16
+
+
+def test_whole_line_loads_still_cover_one_line_per_eight_lanes():
+    row_bytes = 512
+    addr = [(lane // 8) * row_bytes + 16 * kline_chunk(lane) for lane in range(64)]
+    for start in range(0, 64, 8):
+        assert sorted(a % 128 for a in addr[start:start + 8]) == list(range(0, 128, 16))
+        assert len({a // 128 for a in addr[start:start + 8]}) == 1
 
 
 def test_operand_layout_loads_touch_half_lines_and_whole_line_loads_whole_ones():
