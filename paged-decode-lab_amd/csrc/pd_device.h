@@ -617,6 +617,22 @@ __device__ __forceinline__ short4_t lds_read_tr_at(uint32_t base) {
   return r;
 }
 
+// 16 bytes at an LDS byte address (ds_read_b128), issued from inline asm as
+// lds_read_tr_at is; the results pass through lds_wait before use.
+__device__ __forceinline__ u32x4_t lds_read16_at(uint32_t addr) {
+  u32x4_t r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+// Waits for every LDS read of this wavefront and makes the uses of x follow.
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4_t (&x)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(x[i]));
+}
+
 // s_waitcnt vmcnt(N): at most N vector-memory loads of this wavefront remain
 // outstanding (they complete in issue order).
 template <int N>

@@ -583,6 +583,62 @@ struct TileP {
   static constexpr int kKS = kTile / 32;     // 32-token k-steps of PV
 };
 
+// P V of one 64-token tile at D = 256 for wavefront w's output columns
+// [64w, 64w + 64), accumulated into acc (O[head 4(L/16) + r][64w + 16j + L%16]
+// in lane L, element r of acc[j]): k-step ks covers tokens 32ks .. 32ks + 31;
+// lane L supplies k = 8(L/16) + e <-> token 32ks + 8(L/16) + e for both
+// operands (as in matched_tile_kernel).  The probabilities are in `ps`, one
+// 16-row LDS tile per bf16 term; the V rows in `slot`, each wavefront's 16
+// rows in a kSlot part of their own, pieces permuted by vswz.
+template <int GP, int kTerms>
+__device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<256>::kNBW],
+                                             const char (*ps)[16 * TileP<256>::kPitch],
+                                             const char* slot, int lane, int w) {
+  using C = Matched<256, GP>;
+  using P = TileP<256>;
+  const int qh = lane & 15, qg = lane >> 4;
+  auto pv_step = [&](auto KS) __attribute__((always_inline)) {
+    constexpr int ks = decltype(KS)::value;
+    bf16x8_t a[kTerms];
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t) {
+      const char* prow = ps[t] + qh * P::kPitch + (32 * ks + 8 * qg) * 2;
+      const u32x2_t a0 = *reinterpret_cast<const u32x2_t*>(prow);
+      const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(prow + 8);
+      a[t] = __builtin_bit_cast(bf16x8_t, u32x4_t{a0[0], a0[1], a1[0], a1[1]});
+    }
+    // V rows 32ks + 8qg + (qh >> 2) (lo) and + 4 (hi): row t of the tile
+    // is row t % 16 of wavefront t / 16's slot part; columns 64w + 16j.
+    // The transposed reads are issued from inline asm (lds_read_tr_at): the
+    // compiler then adds no vmcnt wait of its own for the LDS copies it
+    // cannot tell apart from this slot's (the caller's wait covers them), and
+    // lds_settle makes the results wait for the reads.
+    const uint32_t vb = lds_address(slot) + (qg >> 1) * C::kSlot +
+                        (8 * (qg & 1) + (qh >> 2)) * C::kPitch;
+    constexpr int kOff = ks * 2 * C::kSlot;
+    short4_t lo[P::kNBW], hi[P::kNBW];
+#pragma unroll
+    for (int j = 0; j < P::kNBW; ++j) {
+      const uint32_t vj =
+          vb + v_read_offset<256, true>(w * P::kCols + 16 * j, lane, 8 * (qg & 1) + (qh >> 2));
+      lo[j] = lds_read_tr_at<kOff>(vj);
+      hi[j] = lds_read_tr_at<kOff + 4 * C::kPitch>(vj);
+    }
+    lds_settle(lo, hi);
+#pragma unroll
+    for (int j = 0; j < P::kNBW; ++j) {
+      const bf16x8_t bv = __builtin_bit_cast(
+          bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo[j])[0], __builtin_bit_cast(u32x2_t, lo[j])[1],
+                            __builtin_bit_cast(u32x2_t, hi[j])[0], __builtin_bit_cast(u32x2_t, hi[j])[1]});
+#pragma unroll
+      for (int t = 0; t < kTerms; ++t)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], bv, acc[j], 0, 0, 0);
+    }
+  };
+  pv_step(std::integral_constant<int, 0>{});
+  pv_step(std::integral_constant<int, 1>{});
+}
+
 // ------------------------------------------- D = 256: P V split by columns
 // The partition for D = 256, the same three protocols as
 // matched_partition_kernel and the same scores, maxima, probabilities and
@@ -783,49 +839,7 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     else if (ti == 1) wait_vmcnt<kKLoads + kVLoads>();
     else wait_vmcnt<0>();
     lds_barrier();
-    // ---- P V over the whole tile, columns 64w .. 64w + 63: k-step ks covers
-    // tokens 32ks .. 32ks + 31; lane L supplies k = 8(L/16) + e <-> token
-    // 32ks + 8(L/16) + e for both operands (as in matched_tile_kernel).
-    auto pv_step = [&](auto KS) __attribute__((always_inline)) {
-      constexpr int ks = decltype(KS)::value;
-      bf16x8_t a[kTerms];
-#pragma unroll
-      for (int t = 0; t < kTerms; ++t) {
-        const char* prow = ps[t] + qh * P::kPitch + (32 * ks + 8 * qg) * 2;
-        const u32x2_t a0 = *reinterpret_cast<const u32x2_t*>(prow);
-        const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(prow + 8);
-        a[t] = __builtin_bit_cast(bf16x8_t, u32x4_t{a0[0], a0[1], a1[0], a1[1]});
-      }
-      // V rows 32ks + 8qg + (qh >> 2) (lo) and + 4 (hi): row t of the tile
-      // is row t % 16 of wavefront t / 16's slot part; columns 64w + 16j.
-      // The transposed reads are issued from inline asm (lds_read_tr_at): the
-      // compiler then adds no vmcnt wait of its own for the LDS copies it
-      // cannot tell apart from this slot's (the wait above covers them), and
-      // lds_settle makes the results wait for the reads.
-      const uint32_t vb = lds_address(slot) + (qg >> 1) * C::kSlot +
-                          (8 * (qg & 1) + (qh >> 2)) * C::kPitch;
-      constexpr int kOff = ks * 2 * C::kSlot;
-      short4_t lo[P::kNBW], hi[P::kNBW];
-#pragma unroll
-      for (int j = 0; j < P::kNBW; ++j) {
-        const uint32_t vj =
-            vb + v_read_offset<D, true>(w * P::kCols + 16 * j, lane, 8 * (qg & 1) + (qh >> 2));
-        lo[j] = lds_read_tr_at<kOff>(vj);
-        hi[j] = lds_read_tr_at<kOff + 4 * C::kPitch>(vj);
-      }
-      lds_settle(lo, hi);
-#pragma unroll
-      for (int j = 0; j < P::kNBW; ++j) {
-        const bf16x8_t bv = __builtin_bit_cast(
-            bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo[j])[0], __builtin_bit_cast(u32x2_t, lo[j])[1],
-                              __builtin_bit_cast(u32x2_t, hi[j])[0], __builtin_bit_cast(u32x2_t, hi[j])[1]});
-#pragma unroll
-        for (int t = 0; t < kTerms; ++t)
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], bv, acc[j], 0, 0, 0);
-      }
-    };
-    pv_step(std::integral_constant<int, 0>{});
-    pv_step(std::integral_constant<int, 1>{});
+    pv_tile_cols<GP, kTerms>(acc, ps, slot, lane, w);
   };
 
   // kWalk: after tile ti, the first tile of partition ti / tpp, that
@@ -992,6 +1006,234 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       for (int e = 0; e < kV; ++e) dst[e] = uint16_t(bf16_bits(mrg[e]));
     }
     if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ------------------------------ D = 256, one workgroup per CU: loader waves
+// The matched protocol at D = 256 for grids that give every workgroup a CU of
+// its own (a few long partitions: 1024-token partitions of one sequence, say).
+// The arithmetic is matched_cols_kernel's, operation for operation, so the
+// partials and LSEs are bit-identical to it; what changes is who loads.  Four
+// wavefronts compute, as matched_cols_kernel's four do, and four more only
+// copy K and V rows into LDS (buffer_load ... lds).  With one workgroup on a
+// CU, each compute wavefront is alone on its SIMD, and a wavefront that
+// issues loads stands still while the CU's load path takes them (about 64
+// bytes per clock, 64 KiB per tile); here the loader wavefronts stand still
+// instead, and the compute wavefronts issue no global load after the query.
+//
+// LDS: two K and two V stages of 32 KiB; tile t uses stage t & 1.  K row r of
+// a stage holds its 16-byte piece p at position p ^ (r & 15): the 16 rows of a
+// compute wavefront's ds_read_b128 (one piece each) then fall on 16 distinct
+// 16-byte bank groups, and each loader copy (1 KiB, two rows, every eight
+// consecutive lanes one 128-byte line) writes one contiguous KiB.  V rows are
+// in matched_cols_kernel's layout.
+//
+// Schedule, tile t (last to first), around the compute wavefronts' barriers:
+//   B1(t)  after QK(t) and the tile maxima.  V stage (t + 1) & 1 is free (P V
+//          of tile t + 1 is done): the loaders issue V(t - 1) into it, then
+//          wait for V(t) and K(t - 1) and go on to B2(t).
+//   B2(t)  before P V of tile t, which needs V(t); QK(t - 1) follows P V with
+//          no barrier between them, so K(t - 1) is in LDS too.  K stage t & 1
+//          is free since B1(t): the loaders issue K(t - 2) into it.
+// Issuing 16 KiB takes a loader about as long as the probabilities take the
+// compute wavefronts (the CU's load path moves about 64 bytes per clock), so
+// each barrier interval holds the issue of one tensor's copies: V between B1
+// and B2, K between B2 and the next B1, alongside P V and QK.
+// A first barrier B0 covers K(count - 1), issued with V(count - 1) and
+// K(count - 2) before it.  Both halves pass the same barriers: B0, B1 and B2
+// of every tile, and the one before the epilogue.
+template <int GP>
+__global__ void __launch_bounds__(2 * kThreads, 1)
+matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
+                      const uint16_t* __restrict__ q, int tsb, int width, int T, int qsb,
+                      int qsh, int G, int Hq, const uint16_t* __restrict__ k,
+                      const uint16_t* __restrict__ v, float* __restrict__ partials,
+                      float* __restrict__ lse_out, int Hkv, int splits, float scale, float c) {
+  constexpr int D = 256;
+  using C = Matched<D, GP>;
+  using P = TileP<D>;
+  constexpr int TILE = C::kTile;
+  constexpr int kStage = TILE * D * 2;  // bytes of one K or V stage
+  constexpr int kCopies = C::kDma;      // 1 KiB copies per loader, tensor and tile
+  static_assert(C::kNG == 1 && C::kTW == 16 && 4 * C::kSlot == kStage && 4 * 1024 * kCopies == kStage,
+                "D = 256 geometry");
+  __shared__ MatchedShared<D, GP> sm;
+  __shared__ __attribute__((aligned(16))) char ks[2][kStage];
+  __shared__ __attribute__((aligned(16))) char vs[2][kStage];
+  __shared__ __attribute__((aligned(16))) char ps[1][16 * P::kPitch];
+
+  const int p = int(blockIdx.x), kh = int(blockIdx.y), b = int(blockIdx.z);
+  const int qb = kh * G;  // G <= 16: one slice holds the group
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = wv & 3;  // compute wavefront w, or loader w for wv >= 4
+  const int qh = lane & 15, qg = lane >> 4;
+  const int start = p * T;
+  const int64_t RS = int64_t(Hkv) * D;
+
+  if (wv >= 4) {
+    PageWindow<2> pw;
+    pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
+    const int end = min(start + T, lengths[b]);
+    const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+    if (count == 0) return;
+    // Copy i of loader w fills rows 2(8w + i) and 2(8w + i) + 1 of K, pieces
+    // in position order; V as matched_cols_kernel's wavefront w copies it.
+    int koff[kCopies], voff[kCopies];
+#pragma unroll
+    for (int i = 0; i < kCopies; ++i) {
+      const int row = 2 * (kCopies * w + i) + (lane >> 5);
+      koff[i] = (row * int(RS) + 8 * ((lane & 31) ^ (row & 15))) * 2;
+      voff[i] = v_copy_offset<D, GP, true>(i, lane, w, int(RS));
+    }
+    pw.settle();
+    auto issue = [&](int ti, bool is_k) __attribute__((always_inline)) {
+      const int t0 = start + ti * TILE;
+      const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
+      char* dst = (is_k ? ks[ti & 1] : vs[ti & 1]) + w * kCopies * 1024;
+#pragma unroll
+      for (int i = 0; i < kCopies; ++i)
+        lds_copy16(is_k ? buf.k : buf.v, dst + 1024 * i, is_k ? koff[i] : voff[i]);
+    };
+    issue(count - 1, true);
+    issue(count - 1, false);
+    if (count >= 2) {
+      issue(count - 2, true);
+      wait_vmcnt<2 * kCopies>();
+    } else {
+      wait_vmcnt<kCopies>();
+    }
+    lds_barrier();  // B0
+    for (int ti = count - 1; ti >= 0; --ti) {
+      lds_barrier();  // B1(ti)
+      if (ti >= 1) {
+        issue(ti - 1, false);
+        wait_vmcnt<kCopies>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      lds_barrier();  // B2(ti)
+      if (ti >= 2) issue(ti - 2, true);
+    }
+    lds_barrier();  // epilogue
+    return;
+  }
+
+  const int end = min(start + T, lengths[b]);
+  const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+  if (count == 0) {
+    write_empty_partition<D, kMatched>(tid, b, Hq, qb, G, splits, p, partials, lse_out, nullptr,
+                                       nullptr);
+    return;
+  }
+  bf16x8_t qf[C::kCH];
+  {
+    const bool live = qh < G;
+    const uint16_t* qrow = q + int64_t(b) * qsb + int64_t(qb + (live ? qh : 0)) * qsh + 8 * qg;
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch)
+      qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
+  }
+  // Lane (qh, qg) reads piece qg + 4ch of K row 16w + qh for k-chunk ch; a
+  // tile's reads are issued once its rows are in LDS (after P V of the tile
+  // before it) and waited for before its QK products.
+  uint32_t kaddr[C::kCH];
+#pragma unroll
+  for (int ch = 0; ch < C::kCH; ++ch)
+    kaddr[ch] = lds_address(ks[0]) + (16 * w + qh) * (2 * D) + (((qg + 4 * ch) ^ qh) * 16);
+  u32x4_t kr[C::kCH];
+  auto read_k = [&](int ti) __attribute__((always_inline)) {
+    const uint32_t stage = (ti & 1) * kStage;
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch) kr[ch] = lds_read16_at(kaddr[ch] + stage);
+  };
+
+  floatx4_t acc[P::kNBW];  // O[head 4*qg + r][64w + 16j + qh]
+#pragma unroll
+  for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  float m4[4];             // running max of heads 4*qg + r
+#pragma unroll
+  for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
+  float m_own = -INFINITY;  // running max of head qh
+  float l_own = 0.f;        // this lane's share of head qh's denominator
+
+  lds_barrier();  // B0
+  read_k(count - 1);
+  for (int ti = count - 1; ti >= 0; --ti) {
+    const int nvalid = end - (start + ti * TILE);
+    lds_wait(kr);
+    floatx4_t s[1] = {floatx4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch)
+      s[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[ch]), qf[ch],
+                                                      s[0], 0, 0, 0);
+    mfma_result_barrier(s);
+    if (nvalid < TILE) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (w * C::kTW + 4 * qg + r >= nvalid) s[0][r] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+    mx = max_rows(mx);
+    float (*wm)[16] = sm.wmax[ti & 1];
+    if (lane < 16) wm[w][lane] = mx;
+    lds_barrier();  // B1(ti)
+
+    float alpha[4];
+    bool moved = false;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * qg + r;
+      const float tm = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+      const float mn = fmaxf(m4[r], tm);
+      moved |= mn != m4[r];
+      alpha[r] = exp2_fast((m4[r] - mn) * c);
+      m4[r] = mn;
+    }
+    const float tm = fmaxf(fmaxf(wm[0][qh], wm[1][qh]), fmaxf(wm[2][qh], wm[3][qh]));
+    const float mn = fmaxf(m_own, tm);
+    const float a_own = exp2_fast((m_own - mn) * c);
+    m_own = mn;
+    const float neg_mc = -(mn * c);
+    float psum = 0.f;
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = exp2_fast(fmaf(s[0][r], c, neg_mc));
+      psum += pr[r];
+    }
+    const int pofs = qh * P::kPitch + (w * C::kTW + 4 * qg) * 2;
+    *reinterpret_cast<u32x2_t*>(ps[0] + pofs) =
+        u32x2_t{qh < G ? pack_bf16(pr[0], pr[1]) : 0u, qh < G ? pack_bf16(pr[2], pr[3]) : 0u};
+    l_own = l_own * a_own + psum;
+    if (ti != count - 1 && __builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
+    }
+    lds_barrier();  // B2(ti): P rows written, V(ti) and K(ti - 1) in LDS
+    pv_tile_cols<GP, 1>(acc, ps, vs[ti & 1], lane, w);
+    if (ti > 0) read_k(ti - 1);
+  }
+
+  // ---- epilogue: denominators over the waves; O needs no reduction
+  const float l = sum_rows(l_own);
+  if (lane < 16) sm.lsum[w][lane] = l;
+  lds_barrier();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * qg + r;
+    if (h >= G) break;
+    const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
+    const float safe = den > 0.f ? den : 1.f;
+    const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
+    const int col = w * P::kCols + qh;
+    const float inv = rcp_fast(safe);
+    const float lv = den > 0.f ? fmaf(m4[r], scale, ln_fast(safe)) : -INFINITY;
+#pragma unroll
+    for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r] * inv;
+    if (w == 0 && qh == 0) lse_out[orow] = lv;
   }
 }
 
@@ -1532,6 +1774,29 @@ void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionAr
 #undef PD_LAUNCH_GP
 }
 
+// The matched protocol at D = 256 with loader wavefronts (matched_stream_kernel),
+// for grids of at most one workgroup per CU.
+void launch_stream(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
+#define PD_LAUNCH_STREAM(GPV)                                                                  \
+  hipLaunchKernelGGL((matched_stream_kernel<GPV>), grid, dim3(2 * kThreads), 0, stream, a.table, \
+                     a.lengths, a.q, a.tsb, a.width, a.T, a.qsb, a.qsh, a.G, a.Hq, a.k, a.v,    \
+                     a.partials, a.lse, a.Hkv, a.splits, a.scale, a.c)
+  switch (gp) {
+    case 1: PD_LAUNCH_STREAM(1); break;
+    case 2: PD_LAUNCH_STREAM(2); break;
+    case 4: PD_LAUNCH_STREAM(4); break;
+    case 8: PD_LAUNCH_STREAM(8); break;
+    default: PD_LAUNCH_STREAM(16); break;
+  }
+#undef PD_LAUNCH_STREAM
+}
+
+// Whether every workgroup of `grid` can have a CU of its own.
+bool one_workgroup_per_cu(dim3 grid) {
+  const int cus = device_cu_count();
+  return cus > 0 && int64_t(grid.x) * grid.y * grid.z <= cus;
+}
+
 // The base and fixed-split protocols at D = 64 with kHeads kv heads per
 // workgroup (matched_partition_kernel's kHeads): gp is the padded size of
 // their query heads, kHeads G <= 16.
@@ -1637,6 +1902,10 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
       case 1024 + kFuseCoherent: launch_tile_d<256, kFuseCoherent>(gp, tgrid, st, a, xcds, groups); break;
       default: launch_tile_d<256, kFuseXcd>(gp, tgrid, st, a, xcds, groups); break;
     }
+    return launch_status(what);
+  }
+  if (head_dim == 256 && !fused && one_workgroup_per_cu(grid)) {
+    launch_stream(gp, grid, st, a);
     return launch_status(what);
   }
   a.order = batch_order(grid);

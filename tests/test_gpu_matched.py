@@ -309,3 +309,44 @@ def test_d256_tile_counts_of_the_column_split_kernel(fused):
     out = matched_decode(*g, resources=res)
     torch.cuda.synchronize()
     check_all(case, g, res, out, where=f"fused={fused}")
+
+
+@pytest.mark.parametrize("splits,tokens,lengths", [
+    (1, 512, [1, 64, 65, 128, 130, 192, 200, 256, 300, 384, 450, 511, 512]),
+    (3, 1024, [2064, 1, 1024, 1025, 2048, 3000, 3072]),
+    (4, 2048, [8192, 6000, 100, 2049]),
+])
+def test_d256_loader_kernel_matches_the_column_split_kernel(splits, tokens, lengths):
+    """D=256 multi-tile partitions run matched_stream_kernel (four compute and four
+    loader wavefronts) when the grid gives every workgroup a CU of its own, else
+    matched_cols_kernel.  Each sequence alone (B=1) and as a row of a batch whose
+    grid exceeds the CUs gives the same partial and LSE bits; the batch passes the
+    oracle."""
+    hq, hkv = 16, 4
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    batch = cus // (splits * hkv) + 1
+    rows = (lengths * batch)[:batch]
+    q, k, v, table, lens = make_case(rows, hq, hkv, 256, seed=77, capacity=splits * tokens)
+    poison_tails(k, v, table, lens)
+    case = (q, k, v, table, lens)
+    g = to_gpu(case)
+
+    def partition(qq, tt, ll):
+        partials = torch.empty((qq.shape[0], hq, splits, 256), device="cuda")
+        lse = torch.empty((qq.shape[0], hq, splits), device="cuda")
+        _native.partition(qq, g[1], g[2], tt, ll, partials, lse, hkv, splits, tokens, 64,
+                          256 ** -0.5)
+        return partials, lse
+
+    big_partials, big_lse = partition(g[0], g[3], g[4])
+    for r in range(len(lengths)):
+        one_partials, one_lse = partition(g[0][r:r + 1], g[3][r:r + 1], g[4][r:r + 1])
+        torch.cuda.synchronize()
+        where = f"length {rows[r]}, {splits} x {tokens}"
+        assert torch.equal(one_partials.view(torch.int32), big_partials[r:r + 1].view(torch.int32)), where
+        assert torch.equal(one_lse.view(torch.int32), big_lse[r:r + 1].view(torch.int32)), where
+    lanes = min(1 << (splits - 1).bit_length(), 32)
+    _, partials, lse, _, partial_bound = OM.matched_decode_with_bounds(*case, splits, tokens, 64,
+                                                                       lanes)
+    np.testing.assert_allclose(to_np(big_lse), lse, atol=2e-5, rtol=1e-6)
+    assert_partials(big_partials, partials, partial_bound)
