@@ -771,7 +771,7 @@ struct OrderedSequence {
   int b, length;
 };
 
-// Requires 0 <= order, 2 <= B <= kMaxOrderedBatch, blockDim.x == kThreads and
+// Requires 0 <= order, 2 <= B <= kMaxOrderedBatch, blockDim.x >= kThreads and
 // every thread of the workgroup; `slens` holds kMaxOrderedBatch + 4 ints of LDS,
 // 16-byte aligned.  One load of the lengths, then thread t counts the
 // sequences ranked before sequence t; the one whose rank row z asks for
@@ -782,7 +782,7 @@ __device__ __forceinline__ OrderedSequence ordered_sequence(const int32_t* __res
   const int tid = threadIdx.x;
   // Entries past B hold INT_MIN: never longer, and a tie only with an index >= B.
   const int len = tid < B ? lengths[tid] : INT32_MIN;
-  slens[tid] = len;
+  if (tid < kMaxOrderedBatch) slens[tid] = len;
   if (tid == 0) slens[kMaxOrderedBatch] = z;  // overwritten below by the one match
   __syncthreads();
   if (tid < B) {

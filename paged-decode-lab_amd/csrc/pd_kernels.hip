@@ -1009,17 +1009,17 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   }
 }
 
-// ------------------------------ D = 256, one workgroup per CU: loader waves
-// The matched protocol at D = 256 for grids that give every workgroup a CU of
-// its own (a few long partitions: 1024-token partitions of one sequence, say).
-// The arithmetic is matched_cols_kernel's, operation for operation, so the
-// partials and LSEs are bit-identical to it; what changes is who loads.  Four
-// wavefronts compute, as matched_cols_kernel's four do, and four more only
-// copy K and V rows into LDS (buffer_load ... lds).  With one workgroup on a
-// CU, each compute wavefront is alone on its SIMD, and a wavefront that
-// issues loads stands still while the CU's load path takes them (about 64
-// bytes per clock, 64 KiB per tile); here the loader wavefronts stand still
-// instead, and the compute wavefronts issue no global load after the query.
+// ------------------------------------- D = 256: P V by columns, loader waves
+// matched_cols_kernel's three protocols with the loads taken off the compute
+// wavefronts: the arithmetic is matched_cols_kernel's, operation for
+// operation, so every output is bit-identical to it; what changes is who
+// loads.  Four wavefronts compute, as matched_cols_kernel's four do, and four
+// more only copy K and V rows into LDS (buffer_load ... lds).  With one
+// workgroup on a CU (the LDS below allows no second), each compute wavefront
+// is alone on its SIMD, and a wavefront that issues loads stands still while
+// the CU's load path takes them (about 64 bytes per clock, 64 KiB per tile);
+// here the loader wavefronts stand still instead, and the compute wavefronts
+// issue no global load after the query.
 //
 // LDS: two K and two V stages of 32 KiB; tile t uses stage t & 1.  K row r of
 // a stage holds its 16-byte piece p at position p ^ (r & 15): the 16 rows of a
@@ -1036,23 +1036,25 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 //          no barrier between them, so K(t - 1) is in LDS too.  K stage t & 1
 //          is free since B1(t): the loaders issue K(t - 2) into it.
 // Issuing 16 KiB takes a loader about as long as the probabilities take the
-// compute wavefronts (the CU's load path moves about 64 bytes per clock), so
-// each barrier interval holds the issue of one tensor's copies: V between B1
-// and B2, K between B2 and the next B1, alongside P V and QK.
-// A first barrier B0 covers K(count - 1), issued with V(count - 1) and
-// K(count - 2) before it.  Both halves pass the same barriers: B0, B1 and B2
-// of every tile, and the one before the epilogue.
-template <int GP>
+// compute wavefronts, so each barrier interval holds the issue of one
+// tensor's copies: V between B1 and B2, K between B2 and the next B1,
+// alongside P V and QK.  A first barrier B0 covers K(count - 1), issued with
+// V(count - 1) and K(count - 2) before it.  Both halves pass the same
+// barriers: B0, B1 and B2 of every tile, the fixed-split walk's barrier after
+// each partition it completes, and the one before the epilogue.
+template <int GP, int kMode>
 __global__ void __launch_bounds__(2 * kThreads, 1)
-matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
-                      const uint16_t* __restrict__ q, int tsb, int width, int T, int qsb,
-                      int qsh, int G, int Hq, const uint16_t* __restrict__ k,
-                      const uint16_t* __restrict__ v, float* __restrict__ partials,
-                      float* __restrict__ lse_out, int Hkv, int splits, float scale, float c) {
+cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
+                   const uint16_t* __restrict__ q, int tsb, int width, int order, int T, int qsb,
+                   int qsh, int G, int hs, int Hq, const uint16_t* __restrict__ k,
+                   const uint16_t* __restrict__ v, float* __restrict__ partials,
+                   float* __restrict__ lse_out, uint16_t* __restrict__ out,
+                   float* __restrict__ maxima, int Hkv, int splits, float scale, float c) {
   constexpr int D = 256;
   using C = Matched<D, GP>;
   using P = TileP<D>;
   constexpr int TILE = C::kTile;
+  constexpr int kTerms = kMode == kMatched ? 1 : 3;
   constexpr int kStage = TILE * D * 2;  // bytes of one K or V stage
   constexpr int kCopies = C::kDma;      // 1 KiB copies per loader, tensor and tile
   static_assert(C::kNG == 1 && C::kTW == 16 && 4 * C::kSlot == kStage && 4 * 1024 * kCopies == kStage,
@@ -1060,22 +1062,34 @@ matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restri
   __shared__ MatchedShared<D, GP> sm;
   __shared__ __attribute__((aligned(16))) char ks[2][kStage];
   __shared__ __attribute__((aligned(16))) char vs[2][kStage];
-  __shared__ __attribute__((aligned(16))) char ps[1][16 * P::kPitch];
+  __shared__ __attribute__((aligned(16))) char ps[kTerms][16 * P::kPitch];
+  __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
 
-  const int p = int(blockIdx.x), kh = int(blockIdx.y), b = int(blockIdx.z);
-  const int qb = kh * G;  // G <= 16: one slice holds the group
+  // The fixed-split protocol walks the whole context of its (kv head,
+  // sequence), as in matched_cols_kernel.
+  constexpr bool kWalk = kMode == kSplit;
+  const int p = kWalk ? 0 : int(blockIdx.x);
+  const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
+  const int qb = kh * G + 16 * slice;
+  const int Gs = min(16, G - 16 * slice);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int w = wv & 3;  // compute wavefront w, or loader w for wv >= 4
+  const bool loader = wv >= 4;
+  const int w = wv & 3;  // compute wavefront w, or loader w
   const int qh = lane & 15, qg = lane >> 4;
   const int start = p * T;
+  OrderedSequence seq{int(blockIdx.z), 0};
+  if (order >= 0) seq = ordered_sequence(lengths, int(gridDim.z), int(blockIdx.z), order, slens);
+  const int b = seq.b;
+  PageWindow<2> pw;
+  if (loader) pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
+  const int length = order >= 0 ? seq.length : lengths[b];
+  const int end = min(kWalk ? splits * T : start + T, length);
+  const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+  const int tpp = T / TILE;  // tiles per partition of the walk
   const int64_t RS = int64_t(Hkv) * D;
 
-  if (wv >= 4) {
-    PageWindow<2> pw;
-    pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
-    const int end = min(start + T, lengths[b]);
-    const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
+  if (loader) {
     if (count == 0) return;
     // Copy i of loader w fills rows 2(8w + i) and 2(8w + i) + 1 of K, pieces
     // in position order; V as matched_cols_kernel's wavefront w copies it.
@@ -1114,21 +1128,21 @@ matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restri
       }
       lds_barrier();  // B2(ti)
       if (ti >= 2) issue(ti - 2, true);
+      if (kWalk && ti % tpp == 0) lds_barrier();  // the walk's partition flush
     }
-    lds_barrier();  // epilogue
+    if constexpr (!kWalk) lds_barrier();  // epilogue
     return;
   }
 
-  const int end = min(start + T, lengths[b]);
-  const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
   if (count == 0) {
-    write_empty_partition<D, kMatched>(tid, b, Hq, qb, G, splits, p, partials, lse_out, nullptr,
-                                       nullptr);
+    for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
+      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
+                                      maxima);
     return;
   }
   bf16x8_t qf[C::kCH];
   {
-    const bool live = qh < G;
+    const bool live = qh < Gs;
     const uint16_t* qrow = q + int64_t(b) * qsb + int64_t(qb + (live ? qh : 0)) * qsh + 8 * qg;
 #pragma unroll
     for (int ch = 0; ch < C::kCH; ++ch)
@@ -1160,6 +1174,7 @@ matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restri
   lds_barrier();  // B0
   read_k(count - 1);
   for (int ti = count - 1; ti >= 0; --ti) {
+    // ---- scores and the tile maxima (matched_cols_kernel's `scores`)
     const int nvalid = end - (start + ti * TILE);
     lds_wait(kr);
     floatx4_t s[1] = {floatx4_t{0.f, 0.f, 0.f, 0.f}};
@@ -1168,6 +1183,10 @@ matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restri
       s[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[ch]), qf[ch],
                                                       s[0], 0, 0, 0);
     mfma_result_barrier(s);
+    if constexpr (kMode != kMatched) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[0][r] *= scale;
+    }
     if (nvalid < TILE) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
@@ -1179,6 +1198,7 @@ matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restri
     if (lane < 16) wm[w][lane] = mx;
     lds_barrier();  // B1(ti)
 
+    // ---- probabilities, P to LDS, rescale (matched_cols_kernel's `finish`)
     float alpha[4];
     bool moved = false;
 #pragma unroll
@@ -1187,24 +1207,40 @@ matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restri
       const float tm = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
       const float mn = fmaxf(m4[r], tm);
       moved |= mn != m4[r];
-      alpha[r] = exp2_fast((m4[r] - mn) * c);
+      alpha[r] = kMode == kMatched ? exp2_fast((m4[r] - mn) * c) : exp_fast(m4[r] - mn);
       m4[r] = mn;
     }
     const float tm = fmaxf(fmaxf(wm[0][qh], wm[1][qh]), fmaxf(wm[2][qh], wm[3][qh]));
     const float mn = fmaxf(m_own, tm);
-    const float a_own = exp2_fast((m_own - mn) * c);
+    const float a_own = kMode == kMatched ? exp2_fast((m_own - mn) * c) : exp_fast(m_own - mn);
     m_own = mn;
     const float neg_mc = -(mn * c);
     float psum = 0.f;
     float pr[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      pr[r] = exp2_fast(fmaf(s[0][r], c, neg_mc));
+      pr[r] = kMode == kMatched ? exp2_fast(fmaf(s[0][r], c, neg_mc)) : exp_fast(s[0][r] - mn);
       psum += pr[r];
     }
     const int pofs = qh * P::kPitch + (w * C::kTW + 4 * qg) * 2;
-    *reinterpret_cast<u32x2_t*>(ps[0] + pofs) =
-        u32x2_t{qh < G ? pack_bf16(pr[0], pr[1]) : 0u, qh < G ? pack_bf16(pr[2], pr[3]) : 0u};
+    if constexpr (kMode == kMatched) {
+      *reinterpret_cast<u32x2_t*>(ps[0] + pofs) =
+          u32x2_t{qh < Gs ? pack_bf16(pr[0], pr[1]) : 0u, qh < Gs ? pack_bf16(pr[2], pr[3]) : 0u};
+    } else {
+      uint32_t t3[3][2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const uint32_t hi = pack_bf16(pr[2 * h2], pr[2 * h2 + 1]);
+        const float r0 = pr[2 * h2] - bf16_lo(hi), r1 = pr[2 * h2 + 1] - bf16_hi(hi);
+        const uint32_t mid = pack_bf16(r0, r1);
+        const uint32_t lo = pack_bf16(r0 - bf16_lo(mid), r1 - bf16_hi(mid));
+        t3[0][h2] = qh < Gs ? lo : 0u;
+        t3[1][h2] = qh < Gs ? mid : 0u;
+        t3[2][h2] = qh < Gs ? hi : 0u;
+      }
+#pragma unroll
+      for (int t = 0; t < 3; ++t) *reinterpret_cast<u32x2_t*>(ps[t] + pofs) = u32x2_t{t3[t][0], t3[t][1]};
+    }
     l_own = l_own * a_own + psum;
     if (ti != count - 1 && __builtin_amdgcn_ballot_w64(moved)) {
 #pragma unroll
@@ -1213,8 +1249,48 @@ matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restri
         for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
     }
     lds_barrier();  // B2(ti): P rows written, V(ti) and K(ti - 1) in LDS
-    pv_tile_cols<GP, 1>(acc, ps, vs[ti & 1], lane, w);
+    pv_tile_cols<GP, kTerms>(acc, ps, vs[ti & 1], lane, w);
     if (ti > 0) read_k(ti - 1);
+
+    if constexpr (kWalk) {
+      // After tile ti, the first tile of partition ti / tpp, that partition
+      // is complete: its (m, l, acc) as matched_cols_kernel's walk stores them
+      // (kernels.py:77-80), and the running state restarts.
+      if (ti % tpp == 0) {
+        const int part = ti / tpp;
+        const float l = sum_rows(l_own);
+        if (lane < 16) sm.lsum[w][lane] = l;
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int h = 4 * qg + r;
+          if (h >= Gs) break;
+          const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
+          const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + part;
+          const int col = w * P::kCols + qh;
+#pragma unroll
+          for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r];
+          if (w == 0 && qh == 0) {
+            maxima[orow] = m4[r];
+            lse_out[orow] = den;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
+        m_own = -INFINITY;
+        l_own = 0.f;
+      }
+    }
+  }
+
+  if constexpr (kWalk) {
+    // Partitions past the sequence's last token are empty.
+    for (int pp = (end + T - 1) / T; pp < splits; ++pp)
+      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
+                                      maxima);
+    return;
   }
 
   // ---- epilogue: denominators over the waves; O needs no reduction
@@ -1224,16 +1300,23 @@ matched_stream_kernel(const int32_t* __restrict__ table, const int32_t* __restri
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int h = 4 * qg + r;
-    if (h >= G) break;
+    if (h >= Gs) break;
     const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
     const float safe = den > 0.f ? den : 1.f;
-    const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
     const int col = w * P::kCols + qh;
-    const float inv = rcp_fast(safe);
-    const float lv = den > 0.f ? fmaf(m4[r], scale, ln_fast(safe)) : -INFINITY;
+    if constexpr (kMode == kBase) {
+      // acc / denom, 0 for an empty sequence (kernels.py:40).
+      uint16_t* dst = out + (int64_t(b) * Hq + qb + h) * D + col;
 #pragma unroll
-    for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r] * inv;
-    if (w == 0 && qh == 0) lse_out[orow] = lv;
+      for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = uint16_t(bf16_bits(acc[j][r] / safe));
+    } else {
+      const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
+      const float inv = rcp_fast(safe);
+      const float lv = den > 0.f ? fmaf(m4[r], scale, ln_fast(safe)) : -INFINITY;
+#pragma unroll
+      for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r] * inv;
+      if (w == 0 && qh == 0) lse_out[orow] = lv;
+    }
   }
 }
 
@@ -1710,9 +1793,11 @@ int xcd_layout() {
 }
 
 // `order` of ordered_sequence (pd_device.h) for a multi-tile launch over
-// `grid` = (splits, kv heads x slices, batch) at two workgroups per CU:
-// * CUs / (grid.x * grid.y) when the whole grid is resident and rows z and
-//   z + that share CUs;
+// `grid` = (splits, kv heads x slices, batch) at `per_cu` workgroups per CU
+// (2 for matched_partition_kernel and matched_cols_kernel, 1 for
+// cols_loader_kernel, whose LDS allows no second):
+// * CUs / (grid.x * grid.y) when two workgroups share each CU, the whole grid
+//   is resident and rows z and z + that share CUs;
 // * 0 (longest first) for up to four rounds of workgroups;
 // * -1 (sequence z) when every workgroup has a CU to itself, the batch has one
 //   sequence or more than kMaxOrderedBatch, the CU count is unknown, or the
@@ -1721,14 +1806,14 @@ int xcd_layout() {
 //   mostly short workgroups (batch 128, lengths up to 4096, D 64, 16 kv heads,
 //   4 fixed partitions) it took the call from 228 to 275 us, and sorting the
 //   batch on the host gained nothing there.
-int batch_order(dim3 grid) {
+int batch_order(dim3 grid, int per_cu) {
   const int B = int(grid.z);
   if (B < 2 || B > kMaxOrderedBatch) return -1;
   const int cus = device_cu_count();
   if (cus <= 0) return -1;
   const int64_t xy = int64_t(grid.x) * grid.y, n = xy * B;
-  if (n <= cus || n > 8 * int64_t(cus)) return -1;
-  if (n <= 2 * int64_t(cus) && cus % xy == 0) return int(cus / xy);
+  if (n <= cus || n > 4 * int64_t(per_cu) * cus) return -1;
+  if (per_cu == 2 && n <= 2 * int64_t(cus) && cus % xy == 0) return int(cus / xy);
   return 0;
 }
 
@@ -1774,27 +1859,23 @@ void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionAr
 #undef PD_LAUNCH_GP
 }
 
-// The matched protocol at D = 256 with loader wavefronts (matched_stream_kernel),
-// for grids of at most one workgroup per CU.
-void launch_stream(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
-#define PD_LAUNCH_STREAM(GPV)                                                                  \
-  hipLaunchKernelGGL((matched_stream_kernel<GPV>), grid, dim3(2 * kThreads), 0, stream, a.table, \
-                     a.lengths, a.q, a.tsb, a.width, a.T, a.qsb, a.qsh, a.G, a.Hq, a.k, a.v,    \
-                     a.partials, a.lse, a.Hkv, a.splits, a.scale, a.c)
+// cols_loader_kernel, the D = 256 partition of every protocol but the fused
+// one.
+template <int kMode>
+void launch_cols_loader(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
+#define PD_LAUNCH_LOADER(GPV)                                                                  \
+  hipLaunchKernelGGL((cols_loader_kernel<GPV, kMode>), grid, dim3(2 * kThreads), 0, stream,     \
+                     a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb, a.qsh, a.G,  \
+                     a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.out, a.maxima, a.Hkv, a.splits, \
+                     a.scale, a.c)
   switch (gp) {
-    case 1: PD_LAUNCH_STREAM(1); break;
-    case 2: PD_LAUNCH_STREAM(2); break;
-    case 4: PD_LAUNCH_STREAM(4); break;
-    case 8: PD_LAUNCH_STREAM(8); break;
-    default: PD_LAUNCH_STREAM(16); break;
+    case 1: PD_LAUNCH_LOADER(1); break;
+    case 2: PD_LAUNCH_LOADER(2); break;
+    case 4: PD_LAUNCH_LOADER(4); break;
+    case 8: PD_LAUNCH_LOADER(8); break;
+    default: PD_LAUNCH_LOADER(16); break;
   }
-#undef PD_LAUNCH_STREAM
-}
-
-// Whether every workgroup of `grid` can have a CU of its own.
-bool one_workgroup_per_cu(dim3 grid) {
-  const int cus = device_cu_count();
-  return cus > 0 && int64_t(grid.x) * grid.y * grid.z <= cus;
+#undef PD_LAUNCH_LOADER
 }
 
 // The base and fixed-split protocols at D = 64 with kHeads kv heads per
@@ -1904,11 +1985,12 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
     }
     return launch_status(what);
   }
-  if (head_dim == 256 && !fused && one_workgroup_per_cu(grid)) {
-    launch_stream(gp, grid, st, a);
+  if (head_dim == 256 && !fused) {
+    a.order = batch_order(grid, 1);
+    launch_cols_loader<kMatched>(gp, grid, st, a);
     return launch_status(what);
   }
-  a.order = batch_order(grid);
+  a.order = batch_order(grid, 2);
   switch (head_dim * 2 + (fused ? 1 : 0)) {
     case 128: launch_partition_d<64, false>(gp, grid, st, a); break;
     case 129: launch_partition_d<64, true>(gp, grid, st, a); break;
@@ -2179,7 +2261,7 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   // 16-head group: a token's two 128-byte rows are one contiguous read.
   const int heads = head_dim != 64 ? 1 : heads_per_workgroup(num_kv_heads, G);
   const dim3 grid(1, heads == 2 ? num_kv_heads / 2 : num_kv_heads * hs, batch);
-  a.order = batch_order(grid);
+  a.order = batch_order(grid, head_dim == 256 ? 1 : 2);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   constexpr int kMode = kSplitMode ? kSplit : kBase;
   if (heads == 2) {
@@ -2190,7 +2272,7 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   switch (head_dim) {
     case 64: launch_partition_d<64, false, kMode>(gp, grid, st, a); break;
     case 128: launch_partition_d<128, false, kMode>(gp, grid, st, a); break;
-    default: launch_partition_d<256, false, kMode>(gp, grid, st, a); break;
+    default: launch_cols_loader<kMode>(gp, grid, st, a); break;
   }
   return launch_status(what);
 }
