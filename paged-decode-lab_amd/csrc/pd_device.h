@@ -458,7 +458,7 @@ struct Matched {
 // depends on the kernel:
 // * row groups (matched_partition_kernel): lanes 0-15 read rows 0-3 of a
 //   16-row group, lanes 16-31 rows 4-7;
-// * column split (matched_tile_kernel, matched_cols_kernel): lanes 0-15 read
+// * column split (matched_tile_kernel, cols_loader_kernel): lanes 0-15 read
 //   rows 0-3 of a 32-token k-step and lanes 16-31 rows 8-11 (rows 4-7 and
 //   12-15 in the second read of the step, which takes the same swizzle).
 // Rows of 2D >= 256 bytes start on bank 0, so the swizzle alone spreads them:

@@ -11,9 +11,10 @@
 //                      partial + LSE), base (FP32 p, whole context, bf16 out)
 //                      and fixed split (FP32 p, (m, l, acc) per partition).
 //                      D = 64 and 128.
-//   matched_cols       the same three protocols at D = 256, with PV split
-//                      across the wavefronts by output columns (P through LDS)
-//                      and K loaded two tiles ahead.
+//   cols_loader        the same three protocols at D = 256 in 512-thread
+//                      workgroups: four wavefronts compute, with PV split by
+//                      output columns (P through LDS), while four copy the K
+//                      and V rows of the next tiles into LDS.
 //   matched_tile       the matched protocol for splits of exactly one tile,
 //                      with PV split across the wavefronts by output columns.
 //   lse_merge          one wavefront per (sequence, query head, 64 columns):
@@ -128,7 +129,7 @@ matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __res
                          uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv,
                          int splits, float scale, float c) {
   static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
-  static_assert(D < 256, "D = 256 runs matched_cols_kernel");
+  static_assert(D < 256, "D = 256 runs cols_loader_kernel");
   static_assert(kHeads == 1 || kMode != kMatched, "kv-head groups change the tile of the protocol");
   static_assert(kHeads == 1 || kHeads == 2, "1 or 2 kv heads per workgroup");
   using C = Matched<D, GP>;
@@ -639,394 +640,33 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<256>::kNBW],
   pv_step(std::integral_constant<int, 1>{});
 }
 
-// ------------------------------------------- D = 256: P V split by columns
-// The partition for D = 256, the same three protocols as
+// ------------------------------------- D = 256: P V by columns, loader waves
+// The partition for D = 256: the same three protocols as
 // matched_partition_kernel and the same scores, maxima, probabilities and
 // denominators (so the same LSEs), with the P V product split by output
-// columns as in matched_tile_kernel: per tile, every wavefront writes its bf16
-// probabilities (three bf16 terms for the base and fixed-split protocols) to
-// LDS, and wavefront w multiplies the whole tile's P by V columns
-// [64w, 64w + 64).  The accumulator then takes 16 VGPRs instead of 64, which
-// leaves room for a second K register set: K rows are loaded two tiles ahead
-// (into the set whose QK products the tile has just used), as below D = 256.
-// There is no cross-wave reduction of O at the end.
+// columns as in matched_tile_kernel: per tile, every compute wavefront writes
+// its bf16 probabilities (three bf16 terms for the base and fixed-split
+// protocols) to LDS, and compute wavefront w multiplies the whole tile's P by
+// V columns [64w, 64w + 64) (pv_tile_cols).  The accumulator takes 16 VGPRs,
+// and O needs no cross-wave reduction at the end.
 //
-// Every wavefront reads every wavefront's V rows, so the V rows of tile ti - 1
-// are copied into the LDS slot of tile ti + 1 only after the first barrier of
-// tile ti (every wavefront has finished P V of tile ti + 1 by then), and P V
-// of tile ti starts after a second barrier, once each wavefront has waited for
-// its own copies of tile ti.  The K rows of tile ti - 2 are loaded right after
-// the V rows of tile ti - 1, so that wait never covers the K rows loaded two
-// tiles ahead: after the V rows of tile ti come the K rows of tile ti - 1 and
-// the V rows of tile ti - 1 and K rows of tile ti - 2 (8 + 8 + 8 loads per
-// wavefront), hence vmcnt(24) before that barrier.
-template <int GP, bool kFused, int kMode>
-__global__ void __launch_bounds__(kThreads, 2)
-matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
-                    const uint16_t* __restrict__ q, int tsb, int width, int order, int T, int qsb,
-                    int qsh, int G, int hs, int Hq, const uint16_t* __restrict__ k,
-                    const uint16_t* __restrict__ v, float* __restrict__ partials,
-                    float* __restrict__ lse_out, int* __restrict__ counters,
-                    uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv, int splits,
-                    float scale, float c) {
-  static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
-  constexpr int D = 256;
-  using C = Matched<D, GP>;
-  using P = TileP<D>;
-  constexpr int TILE = C::kTile;
-  constexpr int kTerms = kMode == kMatched ? 1 : 3;
-  static_assert(C::kNG == 1 && C::kTW == 16 && P::kKS == 2, "D = 256 geometry");
-  constexpr int kKLoads = C::kCH, kVLoads = C::kDma;  // per wavefront and tile
-  __shared__ MatchedShared<D, GP> sm;
-  __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
-  __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
-  __shared__ __attribute__((aligned(16))) char ps[kTerms][16 * P::kPitch];
-  __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
-
-  // The fixed-split protocol walks the whole context of its (kv head,
-  // sequence) in one workgroup (grid.x = 1) and writes the (m, l, acc) of each
-  // T-token partition as the walk leaves it, so a sequence's partitions share
-  // one workgroup's start and its K / V pipeline.
-  constexpr bool kWalk = kMode == kSplit;
-  const int p = kWalk ? 0 : int(blockIdx.x);
-  const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
-  const int qb = kh * G + 16 * slice;
-  const int Gs = min(16, G - 16 * slice);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qh = lane & 15, qg = lane >> 4;
-  const int start = p * T;
-  OrderedSequence seq{int(blockIdx.z), 0};
-  if (order >= 0) seq = ordered_sequence(lengths, int(gridDim.z), int(blockIdx.z), order, slens);
-  const int b = seq.b;
-  PageWindow<2> pw;
-  pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
-  const int length = order >= 0 ? seq.length : lengths[b];
-  const int end = min(kWalk ? splits * T : start + T, length);
-  const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
-  if constexpr (!kFused) {
-    if (count == 0) {
-      for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
-        write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
-                                        maxima);
-      return;
-    }
-  }
-  const int64_t RS = int64_t(Hkv) * D;
-
-  bf16x8_t qf[C::kCH];
-  {
-    const bool live = qh < Gs;
-    const uint16_t* qrow = q + int64_t(b) * qsb + int64_t(qb + (live ? qh : 0)) * qsh + 8 * qg;
-#pragma unroll
-    for (int ch = 0; ch < C::kCH; ++ch)
-      qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
-  }
-  const int koff = ((w * C::kTW + qh) * int(RS) + 8 * qg) * 2;
-  int voff[C::kDma];
-#pragma unroll
-  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, true>(i, lane, w, int(RS));
-
-  floatx4_t acc[P::kNBW];  // O[head 4*qg + r][64w + 16j + qh]
-#pragma unroll
-  for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-  float m4[4];             // running max of heads 4*qg + r
-#pragma unroll
-  for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
-  float m_own = -INFINITY;  // running max of head qh
-  float l_own = 0.f;        // this lane's share of head qh's denominator
-
-  auto issue_k = [&](KTile<D, GP>& R, int ti) __attribute__((always_inline)) {
-    const int t0 = start + ti * TILE;
-    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
-#pragma unroll
-    for (int ch = 0; ch < C::kCH; ++ch) R.k[0][ch] = buffer_load16(buf.k, koff + 64 * ch);
-  };
-  auto issue_v = [&](char* slot, int ti) __attribute__((always_inline)) {
-    const int t0 = start + ti * TILE;
-    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
-#pragma unroll
-    for (int i = 0; i < C::kDma; ++i)
-      lds_copy16(buf.v, slot + w * C::kSlot + 1024 * i, voff[i]);
-  };
-
-  // Tile ti in two parts around the copy of the V rows of tile ti - 1 (into
-  // the slot P V of tile ti + 1 has finished reading) and the refill of R with
-  // the K rows of tile ti - 2, which the caller issues between them: scores
-  // and the tile maximum, then probabilities and P V with the V rows in `slot`.
-  float s0[4];
-  auto scores = [&](KTile<D, GP>& R, int ti) __attribute__((always_inline)) {
-    const int nvalid = end - (start + ti * TILE);
-    floatx4_t s[1] = {floatx4_t{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int ch = 0; ch < C::kCH; ++ch)
-      s[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, R.k[0][ch]),
-                                                      qf[ch], s[0], 0, 0, 0);
-    mfma_result_barrier(s);
-    if constexpr (kMode != kMatched) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[0][r] *= scale;
-    }
-    if (nvalid < TILE) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (w * C::kTW + 4 * qg + r >= nvalid) s[0][r] = -INFINITY;
-    }
-    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
-    mx = max_rows(mx);
-    float (*wm)[16] = sm.wmax[ti & 1];
-    if (lane < 16) wm[w][lane] = mx;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) s0[r] = s[0][r];
-    lds_barrier();
-  };
-  auto finish = [&](const char* slot, int ti, bool first) __attribute__((always_inline)) {
-    float (*wm)[16] = sm.wmax[ti & 1];
-    float alpha[4];
-    bool moved = false;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * qg + r;
-      const float tm = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
-      const float mn = fmaxf(m4[r], tm);
-      moved |= mn != m4[r];
-      alpha[r] = kMode == kMatched ? exp2_fast((m4[r] - mn) * c) : exp_fast(m4[r] - mn);
-      m4[r] = mn;
-    }
-    const float tm = fmaxf(fmaxf(wm[0][qh], wm[1][qh]), fmaxf(wm[2][qh], wm[3][qh]));
-    const float mn = fmaxf(m_own, tm);
-    const float a_own = kMode == kMatched ? exp2_fast((m_own - mn) * c) : exp_fast(m_own - mn);
-    m_own = mn;
-    const float neg_mc = -(mn * c);
-    float psum = 0.f;
-    float pr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      pr[r] = kMode == kMatched ? exp2_fast(fmaf(s0[r], c, neg_mc)) : exp_fast(s0[r] - mn);
-      psum += pr[r];
-    }
-    // P[head qh][tokens w*16 + 4qg .. +3] into row qh of each term's LDS tile
-    // (lo, mid, hi for the FP32 probabilities of the base / split protocols).
-    const int pofs = qh * P::kPitch + (w * C::kTW + 4 * qg) * 2;
-    if constexpr (kMode == kMatched) {
-      *reinterpret_cast<u32x2_t*>(ps[0] + pofs) =
-          u32x2_t{qh < Gs ? pack_bf16(pr[0], pr[1]) : 0u, qh < Gs ? pack_bf16(pr[2], pr[3]) : 0u};
-    } else {
-      uint32_t t3[3][2];
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const uint32_t hi = pack_bf16(pr[2 * h2], pr[2 * h2 + 1]);
-        const float r0 = pr[2 * h2] - bf16_lo(hi), r1 = pr[2 * h2 + 1] - bf16_hi(hi);
-        const uint32_t mid = pack_bf16(r0, r1);
-        const uint32_t lo = pack_bf16(r0 - bf16_lo(mid), r1 - bf16_hi(mid));
-        t3[0][h2] = qh < Gs ? lo : 0u;
-        t3[1][h2] = qh < Gs ? mid : 0u;
-        t3[2][h2] = qh < Gs ? hi : 0u;
-      }
-#pragma unroll
-      for (int t = 0; t < 3; ++t) *reinterpret_cast<u32x2_t*>(ps[t] + pofs) = u32x2_t{t3[t][0], t3[t][1]};
-    }
-    l_own = l_own * a_own + psum;
-    if (!first && __builtin_amdgcn_ballot_w64(moved)) {
-#pragma unroll
-      for (int j = 0; j < P::kNBW; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
-    }
-    // This wavefront's copies of tile ti have landed; after the barrier every
-    // wavefront's have, and every P row is written.
-    if (ti >= 2) wait_vmcnt<2 * kKLoads + kVLoads>();
-    else if (ti == 1) wait_vmcnt<kKLoads + kVLoads>();
-    else wait_vmcnt<0>();
-    lds_barrier();
-    pv_tile_cols<GP, kTerms>(acc, ps, slot, lane, w);
-  };
-
-  // kWalk: after tile ti, the first tile of partition ti / tpp, that
-  // partition is complete: its denominators are summed over the waves and its
-  // (m, l, acc) stored (kernels.py:77-80), and the running state restarts for
-  // the partition before it.  The loads of the next tiles stay in flight.
-  const int tpp = T / TILE;
-  auto flush = [&](int ti) __attribute__((always_inline)) {
-    if (ti % tpp) return;
-    const int part = ti / tpp;
-    const float l = sum_rows(l_own);
-    if (lane < 16) sm.lsum[w][lane] = l;
-    lds_barrier();
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * qg + r;
-      if (h >= Gs) break;
-      const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
-      const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + part;
-      const int col = w * P::kCols + qh;
-#pragma unroll
-      for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r];
-      if (w == 0 && qh == 0) {
-        maxima[orow] = m4[r];
-        lse_out[orow] = den;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
-    m_own = -INFINITY;
-    l_own = 0.f;
-  };
-  auto finish_tile = [&](const char* slot, int ti, bool first) __attribute__((always_inline)) {
-    finish(slot, ti, first);
-    if constexpr (kWalk) flush(ti);
-  };
-
-  // Reverse tile walk (matched_splitkv.py:71), last tile first; register sets
-  // A, B and LDS slots vs0, vs1 alternate.  The first loads, K(ti), V(ti),
-  // K(ti - 1), come in the steady-state order, so the vmcnt above is exact
-  // from the first tile on (smaller for the last two tiles).
-  pw.settle();
-  if (count > 0) {
-    KTile<D, GP> A, B;
-    int ti = count - 1;
-    issue_k(A, ti);
-    issue_v(vs0, ti);
-    if (ti >= 1) issue_k(B, ti - 1);
-    bool first = true;
-    // Pairs of tiles with every load of the steady state issued
-    // unconditionally (so the compiler's own waits for the K registers count
-    // the same loads on every path); the last two or three tiles are peeled.
-    while (ti >= 3) {
-      scores(A, ti);
-      issue_v(vs1, ti - 1);
-      issue_k(A, ti - 2);
-      finish_tile(vs0, ti, first);
-      scores(B, ti - 1);
-      issue_v(vs0, ti - 2);
-      issue_k(B, ti - 3);
-      finish_tile(vs1, ti - 1, false);
-      ti -= 2;
-      first = false;
-    }
-    if (ti == 2) {
-      scores(A, 2);
-      issue_v(vs1, 1);
-      issue_k(A, 0);
-      finish_tile(vs0, 2, first);
-      scores(B, 1);
-      issue_v(vs0, 0);
-      finish_tile(vs1, 1, false);
-      scores(A, 0);
-      finish_tile(vs0, 0, false);
-    } else if (ti == 1) {
-      scores(A, 1);
-      issue_v(vs1, 0);
-      finish_tile(vs0, 1, first);
-      scores(B, 0);
-      finish_tile(vs1, 0, false);
-    } else {
-      scores(A, 0);
-      finish_tile(vs0, 0, first);
-    }
-  }
-
-  if constexpr (kWalk) {
-    // Partitions past the sequence's last token are empty.
-    for (int pp = (end + T - 1) / T; pp < splits; ++pp)
-      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
-                                      maxima);
-    return;
-  }
-
-  // ---- epilogue: denominators over the waves; O needs no reduction
-  const float l = sum_rows(l_own);
-  if (lane < 16) sm.lsum[w][lane] = l;
-  lds_barrier();
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int h = 4 * qg + r;
-    if (h >= Gs) break;
-    const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
-    const float safe = den > 0.f ? den : 1.f;
-    const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
-    const int col = w * P::kCols + qh;
-    if constexpr (kMode == kBase) {
-      // acc / denom, 0 for an empty sequence (kernels.py:40).
-      uint16_t* dst = out + (int64_t(b) * Hq + qb + h) * D + col;
-#pragma unroll
-      for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = uint16_t(bf16_bits(acc[j][r] / safe));
-    } else if constexpr (kMode == kSplit) {
-#pragma unroll
-      for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r];
-      if (w == 0 && qh == 0) {
-        maxima[orow] = m4[r];
-        lse_out[orow] = den;
-      }
-    } else {
-      const float inv = rcp_fast(safe);
-      const float lv = den > 0.f ? fmaf(m4[r], scale, ln_fast(safe)) : -INFINITY;
-      if constexpr (kFused) {
-        // Device-scope stores (global_store sc1), as in matched_partition_kernel.
-#pragma unroll
-        for (int j = 0; j < P::kNBW; ++j)
-          __hip_atomic_store(partials + orow * D + col + 16 * j, acc[j][r] * inv, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        if (w == 0 && qh == 0)
-          __hip_atomic_store(lse_out + orow, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-#pragma unroll
-        for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r] * inv;
-        if (w == 0 && qh == 0) lse_out[orow] = lv;
-      }
-    }
-  }
-
-  if constexpr (kFused) {
-    // Split-completion count and the last workgroup's merge, exactly as in
-    // matched_partition_kernel.
-    int* counter = counters + (int64_t(b) * Hkv + kh) * kCountersPerGroup;  // the first slot
-    wait_memory();
-    __syncthreads();
-    if (tid == 0)
-      sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                splits - 1;
-    __syncthreads();
-    if (!sm.last) return;
-    const int64_t row0 = int64_t(b) * Hq + kh * G;
-    constexpr int kV = D / 64;
-    for (int hh = __builtin_amdgcn_readfirstlane(w); hh < G; hh += 4) {
-      float w0 = 0.f, w1 = 0.f, mrg[kV];
-      merge_splits<kV, kCoherentAux>(
-          partials + (row0 + hh) * splits * D, D, lane * kV, splits,
-          [&] {
-            lse_weights<kCoherentAux>(lse_out + (row0 + hh) * splits, splits, plan_lse_lanes(splits, D),
-                              lane, w0, w1);
-          },
-          [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, mrg);
-      uint16_t* dst = out + (row0 + hh) * D + lane * kV;
-#pragma unroll
-      for (int e = 0; e < kV; ++e) dst[e] = uint16_t(bf16_bits(mrg[e]));
-    }
-    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-// ------------------------------------- D = 256: P V by columns, loader waves
-// matched_cols_kernel's three protocols with the loads taken off the compute
-// wavefronts: the arithmetic is matched_cols_kernel's, operation for
-// operation, so every output is bit-identical to it; what changes is who
-// loads.  Four wavefronts compute, as matched_cols_kernel's four do, and four
-// more only copy K and V rows into LDS (buffer_load ... lds).  With one
-// workgroup on a CU (the LDS below allows no second), each compute wavefront
-// is alone on its SIMD, and a wavefront that issues loads stands still while
-// the CU's load path takes them (about 64 bytes per clock, 64 KiB per tile);
-// here the loader wavefronts stand still instead, and the compute wavefronts
-// issue no global load after the query.
+// Eight wavefronts: four compute and four only copy K and V rows into LDS
+// (buffer_load ... lds).  The LDS below allows one workgroup per CU, so each
+// compute wavefront is alone on its SIMD; a wavefront that issues loads
+// stands still while the CU's load path takes them (about 64 bytes per clock,
+// 64 KiB per tile), so here the loader wavefronts stand still instead, and the
+// compute wavefronts issue no global load after the query.  (Four wavefronts
+// that loaded for themselves, K two tiles ahead into registers and V into
+// LDS, at two workgroups per CU, took 1.17-1.40x the time on few long
+// partitions and 1.02-1.06x on full grids; the outputs are the same bits.)
 //
 // LDS: two K and two V stages of 32 KiB; tile t uses stage t & 1.  K row r of
 // a stage holds its 16-byte piece p at position p ^ (r & 15): the 16 rows of a
 // compute wavefront's ds_read_b128 (one piece each) then fall on 16 distinct
 // 16-byte bank groups, and each loader copy (1 KiB, two rows, every eight
-// consecutive lanes one 128-byte line) writes one contiguous KiB.  V rows are
-// in matched_cols_kernel's layout.
+// consecutive lanes one 128-byte line) writes one contiguous KiB.  Compute
+// wavefront w's V rows (tokens 16w .. 16w + 15) are loader w's kSlot part of
+// a V stage, pieces permuted by vswz.
 //
 // Schedule, tile t (last to first), around the compute wavefronts' barriers:
 //   B1(t)  after QK(t) and the tile maxima.  V stage (t + 1) & 1 is free (P V
@@ -1041,15 +681,18 @@ matched_cols_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
 // alongside P V and QK.  A first barrier B0 covers K(count - 1), issued with
 // V(count - 1) and K(count - 2) before it.  Both halves pass the same
 // barriers: B0, B1 and B2 of every tile, the fixed-split walk's barrier after
-// each partition it completes, and the one before the epilogue.
-template <int GP, int kMode>
+// each partition it completes, the one before the epilogue and the fused
+// split count's two.
+template <int GP, bool kFused, int kMode>
 __global__ void __launch_bounds__(2 * kThreads, 1)
 cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
                    const uint16_t* __restrict__ q, int tsb, int width, int order, int T, int qsb,
                    int qsh, int G, int hs, int Hq, const uint16_t* __restrict__ k,
                    const uint16_t* __restrict__ v, float* __restrict__ partials,
-                   float* __restrict__ lse_out, uint16_t* __restrict__ out,
-                   float* __restrict__ maxima, int Hkv, int splits, float scale, float c) {
+                   float* __restrict__ lse_out, int* __restrict__ counters,
+                   uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv, int splits,
+                   float scale, float c) {
+  static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
   constexpr int D = 256;
   using C = Matched<D, GP>;
   using P = TileP<D>;
@@ -1066,7 +709,9 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
 
   // The fixed-split protocol walks the whole context of its (kv head,
-  // sequence), as in matched_cols_kernel.
+  // sequence) in one workgroup (grid.x = 1) and writes the (m, l, acc) of each
+  // T-token partition as the walk leaves it, so a sequence's partitions share
+  // one workgroup's start and its K / V pipeline.
   constexpr bool kWalk = kMode == kSplit;
   const int p = kWalk ? 0 : int(blockIdx.x);
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
@@ -1090,9 +735,9 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   const int64_t RS = int64_t(Hkv) * D;
 
   if (loader) {
-    if (count == 0) return;
+    if (!kFused && count == 0) return;
     // Copy i of loader w fills rows 2(8w + i) and 2(8w + i) + 1 of K, pieces
-    // in position order; V as matched_cols_kernel's wavefront w copies it.
+    // in position order, and of V the rows of compute wavefront w.
     int koff[kCopies], voff[kCopies];
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) {
@@ -1109,15 +754,17 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       for (int i = 0; i < kCopies; ++i)
         lds_copy16(is_k ? buf.k : buf.v, dst + 1024 * i, is_k ? koff[i] : voff[i]);
     };
-    issue(count - 1, true);
-    issue(count - 1, false);
-    if (count >= 2) {
-      issue(count - 2, true);
-      wait_vmcnt<2 * kCopies>();
-    } else {
-      wait_vmcnt<kCopies>();
+    if (count > 0) {
+      issue(count - 1, true);
+      issue(count - 1, false);
+      if (count >= 2) {
+        issue(count - 2, true);
+        wait_vmcnt<2 * kCopies>();
+      } else {
+        wait_vmcnt<kCopies>();
+      }
+      lds_barrier();  // B0
     }
-    lds_barrier();  // B0
     for (int ti = count - 1; ti >= 0; --ti) {
       lds_barrier();  // B1(ti)
       if (ti >= 1) {
@@ -1131,10 +778,14 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       if (kWalk && ti % tpp == 0) lds_barrier();  // the walk's partition flush
     }
     if constexpr (!kWalk) lds_barrier();  // epilogue
+    if constexpr (kFused) {
+      __syncthreads();  // the split count's two barriers
+      __syncthreads();
+    }
     return;
   }
 
-  if (count == 0) {
+  if (!kFused && count == 0) {
     for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
       write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
                                       maxima);
@@ -1171,10 +822,12 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   float m_own = -INFINITY;  // running max of head qh
   float l_own = 0.f;        // this lane's share of head qh's denominator
 
-  lds_barrier();  // B0
-  read_k(count - 1);
+  if (count > 0) {
+    lds_barrier();  // B0
+    read_k(count - 1);
+  }
   for (int ti = count - 1; ti >= 0; --ti) {
-    // ---- scores and the tile maxima (matched_cols_kernel's `scores`)
+    // ---- scores and the tile maxima
     const int nvalid = end - (start + ti * TILE);
     lds_wait(kr);
     floatx4_t s[1] = {floatx4_t{0.f, 0.f, 0.f, 0.f}};
@@ -1198,7 +851,8 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     if (lane < 16) wm[w][lane] = mx;
     lds_barrier();  // B1(ti)
 
-    // ---- probabilities, P to LDS, rescale (matched_cols_kernel's `finish`)
+    // ---- probabilities, P to LDS (lo, mid, hi for the FP32 probabilities of
+    // the base / split protocols), rescale of O
     float alpha[4];
     bool moved = false;
 #pragma unroll
@@ -1254,8 +908,10 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 
     if constexpr (kWalk) {
       // After tile ti, the first tile of partition ti / tpp, that partition
-      // is complete: its (m, l, acc) as matched_cols_kernel's walk stores them
-      // (kernels.py:77-80), and the running state restarts.
+      // is complete: its denominators are summed over the waves and its
+      // (m, l, acc) stored (kernels.py:77-80), and the running state restarts
+      // for the partition before it.  The copies of the next tiles stay in
+      // flight.
       if (ti % tpp == 0) {
         const int part = ti / tpp;
         const float l = sum_rows(l_own);
@@ -1313,10 +969,50 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
       const float inv = rcp_fast(safe);
       const float lv = den > 0.f ? fmaf(m4[r], scale, ln_fast(safe)) : -INFINITY;
+      if constexpr (kFused) {
+        // Device-scope stores (global_store sc1), as in matched_partition_kernel.
 #pragma unroll
-      for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r] * inv;
-      if (w == 0 && qh == 0) lse_out[orow] = lv;
+        for (int j = 0; j < P::kNBW; ++j)
+          __hip_atomic_store(partials + orow * D + col + 16 * j, acc[j][r] * inv, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        if (w == 0 && qh == 0)
+          __hip_atomic_store(lse_out + orow, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+#pragma unroll
+        for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r] * inv;
+        if (w == 0 && qh == 0) lse_out[orow] = lv;
+      }
     }
+  }
+
+  if constexpr (kFused) {
+    // Split-completion count and the last workgroup's merge, exactly as in
+    // matched_partition_kernel; the loader wavefronts pass the two barriers
+    // and leave.
+    int* counter = counters + (int64_t(b) * Hkv + kh) * kCountersPerGroup;  // the first slot
+    wait_memory();
+    __syncthreads();
+    if (tid == 0)
+      sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                splits - 1;
+    __syncthreads();
+    if (!sm.last) return;
+    const int64_t row0 = int64_t(b) * Hq + kh * G;
+    constexpr int kV = D / 64;
+    for (int hh = __builtin_amdgcn_readfirstlane(w); hh < G; hh += 4) {
+      float w0 = 0.f, w1 = 0.f, mrg[kV];
+      merge_splits<kV, kCoherentAux>(
+          partials + (row0 + hh) * splits * D, D, lane * kV, splits,
+          [&] {
+            lse_weights<kCoherentAux>(lse_out + (row0 + hh) * splits, splits,
+                                      plan_lse_lanes(splits, D), lane, w0, w1);
+          },
+          [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, mrg);
+      uint16_t* dst = out + (row0 + hh) * D + lane * kV;
+#pragma unroll
+      for (int e = 0; e < kV; ++e) dst[e] = uint16_t(bf16_bits(mrg[e]));
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1794,8 +1490,8 @@ int xcd_layout() {
 
 // `order` of ordered_sequence (pd_device.h) for a multi-tile launch over
 // `grid` = (splits, kv heads x slices, batch) at `per_cu` workgroups per CU
-// (2 for matched_partition_kernel and matched_cols_kernel, 1 for
-// cols_loader_kernel, whose LDS allows no second):
+// (2 for matched_partition_kernel, 1 for cols_loader_kernel, whose LDS
+// allows no second):
 // * CUs / (grid.x * grid.y) when two workgroups share each CU, the whole grid
 //   is resident and rows z and z + that share CUs;
 // * 0 (longest first) for up to four rounds of workgroups;
@@ -1835,20 +1531,15 @@ void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a
 #undef PD_LAUNCH_TILE
 }
 
-// D = 256 runs matched_cols_kernel, the other head dims matched_partition_kernel.
+// The multi-tile partition at D = 64 and 128 (matched_partition_kernel).
 template <int D, bool kFused, int kMode = kMatched>
 void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
+  static_assert(D < 256, "D = 256 runs cols_loader_kernel");
 #define PD_LAUNCH_GP(GPV)                                                                      \
-  if constexpr (D == 256)                                                                      \
-    hipLaunchKernelGGL((matched_cols_kernel<GPV, kFused, kMode>), grid, dim3(kThreads), 0,      \
-                       stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb,   \
-                       a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out, \
-                       a.maxima, a.Hkv, a.splits, a.scale, a.c);                               \
-  else                                                                                         \
-    hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused, kMode>), grid, dim3(kThreads), \
-                       0, stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T,      \
-                       a.qsb, a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, \
-                       a.out, a.maxima, a.Hkv, a.splits, a.scale, a.c)
+  hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused, kMode>), grid, dim3(kThreads),   \
+                     0, stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb,   \
+                     a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,   \
+                     a.maxima, a.Hkv, a.splits, a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_GP(1); break;
     case 2: PD_LAUNCH_GP(2); break;
@@ -1859,15 +1550,14 @@ void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionAr
 #undef PD_LAUNCH_GP
 }
 
-// cols_loader_kernel, the D = 256 partition of every protocol but the fused
-// one.
-template <int kMode>
+// The multi-tile partition at D = 256 (cols_loader_kernel), every protocol.
+template <bool kFused, int kMode>
 void launch_cols_loader(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_LOADER(GPV)                                                                  \
-  hipLaunchKernelGGL((cols_loader_kernel<GPV, kMode>), grid, dim3(2 * kThreads), 0, stream,     \
-                     a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb, a.qsh, a.G,  \
-                     a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.out, a.maxima, a.Hkv, a.splits, \
-                     a.scale, a.c)
+  hipLaunchKernelGGL((cols_loader_kernel<GPV, kFused, kMode>), grid, dim3(2 * kThreads), 0,     \
+                     stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb,     \
+                     a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,   \
+                     a.maxima, a.Hkv, a.splits, a.scale, a.c)
   switch (gp) {
     case 1: PD_LAUNCH_LOADER(1); break;
     case 2: PD_LAUNCH_LOADER(2); break;
@@ -1985,19 +1675,14 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
     }
     return launch_status(what);
   }
-  if (head_dim == 256 && !fused) {
-    a.order = batch_order(grid, 1);
-    launch_cols_loader<kMatched>(gp, grid, st, a);
-    return launch_status(what);
-  }
-  a.order = batch_order(grid, 2);
+  a.order = batch_order(grid, head_dim == 256 ? 1 : 2);
   switch (head_dim * 2 + (fused ? 1 : 0)) {
     case 128: launch_partition_d<64, false>(gp, grid, st, a); break;
     case 129: launch_partition_d<64, true>(gp, grid, st, a); break;
     case 256: launch_partition_d<128, false>(gp, grid, st, a); break;
     case 257: launch_partition_d<128, true>(gp, grid, st, a); break;
-    case 512: launch_partition_d<256, false>(gp, grid, st, a); break;
-    default: launch_partition_d<256, true>(gp, grid, st, a); break;
+    case 512: launch_cols_loader<false, kMatched>(gp, grid, st, a); break;
+    default: launch_cols_loader<true, kMatched>(gp, grid, st, a); break;
   }
   return launch_status(what);
 }
@@ -2272,7 +1957,7 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   switch (head_dim) {
     case 64: launch_partition_d<64, false, kMode>(gp, grid, st, a); break;
     case 128: launch_partition_d<128, false, kMode>(gp, grid, st, a); break;
-    default: launch_cols_loader<kMode>(gp, grid, st, a); break;
+    default: launch_cols_loader<false, kMode>(gp, grid, st, a); break;
   }
   return launch_status(what);
 }

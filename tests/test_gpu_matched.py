@@ -297,9 +297,10 @@ def test_single_split_beyond_the_prefetched_table_window():
 
 
 @pytest.mark.parametrize("fused", [False, True])
-def test_d256_tile_counts_of_the_column_split_kernel(fused):
-    """D=256 multi-tile splits run matched_cols_kernel, whose pipeline peels the last
-    two or three tiles: splits of 1 to 8 tiles (64 tokens each), full and partial."""
+def test_d256_tile_counts_of_the_loader_kernel(fused):
+    """D=256 multi-tile splits run cols_loader_kernel, whose loader wavefronts issue
+    and wait differently for one, two and more tiles: splits of 1 to 8 tiles (64
+    tokens each), full and partial."""
     lengths = [1, 64, 65, 128, 130, 192, 200, 256, 300, 384, 450, 511, 512]
     case = make_case(lengths, 16, 4, 256, seed=41, capacity=512)
     g = to_gpu(case)
@@ -316,11 +317,11 @@ def test_d256_tile_counts_of_the_column_split_kernel(fused):
     (3, 1024, [2064, 1, 1024, 1025, 2048, 3000, 3072]),
     (4, 2048, [8192, 6000, 100, 2049]),
 ])
-def test_d256_loader_kernel_matches_the_column_split_kernel(splits, tokens, lengths):
-    """D=256 multi-tile partitions run matched_stream_kernel (four compute and four
-    loader wavefronts) when the grid gives every workgroup a CU of its own, else
-    matched_cols_kernel.  Each sequence alone (B=1) and as a row of a batch whose
-    grid exceeds the CUs gives the same partial and LSE bits; the batch passes the
+def test_d256_partials_of_a_sequence_alone_and_in_a_batch(splits, tokens, lengths):
+    """D=256 multi-tile partitions (cols_loader_kernel) of each sequence alone (B=1,
+    every workgroup on a CU of its own) and as a row of a batch whose grid exceeds
+    the CUs (two rounds, longest first): the same partial and LSE bits, with
+    partial tiles, NaN-poisoned tails and several splits; the batch passes the
     oracle."""
     hq, hkv = 16, 4
     cus = torch.cuda.get_device_properties(0).multi_processor_count

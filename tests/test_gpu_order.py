@@ -1,9 +1,10 @@
 """Batch order of the multi-tile kernels, on the GPU.
 
-With more workgroups than CUs, matched_partition_kernel and matched_cols_kernel hand the
+With more workgroups than CUs, matched_partition_kernel and cols_loader_kernel hand the
 grid's batch rows to the sequences in order of length (ordered_sequence in pd_device.h):
 longest first when the grid runs in two to four rounds, long paired with short on a CU
-when the whole grid is resident; past four rounds the batch keeps its order.  Which workgroup runs an item must not change a bit of the
+when the whole grid is resident at two workgroups per CU (matched_partition_kernel);
+past four rounds the batch keeps its order.  Which workgroup runs an item must not change a bit of the
 result.  Each case runs a batch large enough to switch the ordering on (the mode named
 is the one a 256-CU device takes) and compares every output row, bit for bit, with the
 same sequence run alone (batch 1, where the order is the identity), under the same plan.
@@ -54,7 +55,7 @@ def _check_rows(full, g, alone):
 MATCHED = [
     (128, 32, 8, 64, 2048),    # 512 workgroups, resident: rows z and z + 32 paired
     (128, 8, 8, 48, 2048),     # 384 workgroups: rows 16..31 alone on their CU, 32 paired
-    (256, 32, 4, 128, 2048),   # 512 workgroups (matched_cols_kernel): z and z + 64 paired
+    (256, 32, 4, 128, 2048),   # 512 workgroups, one per CU (cols_loader_kernel): longest first
     (64, 16, 16, 128, 1024),   # 2048 workgroups: longest first
     (128, 8, 8, 256, 512),     # 2048 workgroups, the largest batch that is ranked
     (128, 8, 8, 257, 512),     # 2056 workgroups, one sequence too many: as given
@@ -78,7 +79,7 @@ def test_matched_rows_do_not_depend_on_the_batch_order(dim, hq, hkv, batch, capa
 
 
 def test_two_sequences_over_many_splits():
-    """64 splits x 4 kv heads x 2 sequences = 512 workgroups: rows 0 and 1 share CUs."""
+    """64 splits x 4 kv heads x 2 sequences = 512 workgroups in two rounds: longest first."""
     dim, hq, hkv, capacity = 256, 16, 4, 8192
     lengths = np.array([8192, 3000], dtype=np.int32)
     g = pooled_case(lengths, hq, hkv, dim, capacity, pool_pages=96, seed=2)
@@ -96,7 +97,7 @@ def test_fused_matched_rows_do_not_depend_on_the_batch_order():
     dim, hq, hkv, batch, capacity = 256, 16, 4, 64, 2048
     lengths = _lengths(batch, capacity, seed=7)
     g = pooled_case(lengths, hq, hkv, dim, capacity, pool_pages=batch * 8 + 64, seed=7)
-    # 2 splits x 4 kv heads x 64 sequences = 512 workgroups, rows z and z + 32 paired
+    # 2 splits x 4 kv heads x 64 sequences = 512 workgroups in two rounds: longest first
     res = allocate_matched_resources(DecodeSpec(batch, hq, hkv, dim, capacity), "cuda",
                                      num_splits=2, fused=True)
     full = matched_decode(*g, resources=res).clone()
@@ -107,7 +108,7 @@ def test_fused_matched_rows_do_not_depend_on_the_batch_order():
 
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
 @pytest.mark.parametrize("dim,hq,hkv,batch,capacity", [
-    (256, 32, 4, 128, 2048),   # base: 512 resident workgroups; splitk: 1024, longest first
+    (256, 32, 4, 128, 2048),   # 512 workgroups, one per CU, in two rounds: longest first
     (64, 16, 16, 128, 2048),   # kv-head pairs: 1024 workgroups, longest first
     (64, 32, 8, 64, 2048),     # kv-head pairs of 4-head groups: 256 workgroups, one per CU
     (128, 32, 8, 40, 2048),    # base: 320 workgroups, rows 8..31 alone on their CU

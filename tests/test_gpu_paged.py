@@ -172,9 +172,10 @@ def test_groups_larger_than_16_heads(backend, dim, hq, hkv):
 
 
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
-def test_d256_tile_counts_of_the_column_split_kernel(backend):
-    """D=256 runs matched_cols_kernel for both backends: whole contexts (base) and
-    1024-token partitions (split) of 1 to 20 tiles, full and partial."""
+def test_d256_tile_counts_of_the_loader_kernel(backend):
+    """D=256 runs cols_loader_kernel for both backends: whole contexts (base) and
+    1024-token partitions (split) of 1 to 20 tiles, full and partial: the loader
+    wavefronts' prologue and waits differ for one, two and more tiles."""
     lengths = [1, 64, 65, 129, 192, 255, 320, 1023, 1024, 1025, 1100, 1280]
     q, k, v, table, lens = make_case(lengths, 8, 2, 256, seed=43, capacity=1280)
     poison_tails(k, v, table, lens)
