@@ -403,6 +403,7 @@ def profile_launches(torch, which, calls=50):
     written), used to scale FETCH_SIZE / WRITE_SIZE.  headline: partition and
     merge at the headline shape.  sweep: partition and merge of the bandwidth sweep.
     long: partition and merge at D256 GQA 4:1, B=1, context 131072 (KV from HBM).
+    parts: the headline shape with 1024-token partitions (3 splits, 12 workgroups).
     edge: paged_decode's hip_base and hip_splitk on the edge-coverage batches (B=128,
     a quarter of the lengths 0, the rest U[1, 4096]; D 64 MHA 16/16, D 256 GQA 32/4).
     decoder: the 24-layer random-init decoder, prompt 512, 16 greedy decode steps as
@@ -433,6 +434,13 @@ def profile_launches(torch, which, calls=50):
             case["merge"]()
         torch.cuda.synchronize()
         del case
+    if "parts" in which:
+        case = matched_case(torch, 1, 16, 4, 256, 2112, [2064], 20261105)
+        full, _ = fixed_partition_case(torch, case)
+        for _ in range(calls):
+            full()
+        torch.cuda.synchronize()
+        del case, full
     if "long" in which:
         case = matched_case(torch, 1, 16, 4, 256, 131072, [131072], 11)
         for _ in range(10):
@@ -676,7 +684,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the extra measurements")
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU run")
-    ap.add_argument("--profile", default=None, metavar="headline,sweep,long,edge,decoder",
+    ap.add_argument("--profile", default=None, metavar="headline,sweep,long,parts,edge,decoder",
                     help="only make eager launches for rocprofv3 (calibration copy + cases)")
     ap.add_argument("--require-idle-gpu", action="store_true",
                     help="refuse to run (before any GPU work) if amd-smi lists other processes")
