@@ -454,26 +454,21 @@ struct Matched {
 // LDS serves 32 lanes of a ds_read_b64_tr_b16 per clock, 256 bytes over 64
 // four-byte banks; each lane's 8 bytes are two pieces' halves of one row, and
 // each row's 4 lanes read two adjacent pieces (32 bytes).  The 32 lanes must
-// therefore land on 8 distinct 32-byte bank groups.  Which 8 rows they read
-// depends on the kernel:
-// * row groups (matched_partition_kernel): lanes 0-15 read rows 0-3 of a
-//   16-row group, lanes 16-31 rows 4-7;
-// * column split (matched_tile_kernel, cols_loader_kernel): lanes 0-15 read
-//   rows 0-3 of a 32-token k-step and lanes 16-31 rows 8-11 (rows 4-7 and
-//   12-15 in the second read of the step, which takes the same swizzle).
-// Rows of 2D >= 256 bytes start on bank 0, so the swizzle alone spreads them:
-// bits 0-1 of the row pick one of 4 pairs of pieces, and bit 2 (row groups)
-// or bit 3 (column split) one of two 128-byte halves.  Rows of 128 bytes
-// (D = 64) alternate between the two halves by their own address (bit 0),
-// so the swizzle spreads the rows of one half over its 4 pairs of pieces.
-template <int D, bool kColSplit>
+// therefore land on 8 distinct 32-byte bank groups.  The kernels split P V by
+// output columns: lanes 0-15 read rows 0-3 of a 32-row k-step and lanes 16-31
+// rows 8-11 (rows 4-7 and 12-15 in the second read of the step, which takes
+// the same swizzle).  Rows of 2D >= 256 bytes start on bank 0, so the swizzle
+// alone spreads them: bits 0-1 of the row pick one of 4 pairs of pieces, and
+// bit 3 one of two 128-byte halves.  Rows of 128 bytes (D = 64) alternate
+// between the two halves by their own address (bit 0), so the swizzle spreads
+// the rows of one half over its 4 pairs of pieces.  (A swizzle by r mod 4
+// alone left a 2-way conflict on every read.)
+template <int D>
 __device__ __forceinline__ int vswz(int row) {
   if constexpr (D >= 128)
-    return 2 * (row & 3) + 8 * ((row >> (kColSplit ? 3 : 2)) & 1);
-  else if constexpr (kColSplit)
-    return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1));
+    return 2 * (row & 3) + 8 * ((row >> 3) & 1);
   else
-    return 2 * ((row >> 1) & 3);
+    return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1));
 }
 
 // Element offset (tile-relative) of tile row R: token R / H of the
@@ -486,21 +481,35 @@ __device__ __forceinline__ int tile_row_elems(int R, int RS) {
 
 // Source byte offset (tile-relative) of the 16 bytes that DMA copy i of
 // wavefront w places at LDS position 16 * (64 i + lane) of its rows.
-template <int D, int GP, bool kColSplit, int H = 1>
+template <int D, int GP, int H = 1>
 __device__ __forceinline__ int v_copy_offset(int i, int lane, int w, int RS) {
   using C = Matched<D, GP>;
   const int slot = 64 * i + lane;
   const int row = slot / C::kPieces, pos = slot % C::kPieces;
-  return (tile_row_elems<D, H>(w * C::kTW + row, RS) + 8 * (pos ^ vswz<D, kColSplit>(row))) * 2;
+  return (tile_row_elems<D, H>(w * C::kTW + row, RS) + 8 * (pos ^ vswz<D>(row))) * 2;
 }
 
 // Byte offset within a V row of this lane's 8 bytes of a transposed read of
 // the 16 columns from col0 (a multiple of 16): lane l % 4 = b reads columns
 // col0 + 4b .. +3 of a row whose index within its 16-row group is `row`.
-template <int D, bool kColSplit>
+template <int D>
 __device__ __forceinline__ int v_read_offset(int col0, int lane, int row) {
   const int b = lane & 3;
-  return 16 * (((col0 >> 3) + (b >> 1)) ^ vswz<D, kColSplit>(row)) + 8 * (b & 1);
+  return 16 * (((col0 >> 3) + (b >> 1)) ^ vswz<D>(row)) + 8 * (b & 1);
+}
+
+// K rows staged in LDS by loader wavefronts (cols_loader_kernel): row r of a
+// tile holds its 16-byte piece p at position p ^ kswz(r).  A compute
+// wavefront's ds_read_b128 reads one piece from each of 16 consecutive rows,
+// and 16 lanes are served per clock (256 bytes over 64 four-byte banks), so
+// the 16 pieces must fall on distinct 16-byte bank groups: rows of 2D >= 256
+// bytes start on bank 0 and the XOR with r & 15 spreads them; 128-byte rows
+// (D = 64) alternate halves by address and the XOR with (r >> 1) & 7 spreads
+// each half.  The XOR keeps aligned groups of 8 pieces together, so eight
+// consecutive lanes of a loader copy still read one 128-byte line.
+template <int D>
+__device__ __forceinline__ int kswz(int row) {
+  return D >= 128 ? (row & 15) : ((row >> 1) & 7);
 }
 
 template <int D, int GP>
@@ -745,37 +754,24 @@ struct PageWindow {
 // Which sequence the workgroups of grid row z serve.  Every (split, kv head,
 // sequence) item computes the same values whichever workgroup runs it, so a
 // launch may hand the grid rows to the sequences in any order; taking them by
-// length evens out the work per CU.  The dispatcher sends workgroup i to XCD
-// i % 8; while the whole grid is resident (two workgroups per CU), workgroups
-// i and i + CUs share a CU; past that, each new workgroup takes the next free
-// slot.  `order` (chosen by the launcher from the grid and the CU count):
+// length evens out the work per CU when the grid runs in several rounds (one
+// workgroup per CU), since the longest items then start first.  `order`
+// (chosen by the launcher from the grid and the CU count):
 //   < 0   row z serves sequence z;
-//   0     row z serves the sequence of length rank z (longest first: the grid
-//         runs in several rounds, and the longest items start first);
-//   H > 0 the grid is resident at once and rows z and z + H share CUs: rows
-//         without a partner (z in [B - H, H)) take the longest sequences, and
-//         each pair (z, z + H) one long and one short sequence.
+//   0     row z serves the sequence of length rank z.
 // Ranks order the lengths decreasing, ties by increasing index, so they are a
 // permutation of [0, B).
 constexpr int kMaxOrderedBatch = 256;
 static_assert(kMaxOrderedBatch == kThreads, "one thread per sequence");
 
-__device__ __forceinline__ int order_rank(int z, int B, int order) {
-  if (order <= 0 || B > 2 * order) return z;
-  const int H = order, P = B > H ? B - H : 0;  // P rows z in [0, P) have partner z + H
-  if (z >= H) return B - 1 - (z - H);
-  return z >= P ? z - P : H - P + z;
-}
-
 struct OrderedSequence {
   int b, length;
 };
 
-// Requires 0 <= order, 2 <= B <= kMaxOrderedBatch, blockDim.x >= kThreads and
+// Requires order == 0, 2 <= B <= kMaxOrderedBatch, blockDim.x >= kThreads and
 // every thread of the workgroup; `slens` holds kMaxOrderedBatch + 4 ints of LDS,
 // 16-byte aligned.  One load of the lengths, then thread t counts the
-// sequences ranked before sequence t; the one whose rank row z asks for
-// publishes its index.
+// sequences ranked before sequence t; the one of rank z publishes its index.
 __device__ __forceinline__ OrderedSequence ordered_sequence(const int32_t* __restrict__ lengths,
                                                             int B, int z, int order,
                                                             int* __restrict__ slens) {
@@ -786,7 +782,6 @@ __device__ __forceinline__ OrderedSequence ordered_sequence(const int32_t* __res
   if (tid == 0) slens[kMaxOrderedBatch] = z;  // overwritten below by the one match
   __syncthreads();
   if (tid < B) {
-    const int want = order_rank(z, B, order);
     int rank = 0;
     const int4* s4 = reinterpret_cast<const int4*>(slens);
     for (int u = 0; u < B; u += 4) {
@@ -796,7 +791,7 @@ __device__ __forceinline__ OrderedSequence ordered_sequence(const int32_t* __res
       rank += int(x.z > len) + int(x.z == len && u + 2 < tid);
       rank += int(x.w > len) + int(x.w == len && u + 3 < tid);
     }
-    if (rank == want) slens[kMaxOrderedBatch] = tid;
+    if (rank == z) slens[kMaxOrderedBatch] = tid;
   }
   __syncthreads();
   const int b = __builtin_amdgcn_readfirstlane(slens[kMaxOrderedBatch]);

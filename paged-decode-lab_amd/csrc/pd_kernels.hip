@@ -2,19 +2,18 @@
 // launchers.  See include/paged_decode.h for the tensor contract.
 //
 // Kernels
-//   matched_partition  one 256-thread workgroup per (split, kv head, sequence):
-//                      QK^T on MFMA (v_mfma_f32_16x16x32_bf16), FP32 online
-//                      softmax over 16384/D-token tiles walked last-to-first,
-//                      PV on MFMA with the probabilities taken from the QK
-//                      result registers and V staged in LDS by buffer_load ...
-//                      lds.  Three protocols: matched (bf16 p, normalized FP32
-//                      partial + LSE), base (FP32 p, whole context, bf16 out)
-//                      and fixed split (FP32 p, (m, l, acc) per partition).
-//                      D = 64 and 128.
-//   cols_loader        the same three protocols at D = 256 in 512-thread
-//                      workgroups: four wavefronts compute, with PV split by
-//                      output columns (P through LDS), while four copy the K
-//                      and V rows of the next tiles into LDS.
+//   cols_loader        one 512-thread workgroup per (split, kv head, sequence)
+//                      (per (kv head, sequence) for the base and fixed-split
+//                      protocols, which walk the whole context): QK^T on MFMA
+//                      (v_mfma_f32_16x16x32_bf16), FP32 online softmax over
+//                      16384/D-row tiles walked last-to-first, P through LDS
+//                      and PV on MFMA split across the four compute
+//                      wavefronts by output columns, while four loader
+//                      wavefronts copy the K and V rows of the next tiles into
+//                      LDS (buffer_load ... lds).  Three protocols: matched
+//                      (bf16 p, normalized FP32 partial + LSE), base (FP32 p,
+//                      whole context, bf16 out) and fixed split (FP32 p,
+//                      (m, l, acc) per partition).  D = 64, 128 and 256.
 //   matched_tile       the matched protocol for splits of exactly one tile,
 //                      with PV split across the wavefronts by output columns.
 //   lse_merge          one wavefront per (sequence, query head, 64 columns):
@@ -32,6 +31,7 @@
 #include <cstdint>
 #include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "pd_device.h"
 #include "pd_internal.h"
@@ -44,7 +44,6 @@ template <int D, int GP>
 struct MatchedShared {
   float wmax[2][4][16];  // per-tile maxima, double-buffered by tile parity
   float lsum[4][16];
-  float mfin[16];
   int last;
 };
 
@@ -119,460 +118,6 @@ __device__ __forceinline__ void write_empty_partition(int tid, int b, int Hq, in
   }
 }
 
-template <int D, int GP, bool kFused, int kMode, int kHeads = 1>
-__global__ void __launch_bounds__(kThreads, 2)
-matched_partition_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
-                         const uint16_t* __restrict__ q, int tsb, int width, int order, int T,
-                         int qsb, int qsh, int G, int hs, int Hq, const uint16_t* __restrict__ k,
-                         const uint16_t* __restrict__ v, float* __restrict__ partials,
-                         float* __restrict__ lse_out, int* __restrict__ counters,
-                         uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv,
-                         int splits, float scale, float c) {
-  static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
-  static_assert(D < 256, "D = 256 runs cols_loader_kernel");
-  static_assert(kHeads == 1 || kMode != kMatched, "kv-head groups change the tile of the protocol");
-  static_assert(kHeads == 1 || kHeads == 2, "1 or 2 kv heads per workgroup");
-  using C = Matched<D, GP>;
-  constexpr int TILE = C::kTile;
-  // kHeads = H = 2 (base and fixed-split protocols at D = 64): the
-  // workgroup serves kv heads 2 kh and 2 kh + 1 and their 2 G query heads.
-  // Row R of a tile is token R / 2 of kv head 2 kh + R % 2: the two heads'
-  // rows of a token are 4 D contiguous bytes, so a tile holds TILE / 2
-  // tokens; query head e G + g (e = 0, 1) scores only the rows of its own kv
-  // head (R % 2 = e), and the other rows get probability 0.  A head's D = 64
-  // row is one 128-byte line, Hkv lines apart from the next token's; the
-  // pair reads two adjacent lines per token.
-  constexpr int TTOK = TILE / kHeads;  // tokens per tile
-  __shared__ MatchedShared<D, GP> sm;
-  // V rows of the tile being computed and of the one being loaded; two arrays
-  // (not one) so that the compiler's wait before reading one slot does not
-  // count the copies still in flight into the other.
-  __shared__ __attribute__((aligned(16))) char vs0[4 * C::kSlot];
-  __shared__ __attribute__((aligned(16))) char vs1[4 * C::kSlot];
-  __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
-
-  // The fixed-split protocol walks the whole context of its (kv head,
-  // sequence) in one workgroup (grid.x = 1) and writes the (m, l, acc) of each
-  // T-token partition as the walk leaves it (see flush below).
-  constexpr bool kWalk = kMode == kSplit;
-  const int p = kWalk ? 0 : int(blockIdx.x);
-  const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
-  const int kvh = kHeads * kh;                   // (first) kv head of this workgroup
-  const int qb = kvh * G + 16 * slice;           // first query head of this workgroup
-  const int Gs = min(16, kHeads * G - 16 * slice);  // query heads of this workgroup
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qh = lane & 15, qg = lane >> 4;
-  const int start = p * T;
-  OrderedSequence seq{int(blockIdx.z), 0};
-  if (order >= 0) seq = ordered_sequence(lengths, int(gridDim.z), int(blockIdx.z), order, slens);
-  const int b = seq.b;
-  // The partition's table entries do not depend on the length: fetch them
-  // together with it, so the first KV loads wait for one round trip.
-  PageWindow<2> pw;
-  pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
-  const int length = order >= 0 ? seq.length : lengths[b];
-  const int end = min(kWalk ? splits * T : start + T, length);
-  const int count = end > start ? (end - start + TTOK - 1) / TTOK : 0;
-  if constexpr (!kFused) {
-    if (count == 0) {
-      for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
-        write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
-                                        maxima);
-      return;
-    }
-  }
-  const int64_t RS = int64_t(Hkv) * D;
-
-  // MFMA B operand of QK: the GQA group's query rows.
-  bf16x8_t qf[C::kCH];
-  {
-    const bool live = qh < Gs;
-    const uint16_t* qrow = q + int64_t(b) * qsb + int64_t(qb + (live ? qh : 0)) * qsh + 8 * qg;
-#pragma unroll
-    for (int ch = 0; ch < C::kCH; ++ch)
-      qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
-  }
-
-  // Tile-relative byte offsets: K pieces of this lane, and the source of each
-  // 16-byte LDS piece this lane fills (v_copy_offset); rows past the sequence
-  // end read past the buffer, i.e. zeros.
-  const int koff = (tile_row_elems<D, kHeads>(w * C::kTW + qh, int(RS)) + 8 * qg) * 2;
-  constexpr int kGroupRows = 16 / kHeads;  // tokens of a 16-row group
-  int voff[C::kDma];
-#pragma unroll
-  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, false, kHeads>(i, lane, w, int(RS));
-  // This lane's transposed-read row within its wavefront's LDS rows: row
-  // 4qg + qh/4 of each 16-row group (the row v_read_offset swizzles by).
-  const int trb = w * C::kSlot + (4 * qg + (qh >> 2)) * C::kPitch;
-
-  floatx4_t acc[C::kNB];   // O[head 4*qg + r][16j + qh]
-#pragma unroll
-  for (int j = 0; j < C::kNB; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-  float m4[4];             // running max of heads 4*qg + r
-#pragma unroll
-  for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
-  float m_own = -INFINITY;  // running max of head qh
-  float l_own = 0.f;        // this lane's share of head qh's denominator
-
-  // Loads of tile ti (0 <= ti < count): K rows into registers, V rows into LDS.
-  auto issue_k = [&](KTile<D, GP>& R, int ti) __attribute__((always_inline)) {
-    const int t0 = start + ti * TTOK;
-    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kvh, D);
-#pragma unroll
-    for (int g = 0; g < C::kNG; ++g)
-#pragma unroll
-      for (int ch = 0; ch < C::kCH; ++ch)
-        R.k[g][ch] = buffer_load16(buf.k, koff + g * kGroupRows * int(RS) * 2 + 64 * ch);
-  };
-  auto issue_v = [&](char* slot, int ti) __attribute__((always_inline)) {
-    const int t0 = start + ti * TTOK;
-    const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kvh, D);
-#pragma unroll
-    for (int i = 0; i < C::kDma; ++i)
-      lds_copy16(buf.v, slot + w * C::kSlot + 1024 * i, voff[i]);
-  };
-
-  // first: ti == count - 1, the first tile walked; acc is still zero there,
-  // so its rescale by alpha (0 for a running max of -inf) is skipped.
-  // knext >= 0: once the QK products have read R, R is refilled with the K
-  // rows of tile knext (two tiles ahead of ti in the walk).
-  auto process = [&](KTile<D, GP>& R, const char* slot, int ti, bool first, int knext)
-                     __attribute__((always_inline)) {
-    const int nvalid = end - (start + ti * TTOK);
-    // ---- scores
-    floatx4_t s[C::kNG];
-#pragma unroll
-    for (int g = 0; g < C::kNG; ++g) {
-      s[g] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ch = 0; ch < C::kCH; ++ch)
-        s[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, R.k[g][ch]),
-                                                        qf[ch], s[g], 0, 0, 0);
-    }
-    if (knext >= 0) {
-      // After every QK product has been issued, so the refill reuses R's
-      // registers instead of keeping two generations of K live.
-      __builtin_amdgcn_sched_barrier(0);
-      issue_k(R, knext);
-    }
-    mfma_result_barrier(s);
-    if constexpr (kMode != kMatched) {
-      // Scores in the reference's units: dot(q, k) * SCALE (kernels.py:30).
-#pragma unroll
-      for (int g = 0; g < C::kNG; ++g)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s[g][r] *= scale;
-    }
-    if constexpr (kHeads > 1) {
-      // Rows of the other kv heads (R % H = r % H), and tokens past the end;
-      // padding query lanes (qh >= H G) take the last head's rows.
-      const int e = min(qh / G, kHeads - 1);
-#pragma unroll
-      for (int g = 0; g < C::kNG; ++g)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (r % kHeads != e || (w * C::kTW + 16 * g + 4 * qg + r) / kHeads >= nvalid)
-            s[g][r] = -INFINITY;
-    } else if (nvalid < TILE) {
-#pragma unroll
-      for (int g = 0; g < C::kNG; ++g)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (w * C::kTW + 16 * g + 4 * qg + r >= nvalid) s[g][r] = -INFINITY;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int g = 0; g < C::kNG; ++g)
-      mx = fmaxf(fmaxf(mx, fmaxf(s[g][0], s[g][1])), fmaxf(s[g][2], s[g][3]));
-    mx = max_rows(mx);
-    float (*wm)[16] = sm.wmax[ti & 1];
-    if (lane < 16) wm[w][lane] = mx;
-    lds_barrier();
-    // ---- running maxima (reference order: m' = max(m, rowmax s))
-    float alpha[4];
-    bool moved = false;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * qg + r;
-      const float tm = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
-      const float mn = fmaxf(m4[r], tm);
-      moved |= mn != m4[r];
-      alpha[r] = kMode == kMatched ? exp2_fast((m4[r] - mn) * c) : exp_fast(m4[r] - mn);
-      m4[r] = mn;
-    }
-    const float tm = fmaxf(fmaxf(wm[0][qh], wm[1][qh]), fmaxf(wm[2][qh], wm[3][qh]));
-    const float mn = fmaxf(m_own, tm);
-    const float a_own = kMode == kMatched ? exp2_fast((m_own - mn) * c) : exp_fast(m_own - mn);
-    m_own = mn;
-    const float neg_mc = -(mn * c);
-    float psum = 0.f;
-    // PV A operand: bf16 probabilities (matched), or the three bf16 terms of
-    // the FP32 probabilities (base / split), lo first.
-    constexpr int kTerms = kMode == kMatched ? 1 : 3;
-    uint32_t pb[kTerms][C::kNG][2];
-#pragma unroll
-    for (int g = 0; g < C::kNG; ++g) {
-      float pr[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pr[r] = kMode == kMatched ? exp2_fast(fmaf(s[g][r], c, neg_mc)) : exp_fast(s[g][r] - mn);
-        psum += pr[r];
-      }
-      if constexpr (kMode == kMatched) {
-        pb[0][g][0] = qh < Gs ? pack_bf16(pr[0], pr[1]) : 0u;
-        pb[0][g][1] = qh < Gs ? pack_bf16(pr[2], pr[3]) : 0u;
-      } else {
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const uint32_t hi = pack_bf16(pr[2 * h2], pr[2 * h2 + 1]);
-          const float r0 = pr[2 * h2] - bf16_lo(hi), r1 = pr[2 * h2 + 1] - bf16_hi(hi);
-          const uint32_t mid = pack_bf16(r0, r1);
-          const uint32_t lo = pack_bf16(r0 - bf16_lo(mid), r1 - bf16_hi(mid));
-          pb[0][g][h2] = qh < Gs ? lo : 0u;
-          pb[1][g][h2] = qh < Gs ? mid : 0u;
-          pb[2][g][h2] = qh < Gs ? hi : 0u;
-        }
-      }
-    }
-    l_own = l_own * a_own + psum;
-    // ---- PV (rescale only when a running maximum moved; alpha = 1 otherwise)
-    if (!first && __builtin_amdgcn_ballot_w64(moved)) {
-#pragma unroll
-      for (int j = 0; j < C::kNB; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
-    }
-    const char* base = slot + trb;
-    static_assert(C::kNG % 2 == 0, "16-token groups in pairs");
-#pragma unroll
-    for (int g = 0; g < C::kNG; g += 2) {
-#pragma unroll
-      for (int j = 0; j < C::kNB; ++j) {
-        const int col = v_read_offset<D, false>(16 * j, lane, 4 * qg + (qh >> 2));
-        const short4_t lo = lds_read_tr(base + 16 * g * C::kPitch + col);
-        const short4_t hi = lds_read_tr(base + 16 * (g + 1) * C::kPitch + col);
-        const bf16x8_t bv = __builtin_bit_cast(
-            bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo)[0], __builtin_bit_cast(u32x2_t, lo)[1],
-                              __builtin_bit_cast(u32x2_t, hi)[0], __builtin_bit_cast(u32x2_t, hi)[1]});
-#pragma unroll
-        for (int t = 0; t < kTerms; ++t) {
-          const bf16x8_t a = __builtin_bit_cast(
-              bf16x8_t, u32x4_t{pb[t][g][0], pb[t][g][1], pb[t][g + 1][0], pb[t][g + 1][1]});
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
-        }
-      }
-    }
-  };
-
-  // O of wavefront w as 16-byte slots: slot (q, j, n) holds the four heads
-  // 4q .. 4q+3 of column 16j + n, i.e. lane 16q + n's acc[j] as it is (one
-  // ds_write_b128 per column block).  Only the row groups q < NQ hold real
-  // heads.
-  constexpr int NQ = GP >= 4 ? GP / 4 : 1;
-  constexpr int kSlots = NQ * C::kNB * 16;
-  static_assert(kSlots * 16 <= C::kSlot, "a wavefront's O fits its V rows");
-
-  // kWalk: after tile ti, the first tile of partition ti / tpp, that
-  // partition is complete.  Each wavefront has read its own V rows of tile ti
-  // (in `slot`), and the next copies into that slot are issued only after
-  // this, so its rows there hold its O; thread t then sums slot t over the
-  // waves (the epilogue's fixed order), the partition's (m, l, acc) are stored
-  // (kernels.py:77-80), and the running state restarts for the partition
-  // before it.  Copies and loads of the next tiles stay in flight.
-  const int tpp = T / TTOK;
-  auto flush = [&](char* slot, int ti) __attribute__((always_inline)) {
-    if (ti % tpp) return;
-    const int part = ti / tpp;
-    const float l = sum_rows(l_own);
-    if (lane < 16) sm.lsum[w][lane] = l;
-    if (tid < 16) sm.mfin[tid] = m_own;
-    if (qg < NQ) {
-      floatx4_t* mine = reinterpret_cast<floatx4_t*>(slot + w * C::kSlot) + qg * C::kNB * 16 + qh;
-#pragma unroll
-      for (int j = 0; j < C::kNB; ++j) mine[16 * j] = acc[j];
-    }
-    lds_barrier();
-    for (int sl = tid; sl < kSlots; sl += kThreads) {
-      const int q = sl / (C::kNB * 16), col = sl % (C::kNB * 16);
-      const floatx4_t* o = reinterpret_cast<const floatx4_t*>(slot) + sl;
-      constexpr int kW = C::kSlot / 16;  // floatx4 per wavefront's rows
-      const floatx4_t o0 = o[0], o1 = o[kW], o2 = o[2 * kW], o3 = o[3 * kW];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int h = 4 * q + r;
-        if (h >= Gs) break;
-        const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + part;
-        partials[orow * D + col] = (o0[r] + o1[r]) + (o2[r] + o3[r]);
-        if (col == 0) {
-          maxima[orow] = sm.mfin[h];
-          lse_out[orow] = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
-        }
-      }
-    }
-    lds_barrier();  // every read of the slot is done before copies refill it
-#pragma unroll
-    for (int j = 0; j < C::kNB; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
-    m_own = -INFINITY;
-    l_own = 0.f;
-  };
-  auto step = [&](KTile<D, GP>& R, char* slot, int ti, bool first, int knext)
-                  __attribute__((always_inline)) {
-    process(R, slot, ti, first, knext);
-    if constexpr (kWalk) flush(slot, ti);
-  };
-
-  // Reverse tile walk (matched_splitkv.py:71): last tile first.  Two register
-  // sets and two LDS slots alternate.  V rows are loaded one tile ahead, into
-  // the LDS slot the previous tile's PV has finished reading; K rows two tiles
-  // ahead, into the register set whose QK products have just been issued.
-  // The loop handles tiles in pairs and the last ones are peeled, so no load
-  // is issued past tile 0 (an issue takes the CU's load path for as long as a
-  // real one).
-  pw.settle();
-  if (count == 1) {
-    KTile<D, GP> A;
-    issue_k(A, 0);
-    issue_v(vs0, 0);
-    step(A, vs0, 0, true, -1);
-  } else if (count > 1) {
-    KTile<D, GP> A, B;
-    int ti = count - 1;
-    issue_k(A, ti);
-    issue_v(vs0, ti);
-    issue_k(B, ti - 1);
-    bool first = true;
-    while (ti >= 3) {
-      issue_v(vs1, ti - 1);
-      step(A, vs0, ti, first, ti - 2);
-      issue_v(vs0, ti - 2);
-      step(B, vs1, ti - 1, false, ti - 3);
-      ti -= 2;
-      first = false;
-    }
-    if (ti == 2) {
-      issue_v(vs1, 1);
-      step(A, vs0, 2, first, 0);
-      issue_v(vs0, 0);
-      step(B, vs1, 1, false, -1);
-      step(A, vs0, 0, false, -1);
-    } else {  // ti == 1
-      issue_v(vs1, 0);
-      step(A, vs0, 1, first, -1);
-      step(B, vs1, 0, false, -1);
-    }
-  }
-
-  if constexpr (kWalk) {
-    // Partitions past the sequence's last token are empty.
-    for (int pp = (end + T - 1) / T; pp < splits; ++pp)
-      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
-                                      maxima);
-    return;
-  }
-
-  // ---- epilogue: combine the 4 waves' accumulators and denominators
-  const float l = sum_rows(l_own);
-  if (lane < 16) sm.lsum[w][lane] = l;
-  if (tid < 16) sm.mfin[tid] = m_own;
-  __syncthreads();  // every wavefront is done with its V rows (aliased by red)
-  // The slots of wavefronts 0, 1 go to vs0 and those of 2, 3 to vs1.
-  static_assert(2 * kSlots * 16 <= 4 * C::kSlot, "reduction buffer");
-  auto red = [&](int wave) __attribute__((always_inline)) {
-    return reinterpret_cast<floatx4_t*>(wave < 2 ? vs0 : vs1) + (wave & 1) * kSlots;
-  };
-  if (qg < NQ) {
-    floatx4_t* mine = red(w) + qg * C::kNB * 16 + qh;
-#pragma unroll
-    for (int j = 0; j < C::kNB; ++j) mine[16 * j] = acc[j];
-  }
-  lds_barrier();
-
-  // Thread t sums slot t (and t + 256, ...) over the waves in a fixed order
-  // and writes the normalized values of its (up to) four heads; for each head
-  // the threads of a wavefront write consecutive columns.
-  for (int sl = tid; sl < kSlots; sl += kThreads) {
-    const int q = sl / (C::kNB * 16), col = sl % (C::kNB * 16);
-    const floatx4_t o0 = red(0)[sl], o1 = red(1)[sl], o2 = red(2)[sl], o3 = red(3)[sl];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * q + r;
-      if (h >= Gs) break;
-      const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
-      const float safe = den > 0.f ? den : 1.f;
-      const float num = (o0[r] + o1[r]) + (o2[r] + o3[r]);
-      const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
-      if constexpr (kMode == kBase) {
-        // acc / denom, 0 for an empty sequence (kernels.py:40).
-        out[(int64_t(b) * Hq + qb + h) * D + col] = uint16_t(bf16_bits(num / safe));
-        continue;
-      } else if constexpr (kMode == kSplit) {
-        partials[orow * D + col] = num;
-        if (col == 0) {
-          maxima[orow] = sm.mfin[h];
-          lse_out[orow] = den;
-        }
-        continue;
-      }
-      const float val = num * rcp_fast(safe);
-      const float lv = den > 0.f ? fmaf(sm.mfin[h], scale, ln_fast(safe)) : -INFINITY;
-      if constexpr (kFused) {
-        // Device-scope stores (global_store sc1): written through to the
-        // coherence point, so another XCD can read them without any L2 flush.
-        __hip_atomic_store(partials + orow * D + col, val, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        if (col == 0)
-          __hip_atomic_store(lse_out + orow, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-        partials[orow * D + col] = val;
-        if (col == 0) lse_out[orow] = lv;
-      }
-    }
-  }
-
-  if constexpr (kFused) {
-    // Split-completion count.  Every partial and LSE value exchanged between
-    // workgroups is written and read with device-scope (sc1) accesses.  Each
-    // wavefront waits until its own stores have completed (vmcnt(0): written
-    // through to the coherence point), then the barrier orders all four
-    // wavefronts' completed stores before thread 0 increments the counter.
-    // The last workgroup issues its loads only after its increment returned
-    // splits - 1, i.e. after every other workgroup's stores completed, and
-    // those loads are device-scope, so they are served from the coherence
-    // point rather than from a line this XCD's caches may hold from an
-    // earlier call.  No cache-wide writeback or invalidate is needed, so the
-    // KV tiles other calls keep in L2 stay resident.
-    int* counter = counters + (int64_t(b) * Hkv + kh) * kCountersPerGroup;  // the first slot
-    wait_memory();
-    __syncthreads();
-    if (tid == 0)
-      sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                splits - 1;
-    __syncthreads();
-    if (!sm.last) return;
-    // Wavefront w merges query heads w, w + 4, ... of the group; lane owns
-    // D/64 consecutive columns, as in lse_merge_kernel's wavefronts.
-    const int64_t row0 = int64_t(b) * Hq + kh * G;  // first query head of the group
-    constexpr int kV = D / 64;
-    for (int hh = __builtin_amdgcn_readfirstlane(w); hh < G; hh += 4) {
-      float w0 = 0.f, w1 = 0.f, acc[kV];
-      merge_splits<kV, kCoherentAux>(
-          partials + (row0 + hh) * splits * D, D, lane * kV, splits,
-          [&] {
-            lse_weights<kCoherentAux>(lse_out + (row0 + hh) * splits, splits, plan_lse_lanes(splits, D),
-                              lane, w0, w1);
-          },
-          [&](int s0, int j) { return wave_weight(w0, w1, s0 + j); }, acc);
-      uint16_t* dst = out + (row0 + hh) * D + lane * kV;
-#pragma unroll
-      for (int e = 0; e < kV; ++e) dst[e] = uint16_t(bf16_bits(acc[e]));
-    }
-    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
 template <int D>
 struct TileP {
   static constexpr int kTile = 16384 / D;
@@ -584,20 +129,30 @@ struct TileP {
   static constexpr int kKS = kTile / 32;     // 32-token k-steps of PV
 };
 
-// P V of one 64-token tile at D = 256 for wavefront w's output columns
-// [64w, 64w + 64), accumulated into acc (O[head 4(L/16) + r][64w + 16j + L%16]
-// in lane L, element r of acc[j]): k-step ks covers tokens 32ks .. 32ks + 31;
-// lane L supplies k = 8(L/16) + e <-> token 32ks + 8(L/16) + e for both
-// operands (as in matched_tile_kernel).  The probabilities are in `ps`, one
-// 16-row LDS tile per bf16 term; the V rows in `slot`, each wavefront's 16
-// rows in a kSlot part of their own, pieces permuted by vswz.
-template <int GP, int kTerms>
-__device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<256>::kNBW],
-                                             const char (*ps)[16 * TileP<256>::kPitch],
+// f(integral_constant<int, K>) for K = KS... in order.
+template <typename F, int... KS>
+__device__ __forceinline__ void for_each_step(F&& f, std::integer_sequence<int, KS...>) {
+  (f(std::integral_constant<int, KS>{}), ...);
+}
+
+// P V of one tile for wavefront w's output columns [w D/4, (w + 1) D/4),
+// accumulated into acc (O[head 4(L/16) + r][w D/4 + 16j + L%16] in lane L,
+// element r of acc[j]): k-step ks covers tile rows 32ks .. 32ks + 31; lane L
+// supplies k = 8(L/16) + e <-> row 32ks + 8(L/16) + e for both operands (as in
+// matched_tile_kernel).  The probabilities are in `ps`, one 16-row LDS tile
+// per bf16 term; the V rows in `slot`, wavefront x's kTW rows in a kSlot part
+// of their own, pieces permuted by vswz.
+template <int D, int GP, int kTerms>
+__device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<D>::kNBW],
+                                             const char (*ps)[16 * TileP<D>::kPitch],
                                              const char* slot, int lane, int w) {
-  using C = Matched<256, GP>;
-  using P = TileP<256>;
+  using C = Matched<D, GP>;
+  using P = TileP<D>;
   const int qh = lane & 15, qg = lane >> 4;
+  // Row u = 8qg + qh/4 of a k-step (lo; hi is u + 4), and its place in the
+  // slot: wavefront part u / kTW, row u % kTW (u + 4 stays in the same part).
+  const int u = 8 * qg + (qh >> 2);
+  const uint32_t vb = lds_address(slot) + (u / C::kTW) * C::kSlot + (u % C::kTW) * C::kPitch;
   auto pv_step = [&](auto KS) __attribute__((always_inline)) {
     constexpr int ks = decltype(KS)::value;
     bf16x8_t a[kTerms];
@@ -608,20 +163,15 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<256>::kNBW],
       const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(prow + 8);
       a[t] = __builtin_bit_cast(bf16x8_t, u32x4_t{a0[0], a0[1], a1[0], a1[1]});
     }
-    // V rows 32ks + 8qg + (qh >> 2) (lo) and + 4 (hi): row t of the tile
-    // is row t % 16 of wavefront t / 16's slot part; columns 64w + 16j.
     // The transposed reads are issued from inline asm (lds_read_tr_at): the
     // compiler then adds no vmcnt wait of its own for the LDS copies it
     // cannot tell apart from this slot's (the caller's wait covers them), and
     // lds_settle makes the results wait for the reads.
-    const uint32_t vb = lds_address(slot) + (qg >> 1) * C::kSlot +
-                        (8 * (qg & 1) + (qh >> 2)) * C::kPitch;
-    constexpr int kOff = ks * 2 * C::kSlot;
+    constexpr int kOff = (32 * ks / C::kTW) * C::kSlot + (32 * ks % C::kTW) * C::kPitch;
     short4_t lo[P::kNBW], hi[P::kNBW];
 #pragma unroll
     for (int j = 0; j < P::kNBW; ++j) {
-      const uint32_t vj =
-          vb + v_read_offset<256, true>(w * P::kCols + 16 * j, lane, 8 * (qg & 1) + (qh >> 2));
+      const uint32_t vj = vb + v_read_offset<D>(w * P::kCols + 16 * j, lane, u % 16);
       lo[j] = lds_read_tr_at<kOff>(vj);
       hi[j] = lds_read_tr_at<kOff + 4 * C::kPitch>(vj);
     }
@@ -636,19 +186,22 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<256>::kNBW],
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], bv, acc[j], 0, 0, 0);
     }
   };
-  pv_step(std::integral_constant<int, 0>{});
-  pv_step(std::integral_constant<int, 1>{});
+  for_each_step(pv_step, std::make_integer_sequence<int, P::kKS>{});
 }
 
-// ------------------------------------- D = 256: P V by columns, loader waves
-// The partition for D = 256: the same three protocols as
-// matched_partition_kernel and the same scores, maxima, probabilities and
-// denominators (so the same LSEs), with the P V product split by output
-// columns as in matched_tile_kernel: per tile, every compute wavefront writes
-// its bf16 probabilities (three bf16 terms for the base and fixed-split
-// protocols) to LDS, and compute wavefront w multiplies the whole tile's P by
-// V columns [64w, 64w + 64) (pv_tile_cols).  The accumulator takes 16 VGPRs,
-// and O needs no cross-wave reduction at the end.
+// --------------------------------------- multi-tile partition, loader waves
+// The partition of every multi-tile plan, for the three protocols (kMode):
+// scores on MFMA, the running maxima and denominators of the FP32 online
+// softmax, and the P V product split by output columns as in
+// matched_tile_kernel: per tile, every compute wavefront writes its bf16
+// probabilities (three bf16 terms for the base and fixed-split protocols) to
+// LDS, and compute wavefront w multiplies the whole tile's P by V columns
+// [w D/4, (w + 1) D/4) (pv_tile_cols).  The accumulator takes D/16 VGPRs, and
+// O needs no cross-wave reduction at the end.  At D = 64, kHeads = 2 serves
+// two adjacent kv heads (base and fixed-split protocols): row R of a tile is
+// token R / 2 of kv head 2 kh + R % 2, a token's two rows one contiguous
+// 256-byte read; query head e G + g scores only the rows of its own kv head
+// (R % 2 = e), and the other rows get probability 0.
 //
 // Eight wavefronts: four compute and four only copy K and V rows into LDS
 // (buffer_load ... lds).  The LDS below allows one workgroup per CU, so each
@@ -657,16 +210,18 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<256>::kNBW],
 // 64 KiB per tile), so here the loader wavefronts stand still instead, and the
 // compute wavefronts issue no global load after the query.  (Four wavefronts
 // that loaded for themselves, K two tiles ahead into registers and V into
-// LDS, at two workgroups per CU, took 1.17-1.40x the time on few long
-// partitions and 1.02-1.06x on full grids; the outputs are the same bits.)
+// LDS, at two workgroups per CU, took 1.17-1.40x the time at D = 256 on few
+// long partitions, 1.02-1.06x on full grids, and 1.02-1.04x at D = 64 and
+// 128 on full grids.)
 //
-// LDS: two K and two V stages of 32 KiB; tile t uses stage t & 1.  K row r of
-// a stage holds its 16-byte piece p at position p ^ (r & 15): the 16 rows of a
-// compute wavefront's ds_read_b128 (one piece each) then fall on 16 distinct
-// 16-byte bank groups, and each loader copy (1 KiB, two rows, every eight
-// consecutive lanes one 128-byte line) writes one contiguous KiB.  Compute
-// wavefront w's V rows (tokens 16w .. 16w + 15) are loader w's kSlot part of
-// a V stage, pieces permuted by vswz.
+// LDS: two K and two V stages of 32 KiB (a tile is 16384 / D rows of 2D
+// bytes); tile t uses stage t & 1.  K row r of a stage holds its 16-byte
+// piece p at position p ^ kswz(r), so the 16 rows of a compute wavefront's
+// ds_read_b128 (one piece each) fall on 16 distinct 16-byte bank groups, and
+// each loader copy (1 KiB, every eight consecutive lanes one 128-byte line)
+// writes one contiguous KiB.  Compute wavefront w's V rows (tile rows kTW w ..
+// kTW w + kTW - 1) are loader w's kSlot part of a V stage, pieces permuted by
+// vswz.
 //
 // Schedule, tile t (last to first), around the compute wavefronts' barriers:
 //   B1(t)  after QK(t) and the tile maxima.  V stage (t + 1) & 1 is free (P V
@@ -683,7 +238,7 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<256>::kNBW],
 // barriers: B0, B1 and B2 of every tile, the fixed-split walk's barrier after
 // each partition it completes, the one before the epilogue and the fused
 // split count's two.
-template <int GP, bool kFused, int kMode>
+template <int D, int GP, bool kFused, int kMode, int kHeads = 1>
 __global__ void __launch_bounds__(2 * kThreads, 1)
 cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
                    const uint16_t* __restrict__ q, int tsb, int width, int order, int T, int qsb,
@@ -693,15 +248,18 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
                    uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv, int splits,
                    float scale, float c) {
   static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
-  constexpr int D = 256;
+  static_assert(kHeads == 1 || kMode != kMatched, "kv-head groups change the tile of the protocol");
+  static_assert(kHeads == 1 || (kHeads == 2 && D == 64), "kv-head pairs at D = 64 only");
   using C = Matched<D, GP>;
   using P = TileP<D>;
-  constexpr int TILE = C::kTile;
+  constexpr int TILE = C::kTile;        // tile rows: TILE / kHeads tokens of kHeads kv heads
+  constexpr int TTOK = TILE / kHeads;   // tokens per tile
   constexpr int kTerms = kMode == kMatched ? 1 : 3;
   constexpr int kStage = TILE * D * 2;  // bytes of one K or V stage
   constexpr int kCopies = C::kDma;      // 1 KiB copies per loader, tensor and tile
-  static_assert(C::kNG == 1 && C::kTW == 16 && 4 * C::kSlot == kStage && 4 * 1024 * kCopies == kStage,
-                "D = 256 geometry");
+  constexpr int kPieces = D / 8;        // 16-byte pieces per K row
+  static_assert(4 * C::kSlot == kStage && 4 * 1024 * kCopies == kStage && C::kNG * C::kCH == 8,
+                "tile geometry");
   __shared__ MatchedShared<D, GP> sm;
   __shared__ __attribute__((aligned(16))) char ks[2][kStage];
   __shared__ __attribute__((aligned(16))) char vs[2][kStage];
@@ -715,8 +273,9 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   constexpr bool kWalk = kMode == kSplit;
   const int p = kWalk ? 0 : int(blockIdx.x);
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
-  const int qb = kh * G + 16 * slice;
-  const int Gs = min(16, G - 16 * slice);
+  const int kvh = kHeads * kh;                      // (first) kv head of this workgroup
+  const int qb = kvh * G + 16 * slice;              // first query head of this workgroup
+  const int Gs = min(16, kHeads * G - 16 * slice);  // query heads of this workgroup
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool loader = wv >= 4;
@@ -730,25 +289,27 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   if (loader) pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
   const int length = order >= 0 ? seq.length : lengths[b];
   const int end = min(kWalk ? splits * T : start + T, length);
-  const int count = end > start ? (end - start + TILE - 1) / TILE : 0;
-  const int tpp = T / TILE;  // tiles per partition of the walk
+  const int count = end > start ? (end - start + TTOK - 1) / TTOK : 0;
+  const int tpp = T / TTOK;  // tiles per partition of the walk
   const int64_t RS = int64_t(Hkv) * D;
 
   if (loader) {
     if (!kFused && count == 0) return;
-    // Copy i of loader w fills rows 2(8w + i) and 2(8w + i) + 1 of K, pieces
-    // in position order, and of V the rows of compute wavefront w.
+    // Copy i of loader w fills KiB 8w + i of the K stage, pieces in position
+    // order (piece p of row r at position p ^ kswz(r)), and of V the rows of
+    // compute wavefront w.
     int koff[kCopies], voff[kCopies];
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) {
-      const int row = 2 * (kCopies * w + i) + (lane >> 5);
-      koff[i] = (row * int(RS) + 8 * ((lane & 31) ^ (row & 15))) * 2;
-      voff[i] = v_copy_offset<D, GP, true>(i, lane, w, int(RS));
+      const int pos = 64 * (kCopies * w + i) + lane;
+      const int row = pos / kPieces;
+      koff[i] = (tile_row_elems<D, kHeads>(row, int(RS)) + 8 * ((pos % kPieces) ^ kswz<D>(row))) * 2;
+      voff[i] = v_copy_offset<D, GP, kHeads>(i, lane, w, int(RS));
     }
     pw.settle();
     auto issue = [&](int ti, bool is_k) __attribute__((always_inline)) {
-      const int t0 = start + ti * TILE;
-      const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kh, D);
+      const int t0 = start + ti * TTOK;
+      const TileBuffers buf = tile_buffers(k, v, pw.page(t0), t0, end, RS, kvh, D);
       char* dst = (is_k ? ks[ti & 1] : vs[ti & 1]) + w * kCopies * 1024;
 #pragma unroll
       for (int i = 0; i < kCopies; ++i)
@@ -799,18 +360,24 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     for (int ch = 0; ch < C::kCH; ++ch)
       qf[ch] = __builtin_bit_cast(bf16x8_t, live ? load16(qrow + 32 * ch) : u32x4_t{0, 0, 0, 0});
   }
-  // Lane (qh, qg) reads piece qg + 4ch of K row 16w + qh for k-chunk ch; a
-  // tile's reads are issued once its rows are in LDS (after P V of the tile
-  // before it) and waited for before its QK products.
-  uint32_t kaddr[C::kCH];
+  // Lane (qh, qg) reads piece qg + 4ch of K row kTW w + 16g + qh for 16-row
+  // group g and k-chunk ch; a tile's reads are issued once its rows are in
+  // LDS (after P V of the tile before it) and waited for before its QK
+  // products.
+  uint32_t kaddr[C::kNG * C::kCH];
 #pragma unroll
-  for (int ch = 0; ch < C::kCH; ++ch)
-    kaddr[ch] = lds_address(ks[0]) + (16 * w + qh) * (2 * D) + (((qg + 4 * ch) ^ qh) * 16);
-  u32x4_t kr[C::kCH];
+  for (int g = 0; g < C::kNG; ++g) {
+    const int row = w * C::kTW + 16 * g + qh;
+#pragma unroll
+    for (int ch = 0; ch < C::kCH; ++ch)
+      kaddr[g * C::kCH + ch] =
+          lds_address(ks[0]) + row * (2 * D) + (((qg + 4 * ch) ^ kswz<D>(row)) * 16);
+  }
+  u32x4_t kr[C::kNG * C::kCH];
   auto read_k = [&](int ti) __attribute__((always_inline)) {
     const uint32_t stage = (ti & 1) * kStage;
 #pragma unroll
-    for (int ch = 0; ch < C::kCH; ++ch) kr[ch] = lds_read16_at(kaddr[ch] + stage);
+    for (int i = 0; i < C::kNG * C::kCH; ++i) kr[i] = lds_read16_at(kaddr[i] + stage);
   };
 
   floatx4_t acc[P::kNBW];  // O[head 4*qg + r][64w + 16j + qh]
@@ -828,24 +395,46 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   }
   for (int ti = count - 1; ti >= 0; --ti) {
     // ---- scores and the tile maxima
-    const int nvalid = end - (start + ti * TILE);
+    const int nvalid = end - (start + ti * TTOK);
     lds_wait(kr);
-    floatx4_t s[1] = {floatx4_t{0.f, 0.f, 0.f, 0.f}};
+    floatx4_t s[C::kNG];
 #pragma unroll
-    for (int ch = 0; ch < C::kCH; ++ch)
-      s[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[ch]), qf[ch],
-                                                      s[0], 0, 0, 0);
+    for (int g = 0; g < C::kNG; ++g) {
+      s[g] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ch = 0; ch < C::kCH; ++ch)
+        s[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, kr[g * C::kCH + ch]), qf[ch], s[g], 0, 0, 0);
+    }
     mfma_result_barrier(s);
     if constexpr (kMode != kMatched) {
+      // Scores in the reference's units: dot(q, k) * SCALE (kernels.py:30).
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[0][r] *= scale;
-    }
-    if (nvalid < TILE) {
+      for (int g = 0; g < C::kNG; ++g)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (w * C::kTW + 4 * qg + r >= nvalid) s[0][r] = -INFINITY;
+        for (int r = 0; r < 4; ++r) s[g][r] *= scale;
     }
-    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+    if constexpr (kHeads > 1) {
+      // Rows of the other kv head (R % 2 = r % 2), and tokens past the end;
+      // padding query lanes (qh >= 2 G) take the last head's rows.
+      const int e = min(qh / G, kHeads - 1);
+#pragma unroll
+      for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (r % kHeads != e || (w * C::kTW + 16 * g + 4 * qg + r) / kHeads >= nvalid)
+            s[g][r] = -INFINITY;
+    } else if (nvalid < TILE) {
+#pragma unroll
+      for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (w * C::kTW + 16 * g + 4 * qg + r >= nvalid) s[g][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < C::kNG; ++g)
+      mx = fmaxf(fmaxf(mx, fmaxf(s[g][0], s[g][1])), fmaxf(s[g][2], s[g][3]));
     mx = max_rows(mx);
     float (*wm)[16] = sm.wmax[ti & 1];
     if (lane < 16) wm[w][lane] = mx;
@@ -870,30 +459,36 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     m_own = mn;
     const float neg_mc = -(mn * c);
     float psum = 0.f;
-    float pr[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      pr[r] = kMode == kMatched ? exp2_fast(fmaf(s[0][r], c, neg_mc)) : exp_fast(s[0][r] - mn);
-      psum += pr[r];
-    }
-    const int pofs = qh * P::kPitch + (w * C::kTW + 4 * qg) * 2;
-    if constexpr (kMode == kMatched) {
-      *reinterpret_cast<u32x2_t*>(ps[0] + pofs) =
-          u32x2_t{qh < Gs ? pack_bf16(pr[0], pr[1]) : 0u, qh < Gs ? pack_bf16(pr[2], pr[3]) : 0u};
-    } else {
-      uint32_t t3[3][2];
+    for (int g = 0; g < C::kNG; ++g) {
+      float pr[4];
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const uint32_t hi = pack_bf16(pr[2 * h2], pr[2 * h2 + 1]);
-        const float r0 = pr[2 * h2] - bf16_lo(hi), r1 = pr[2 * h2 + 1] - bf16_hi(hi);
-        const uint32_t mid = pack_bf16(r0, r1);
-        const uint32_t lo = pack_bf16(r0 - bf16_lo(mid), r1 - bf16_hi(mid));
-        t3[0][h2] = qh < Gs ? lo : 0u;
-        t3[1][h2] = qh < Gs ? mid : 0u;
-        t3[2][h2] = qh < Gs ? hi : 0u;
+      for (int r = 0; r < 4; ++r) {
+        pr[r] = kMode == kMatched ? exp2_fast(fmaf(s[g][r], c, neg_mc)) : exp_fast(s[g][r] - mn);
+        psum += pr[r];
       }
+      // P[head qh][tile rows kTW w + 16g + 4qg .. +3] into row qh of each
+      // term's LDS tile.
+      const int pofs = qh * P::kPitch + (w * C::kTW + 16 * g + 4 * qg) * 2;
+      if constexpr (kMode == kMatched) {
+        *reinterpret_cast<u32x2_t*>(ps[0] + pofs) =
+            u32x2_t{qh < Gs ? pack_bf16(pr[0], pr[1]) : 0u, qh < Gs ? pack_bf16(pr[2], pr[3]) : 0u};
+      } else {
+        uint32_t t3[3][2];
 #pragma unroll
-      for (int t = 0; t < 3; ++t) *reinterpret_cast<u32x2_t*>(ps[t] + pofs) = u32x2_t{t3[t][0], t3[t][1]};
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const uint32_t hi = pack_bf16(pr[2 * h2], pr[2 * h2 + 1]);
+          const float r0 = pr[2 * h2] - bf16_lo(hi), r1 = pr[2 * h2 + 1] - bf16_hi(hi);
+          const uint32_t mid = pack_bf16(r0, r1);
+          const uint32_t lo = pack_bf16(r0 - bf16_lo(mid), r1 - bf16_hi(mid));
+          t3[0][h2] = qh < Gs ? lo : 0u;
+          t3[1][h2] = qh < Gs ? mid : 0u;
+          t3[2][h2] = qh < Gs ? hi : 0u;
+        }
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+          *reinterpret_cast<u32x2_t*>(ps[t] + pofs) = u32x2_t{t3[t][0], t3[t][1]};
+      }
     }
     l_own = l_own * a_own + psum;
     if (ti != count - 1 && __builtin_amdgcn_ballot_w64(moved)) {
@@ -903,7 +498,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
         for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
     }
     lds_barrier();  // B2(ti): P rows written, V(ti) and K(ti - 1) in LDS
-    pv_tile_cols<GP, kTerms>(acc, ps, vs[ti & 1], lane, w);
+    pv_tile_cols<D, GP, kTerms>(acc, ps, vs[ti & 1], lane, w);
     if (ti > 0) read_k(ti - 1);
 
     if constexpr (kWalk) {
@@ -970,7 +565,8 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       const float inv = rcp_fast(safe);
       const float lv = den > 0.f ? fmaf(m4[r], scale, ln_fast(safe)) : -INFINITY;
       if constexpr (kFused) {
-        // Device-scope stores (global_store sc1), as in matched_partition_kernel.
+        // Device-scope stores (global_store sc1): written through to the
+        // coherence point, so another XCD can read them without any L2 flush.
 #pragma unroll
         for (int j = 0; j < P::kNBW; ++j)
           __hip_atomic_store(partials + orow * D + col + 16 * j, acc[j][r] * inv, __ATOMIC_RELAXED,
@@ -986,9 +582,20 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   }
 
   if constexpr (kFused) {
-    // Split-completion count and the last workgroup's merge, exactly as in
-    // matched_partition_kernel; the loader wavefronts pass the two barriers
-    // and leave.
+    // Split-completion count.  Every partial and LSE value exchanged between
+    // workgroups is written and read with device-scope (sc1) accesses.  Each
+    // compute wavefront waits until its own stores have completed (vmcnt(0):
+    // written through to the coherence point), then the barrier orders the
+    // four wavefronts' completed stores before thread 0 increments the
+    // counter; the loader wavefronts pass the two barriers and leave.  The
+    // last workgroup issues its loads only after its increment returned
+    // splits - 1, i.e. after every other workgroup's stores completed, and
+    // those loads are device-scope, so they are served from the coherence
+    // point rather than from a line this XCD's caches may hold from an
+    // earlier call.  No cache-wide writeback or invalidate is needed, so the
+    // KV tiles other calls keep in L2 stay resident.  Compute wavefront w
+    // merges query heads w, w + 4, ... of the group; each lane owns D / 64
+    // consecutive columns, as in lse_merge_kernel's wavefronts.
     int* counter = counters + (int64_t(b) * Hkv + kh) * kCountersPerGroup;  // the first slot
     wait_memory();
     __syncthreads();
@@ -1017,7 +624,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 }
 
 // ----------------------------------------------------- single-tile partition
-// The same partial + LSE as matched_partition_kernel for plans whose splits
+// The same partial + LSE as cols_loader_kernel for plans whose splits
 // are exactly one tile (tokens_per_split == 16384 / D: the headline D=256
 // plan of 64-token splits, and every plan of small contexts).  With a single
 // tile there is no running maximum to carry, so the workgroup splits the PV
@@ -1026,9 +633,11 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 // wavefront w then multiplies the whole tile's P by V columns
 // [w*D/4, (w+1)*D/4) on v_mfma_f32_16x16x32_bf16.  That needs one more barrier
 // but no cross-wave reduction of O at the end, and half the PV instructions
-// of the 16-token grouping at D=256.  Scores, maxima, probabilities,
-// denominators and LSEs are bit-identical to matched_partition_kernel's; the
-// partial differs only in the fp32 summation order of P V.
+// of a 16-token grouping at D=256.  With one tile per workgroup there are no
+// later loads to hide, so the four wavefronts load for themselves (no loader
+// wavefronts) and two workgroups share a CU.  Scores, maxima, probabilities,
+// denominators and LSEs are computed as cols_loader_kernel computes them, and
+// P V in the same k-step order.
 //
 // kFused = true also merges, in the same launch, with the work of the merge
 // spread over the column slices the wavefronts already own.  Wavefront w of
@@ -1166,7 +775,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   const int kl = kline_offset(lane, int(RS)) + w * C::kTW * int(RS) * 2;
   int voff[C::kDma];
 #pragma unroll
-  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP, true>(i, lane, w, int(RS));
+  for (int i = 0; i < C::kDma; ++i) voff[i] = v_copy_offset<D, GP>(i, lane, w, int(RS));
 
   KTile<D, GP> R;
   {
@@ -1245,7 +854,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     const char* hi_row = vs + (t_hi / C::kTW) * C::kSlot + (t_hi % C::kTW) * C::kPitch;
 #pragma unroll
     for (int j = 0; j < P::kNBW; ++j) {
-      const int cb = v_read_offset<D, true>(w * P::kCols + 16 * j, lane, 8 * (qg & 1) + (qh >> 2));
+      const int cb = v_read_offset<D>(w * P::kCols + 16 * j, lane, 8 * (qg & 1) + (qh >> 2));
       const short4_t lo = lds_read_tr(lo_row + cb);
       const short4_t hi = lds_read_tr(hi_row + cb);
       const bf16x8_t bv = __builtin_bit_cast(
@@ -1489,28 +1098,22 @@ int xcd_layout() {
 }
 
 // `order` of ordered_sequence (pd_device.h) for a multi-tile launch over
-// `grid` = (splits, kv heads x slices, batch) at `per_cu` workgroups per CU
-// (2 for matched_partition_kernel, 1 for cols_loader_kernel, whose LDS
-// allows no second):
-// * CUs / (grid.x * grid.y) when two workgroups share each CU, the whole grid
-//   is resident and rows z and z + that share CUs;
-// * 0 (longest first) for up to four rounds of workgroups;
+// `grid` = (splits, kv heads x slices, batch), one workgroup per CU:
+// * 0 (longest first) for two to four rounds of workgroups;
 // * -1 (sequence z) when every workgroup has a CU to itself, the batch has one
 //   sequence or more than kMaxOrderedBatch, the CU count is unknown, or the
 //   grid runs more than four rounds.  There the ranking's extra round trip at
 //   the start of every workgroup costs more than the order gains: with 8192
 //   mostly short workgroups (batch 128, lengths up to 4096, D 64, 16 kv heads,
-//   4 fixed partitions) it took the call from 228 to 275 us, and sorting the
-//   batch on the host gained nothing there.
-int batch_order(dim3 grid, int per_cu) {
+//   4 fixed partitions, two workgroups per CU) it took the call from 228 to
+//   275 us, and sorting the batch on the host gained nothing there.
+int batch_order(dim3 grid) {
   const int B = int(grid.z);
   if (B < 2 || B > kMaxOrderedBatch) return -1;
   const int cus = device_cu_count();
   if (cus <= 0) return -1;
-  const int64_t xy = int64_t(grid.x) * grid.y, n = xy * B;
-  if (n <= cus || n > 4 * int64_t(per_cu) * cus) return -1;
-  if (per_cu == 2 && n <= 2 * int64_t(cus) && cus % xy == 0) return int(cus / xy);
-  return 0;
+  const int64_t n = int64_t(grid.x) * grid.y * B;
+  return n <= cus || n > 4 * int64_t(cus) ? -1 : 0;
 }
 
 template <int D, int kFuse>
@@ -1531,30 +1134,11 @@ void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a
 #undef PD_LAUNCH_TILE
 }
 
-// The multi-tile partition at D = 64 and 128 (matched_partition_kernel).
-template <int D, bool kFused, int kMode = kMatched>
-void launch_partition_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
-  static_assert(D < 256, "D = 256 runs cols_loader_kernel");
-#define PD_LAUNCH_GP(GPV)                                                                      \
-  hipLaunchKernelGGL((matched_partition_kernel<D, GPV, kFused, kMode>), grid, dim3(kThreads),   \
-                     0, stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb,   \
-                     a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,   \
-                     a.maxima, a.Hkv, a.splits, a.scale, a.c)
-  switch (gp) {
-    case 1: PD_LAUNCH_GP(1); break;
-    case 2: PD_LAUNCH_GP(2); break;
-    case 4: PD_LAUNCH_GP(4); break;
-    case 8: PD_LAUNCH_GP(8); break;
-    default: PD_LAUNCH_GP(16); break;
-  }
-#undef PD_LAUNCH_GP
-}
-
-// The multi-tile partition at D = 256 (cols_loader_kernel), every protocol.
-template <bool kFused, int kMode>
+// The multi-tile partition with loader wavefronts (cols_loader_kernel).
+template <int D, bool kFused, int kMode, int kHeads = 1>
 void launch_cols_loader(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_LOADER(GPV)                                                                  \
-  hipLaunchKernelGGL((cols_loader_kernel<GPV, kFused, kMode>), grid, dim3(2 * kThreads), 0,     \
+  hipLaunchKernelGGL((cols_loader_kernel<D, GPV, kFused, kMode, kHeads>), grid, dim3(2 * kThreads), 0, \
                      stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb,     \
                      a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,   \
                      a.maxima, a.Hkv, a.splits, a.scale, a.c)
@@ -1566,25 +1150,6 @@ void launch_cols_loader(int gp, dim3 grid, hipStream_t stream, const PartitionAr
     default: PD_LAUNCH_LOADER(16); break;
   }
 #undef PD_LAUNCH_LOADER
-}
-
-// The base and fixed-split protocols at D = 64 with kHeads kv heads per
-// workgroup (matched_partition_kernel's kHeads): gp is the padded size of
-// their query heads, kHeads G <= 16.
-template <int kMode, int kHeads>
-void launch_heads_d64(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
-#define PD_LAUNCH_PAIR(GPV)                                                                    \
-  hipLaunchKernelGGL((matched_partition_kernel<64, GPV, false, kMode, kHeads>), grid,           \
-                     dim3(kThreads), 0, stream, a.table, a.lengths, a.q, a.tsb, a.width,        \
-                     a.order, a.T, a.qsb, a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse,  \
-                     a.counters, a.out, a.maxima, a.Hkv, a.splits, a.scale, a.c)
-  switch (gp) {
-    case 2: PD_LAUNCH_PAIR(2); break;
-    case 4: PD_LAUNCH_PAIR(4); break;
-    case 8: PD_LAUNCH_PAIR(8); break;
-    default: PD_LAUNCH_PAIR(16); break;
-  }
-#undef PD_LAUNCH_PAIR
 }
 
 int padded_group(int g) {
@@ -1675,14 +1240,14 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
     }
     return launch_status(what);
   }
-  a.order = batch_order(grid, head_dim == 256 ? 1 : 2);
+  a.order = batch_order(grid);
   switch (head_dim * 2 + (fused ? 1 : 0)) {
-    case 128: launch_partition_d<64, false>(gp, grid, st, a); break;
-    case 129: launch_partition_d<64, true>(gp, grid, st, a); break;
-    case 256: launch_partition_d<128, false>(gp, grid, st, a); break;
-    case 257: launch_partition_d<128, true>(gp, grid, st, a); break;
-    case 512: launch_cols_loader<false, kMatched>(gp, grid, st, a); break;
-    default: launch_cols_loader<true, kMatched>(gp, grid, st, a); break;
+    case 128: launch_cols_loader<64, false, kMatched>(gp, grid, st, a); break;
+    case 129: launch_cols_loader<64, true, kMatched>(gp, grid, st, a); break;
+    case 256: launch_cols_loader<128, false, kMatched>(gp, grid, st, a); break;
+    case 257: launch_cols_loader<128, true, kMatched>(gp, grid, st, a); break;
+    case 512: launch_cols_loader<256, false, kMatched>(gp, grid, st, a); break;
+    default: launch_cols_loader<256, true, kMatched>(gp, grid, st, a); break;
   }
   return launch_status(what);
 }
@@ -1946,18 +1511,18 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   // 16-head group: a token's two 128-byte rows are one contiguous read.
   const int heads = head_dim != 64 ? 1 : heads_per_workgroup(num_kv_heads, G);
   const dim3 grid(1, heads == 2 ? num_kv_heads / 2 : num_kv_heads * hs, batch);
-  a.order = batch_order(grid, head_dim == 256 ? 1 : 2);
+  a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   constexpr int kMode = kSplitMode ? kSplit : kBase;
   if (heads == 2) {
-    launch_heads_d64<kMode, 2>(padded_group(2 * G), grid, st, a);
+    launch_cols_loader<64, false, kMode, 2>(padded_group(2 * G), grid, st, a);
     return launch_status(what);
   }
   const int gp = padded_group(G < 16 ? G : 16);
   switch (head_dim) {
-    case 64: launch_partition_d<64, false, kMode>(gp, grid, st, a); break;
-    case 128: launch_partition_d<128, false, kMode>(gp, grid, st, a); break;
-    default: launch_cols_loader<false, kMode>(gp, grid, st, a); break;
+    case 64: launch_cols_loader<64, false, kMode>(gp, grid, st, a); break;
+    case 128: launch_cols_loader<128, false, kMode>(gp, grid, st, a); break;
+    default: launch_cols_loader<256, false, kMode>(gp, grid, st, a); break;
   }
   return launch_status(what);
 }

@@ -1,10 +1,9 @@
 """Batch order of the multi-tile kernels, on the GPU.
 
-With more workgroups than CUs, matched_partition_kernel and cols_loader_kernel hand the
-grid's batch rows to the sequences in order of length (ordered_sequence in pd_device.h):
-longest first when the grid runs in two to four rounds, long paired with short on a CU
-when the whole grid is resident at two workgroups per CU (matched_partition_kernel);
-past four rounds the batch keeps its order.  Which workgroup runs an item must not change a bit of the
+With more workgroups than CUs, the multi-tile kernel (cols_loader_kernel, one workgroup
+per CU) hands the grid's batch rows to the sequences in order of length
+(ordered_sequence in pd_device.h): longest first when the grid runs in two to four
+rounds; past four rounds the batch keeps its order.  Which workgroup runs an item must not change a bit of the
 result.  Each case runs a batch large enough to switch the ordering on (the mode named
 is the one a 256-CU device takes) and compares every output row, bit for bit, with the
 same sequence run alone (batch 1, where the order is the identity), under the same plan.
@@ -53,11 +52,11 @@ def _check_rows(full, g, alone):
 
 # (dim, hq, hkv, batch, capacity): mode on 256 CUs for one split per sequence
 MATCHED = [
-    (128, 32, 8, 64, 2048),    # 512 workgroups, resident: rows z and z + 32 paired
-    (128, 8, 8, 48, 2048),     # 384 workgroups: rows 16..31 alone on their CU, 32 paired
+    (128, 32, 8, 64, 2048),    # 512 workgroups, two rounds: longest first
+    (128, 8, 8, 48, 2048),     # 384 workgroups, one and a half rounds: longest first
     (256, 32, 4, 128, 2048),   # 512 workgroups, one per CU (cols_loader_kernel): longest first
-    (64, 16, 16, 128, 1024),   # 2048 workgroups: longest first
-    (128, 8, 8, 256, 512),     # 2048 workgroups, the largest batch that is ranked
+    (64, 16, 16, 128, 1024),   # 2048 workgroups, past four rounds: as given
+    (128, 16, 4, 256, 512),    # 1024 workgroups, the largest batch that is ranked
     (128, 8, 8, 257, 512),     # 2056 workgroups, one sequence too many: as given
 ]
 
@@ -111,7 +110,7 @@ def test_fused_matched_rows_do_not_depend_on_the_batch_order():
     (256, 32, 4, 128, 2048),   # 512 workgroups, one per CU, in two rounds: longest first
     (64, 16, 16, 128, 2048),   # kv-head pairs: 1024 workgroups, longest first
     (64, 32, 8, 64, 2048),     # kv-head pairs of 4-head groups: 256 workgroups, one per CU
-    (128, 32, 8, 40, 2048),    # base: 320 workgroups, rows 8..31 alone on their CU
+    (128, 32, 8, 40, 2048),    # 320 workgroups, one and a quarter rounds: longest first
     (128, 64, 2, 128, 1024),   # 32-head groups in two 16-head slices: 512 workgroups
 ])
 def test_paged_rows_do_not_depend_on_the_batch_order(backend, dim, hq, hkv, batch, capacity):

@@ -111,40 +111,32 @@ def test_operand_layout_loads_touch_half_lines_and_whole_line_loads_whole_ones()
         assert len({line_of(a) for a in operand[start:start + 8]}) == 8
 
 
-def vswz(dim, col_split, row):
+def vswz(dim, row):
     if dim >= 128:
-        return 2 * (row & 3) + 8 * ((row >> (3 if col_split else 2)) & 1)
-    if col_split:
-        return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1))
-    return 2 * ((row >> 1) & 3)
+        return 2 * (row & 3) + 8 * ((row >> 3) & 1)
+    return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1))
 
 
-def v_read_offset(dim, col_split, col0, lane, row):
+def v_read_offset(dim, col0, lane, row):
     b = lane & 3
-    return 16 * (((col0 >> 3) + (b >> 1)) ^ vswz(dim, col_split, row)) + 8 * (b & 1)
+    return 16 * (((col0 >> 3) + (b >> 1)) ^ vswz(dim, row)) + 8 * (b & 1)
 
 
-def read_row(col_split, lane, step, second):
-    """Row (within the wavefront's LDS rows) that `lane` reads in a transposed read:
-    row groups: rows 4(L/16) + (L%16)/4 of 16-row group `step`; column split: rows
-    8(L/16) + (L%16)/4 (+4 in the second read) of 32-token k-step `step`."""
-    c = (lane & 15) >> 2
-    if col_split:
-        return 32 * step + 8 * (lane >> 4) + c + (4 if second else 0)
-    return 16 * step + 4 * (lane >> 4) + c
+def read_row(lane, step, second):
+    """Tile row that `lane` reads in a transposed read of the column-split P V: rows
+    8(L/16) + (L%16)/4 (+4 in the second read) of 32-row k-step `step`."""
+    return 32 * step + 8 * (lane >> 4) + ((lane & 15) >> 2) + (4 if second else 0)
 
 
 @pytest.mark.parametrize("dim", [64, 128, 256])
-@pytest.mark.parametrize("col_split", [False, True])
-def test_v_rows_swizzle_round_trips_and_transposed_reads_are_conflict_free(dim, col_split):
+def test_v_rows_swizzle_round_trips_and_transposed_reads_are_conflict_free(dim):
     """pd_device.h stores V rows in LDS unpadded, 16-byte piece p of row r at position
     p ^ vswz(r) (v_copy_offset), and reads them back with v_read_offset.  Every copy
     lane fills one distinct position and every transposed read finds the logical columns
     it asks for.  The LDS serves 32 lanes of a read per clock over 64 four-byte banks
-    (256 bytes); the 32 lanes of each half-wavefront hit 256 distinct bytes, for the
-    row-group reads of matched_partition_kernel and the column-split reads of the tile
-    and D=256 kernels.  (The previous 4-row swizzle gave 2-way conflicts here, which
-    SQ_LDS_BANK_CONFLICT showed on MI355X.)"""
+    (256 bytes); the 32 lanes of each half-wavefront hit 256 distinct bytes for the
+    column-split reads of the tile and loader kernels.  (A 4-row swizzle gave 2-way
+    conflicts here, which SQ_LDS_BANK_CONFLICT showed on MI355X.)"""
     pieces = dim // 8
     pitch = 16 * pieces
     tile = 16384 // dim
@@ -155,7 +147,7 @@ def test_v_rows_swizzle_round_trips_and_transposed_reads_are_conflict_free(dim, 
         for lane in range(64):
             slot = 64 * i + lane
             row, pos = divmod(slot, pieces)
-            stored[(row, pos)] = (row, pos ^ vswz(dim, col_split, row))
+            stored[(row, pos)] = (row, pos ^ vswz(dim, row))
     assert len(stored) == tw * pieces
     assert sorted(stored.values()) == [(r, p) for r in range(tw) for p in range(pieces)]
 
@@ -163,21 +155,68 @@ def test_v_rows_swizzle_round_trips_and_transposed_reads_are_conflict_free(dim, 
         """Byte address of `row` of the tile: wavefront row // tw's slot, then the row."""
         return (row // tw) * tw * pitch + (row % tw) * pitch
 
-    steps = (tile // 32) if col_split else (tw // 16)
-    for step in range(steps):
-        for second in ((False, True) if col_split else (False,)):
-            cols = range(0, dim, 16)
-            for col0 in cols:
+    for step in range(tile // 32):
+        for second in (False, True):
+            for col0 in range(0, dim, 16):
                 for half in (0, 32):
                     chunks = set()
                     for lane in range(half, half + 32):
-                        row = read_row(col_split, lane, step, second)
-                        local = row % tw if col_split else row
-                        off = v_read_offset(dim, col_split, col0, lane, local % 16)
+                        row = read_row(lane, step, second)
+                        local = row % tw
+                        off = v_read_offset(dim, col0, lane, local % 16)
                         pos, within = divmod(off, 16)
                         b = lane & 3
                         assert stored[(local, pos)] == (local, (col0 + 4 * b) // 8)
                         assert within == 8 * (b & 1)
-                        base = address(row) if col_split else row * pitch
-                        chunks.add(((base + off) % 256) // 8)
+                        chunks.add(((address(row) + off) % 256) // 8)
                     assert len(chunks) == 32, (step, second, col0, half)
+
+
+def kswz(dim, row):
+    return row & 15 if dim >= 128 else (row >> 1) & 7
+
+
+@pytest.mark.parametrize("dim,heads", [(64, 1), (64, 2), (128, 1), (256, 1)])
+def test_loader_k_stage_layout(dim, heads):
+    """cols_loader_kernel's K stage: loader w's copy i (1 KiB, lane l at byte 16 l)
+    fills position 64 (8 w + i) + l, i.e. row pos // (D/8), piece (pos % (D/8)) ^
+    kswz(row), read from global memory at that row's offset; compute wavefront w's lane
+    (qh, qg) reads piece qg + 4 ch of row kTW w + 16 g + qh with one ds_read_b128.
+    Every position is filled once, every read finds its logical piece, the 16 lanes a
+    ds_read_b128 serves per clock (256 bytes over 64 banks) hit 16 distinct 16-byte
+    groups, and every 8 consecutive lanes of a copy read one 128-byte line of K.  With
+    kv-head pairs (D 64) tile row R is token R // 2 of kv head R % 2: a token's two
+    rows are adjacent 128-byte lines."""
+    pieces = dim // 8
+    tile = 16384 // dim
+    tw = tile // 4
+    hkv = 4 if heads == 2 else 1
+    row_stride = hkv * dim * 2                  # bytes between tokens in the pool
+
+    def source(row, piece):
+        return (row // heads) * row_stride + (row % heads) * dim * 2 + 16 * piece
+
+    stage = {}
+    for w in range(4):
+        for i in range(8):
+            lines = []
+            for lane in range(64):
+                pos = 64 * (8 * w + i) + lane
+                row, ph = divmod(pos, pieces)
+                assert (row, ph) not in stage
+                stage[(row, ph)] = ph ^ kswz(dim, row)      # logical piece held there
+                lines.append(source(row, ph ^ kswz(dim, row)) // 128)
+            for start in range(0, 64, 8):
+                assert len(set(lines[start:start + 8])) == 1, (w, i, start)
+    assert len(stage) == tile * pieces
+    for w in range(4):
+        for g in range(tw // 16):
+            for ch in range(dim // 32):
+                for qg in range(4):
+                    banks = set()
+                    for qh in range(16):
+                        row = tw * w + 16 * g + qh
+                        ph = (qg + 4 * ch) ^ kswz(dim, row)
+                        assert stage[(row, ph)] == qg + 4 * ch
+                        banks.add(((row * 2 * dim + 16 * ph) % 256) // 16)
+                    assert len(banks) == 16, (w, g, ch, qg)
