@@ -351,3 +351,26 @@ def test_d256_partials_of_a_sequence_alone_and_in_a_batch(splits, tokens, length
                                                                        lanes)
     np.testing.assert_allclose(to_np(big_lse), lse, atol=2e-5, rtol=1e-6)
     assert_partials(big_partials, partials, partial_bound)
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 8, 2), (128, 16, 4), (256, 16, 4), (256, 12, 3)])
+def test_single_tile_and_multi_tile_kernels_agree_on_one_tile(dim, hq, hkv):
+    """A split holding one tile of tokens gives the same partial and LSE bits whether it
+    runs the single-tile kernel (tokens_per_split == tile) or the loader kernel (a
+    two-tile split whose second tile is past the sequence end): both compute scores,
+    maxima, probabilities and denominators the same way and P V in the same k-step
+    order."""
+    tile = 16384 // dim
+    lengths = [tile, tile - 1, 1, 0, tile // 2 + 3]
+    q, k, v, table, lens = make_case(lengths, hq, hkv, dim, seed=61, capacity=2 * tile)
+    poison_tails(k, v, table, lens)
+    g = to_gpu((q, k, v, table, lens))
+    out = {}
+    for tokens in (tile, 2 * tile):
+        partials = torch.empty((len(lengths), hq, 1, dim), device="cuda")
+        lse = torch.empty((len(lengths), hq, 1), device="cuda")
+        _native.partition(*g, partials, lse, hkv, 1, tokens, tile, dim ** -0.5)
+        torch.cuda.synchronize()
+        out[tokens] = (partials, lse)
+    assert torch.equal(out[tile][1].view(torch.int32), out[2 * tile][1].view(torch.int32))
+    assert torch.equal(out[tile][0].view(torch.int32), out[2 * tile][0].view(torch.int32))
