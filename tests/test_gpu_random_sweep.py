@@ -29,7 +29,7 @@ from paged_decode.spec import DecodeSpec
 pytestmark = pytest.mark.gpu
 
 BACKENDS = ("matched", "matched_splits", "matched_fused", "hip_base", "hip_splitk")
-CASES = 120
+CASES = 180
 BOUNDARIES = (0, 1, 2, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 512, 513, 1023, 1024,
               1025)
 
