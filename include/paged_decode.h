@@ -175,11 +175,12 @@ int pd_matched_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_strid
 /* Base decode: FP32 online softmax over the whole context with FP32
  * probabilities, out = acc / denom (0 for an empty row), for every query head.
  * One workgroup per (kv head, sequence) serves the kv head's query heads (16 at
- * a time), so K/V is read once per kv head; at head_dim 64 with an even
- * num_kv_heads and at most 8 query heads per kv head, one workgroup serves two
- * adjacent kv heads (a token's two rows are one contiguous read).  Replaces
- * _base (kernels.py:10-41) as launched by paged_decode (runtime.py:109).
- * Writes out rows [0, batch). */
+ * a time), so K/V is read once per kv head; at head_dim 64, one workgroup
+ * serves four adjacent kv heads when num_kv_heads is a multiple of 4 and they
+ * have at most 4 query heads each, else two when num_kv_heads is even and they
+ * have at most 8 (a token's rows of those heads are one contiguous read).
+ * Replaces _base (kernels.py:10-41) as launched by paged_decode
+ * (runtime.py:109).  Writes out rows [0, batch). */
 int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h,
             const void* k, const void* v,
             const int32_t* table, int64_t table_stride_b, int32_t table_width,

@@ -197,11 +197,11 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<D>::kNBW],
 // probabilities (three bf16 terms for the base and fixed-split protocols) to
 // LDS, and compute wavefront w multiplies the whole tile's P by V columns
 // [w D/4, (w + 1) D/4) (pv_tile_cols).  The accumulator takes D/16 VGPRs, and
-// O needs no cross-wave reduction at the end.  At D = 64, kHeads = 2 serves
-// two adjacent kv heads (base and fixed-split protocols): row R of a tile is
-// token R / 2 of kv head 2 kh + R % 2, a token's two rows one contiguous
-// 256-byte read; query head e G + g scores only the rows of its own kv head
-// (R % 2 = e), and the other rows get probability 0.
+// O needs no cross-wave reduction at the end.  At D = 64, kHeads = H = 2 or 4
+// serves H adjacent kv heads (base and fixed-split protocols): row R of a
+// tile is token R / H of kv head H kh + R % H, a token's H rows one contiguous
+// read of 128 H bytes; query head e G + g scores only the rows of its own kv
+// head (R % H = e), and the other rows get probability 0.
 //
 // Eight wavefronts: four compute and four only copy K and V rows into LDS
 // (buffer_load ... lds).  The LDS below allows one workgroup per CU, so each
@@ -249,7 +249,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
                    float scale, float c) {
   static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
   static_assert(kHeads == 1 || kMode != kMatched, "kv-head groups change the tile of the protocol");
-  static_assert(kHeads == 1 || (kHeads == 2 && D == 64), "kv-head pairs at D = 64 only");
+  static_assert(kHeads == 1 || ((kHeads == 2 || kHeads == 4) && D == 64), "kv-head groups at D = 64 only");
   using C = Matched<D, GP>;
   using P = TileP<D>;
   constexpr int TILE = C::kTile;        // tile rows: TILE / kHeads tokens of kHeads kv heads
@@ -415,8 +415,8 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
         for (int r = 0; r < 4; ++r) s[g][r] *= scale;
     }
     if constexpr (kHeads > 1) {
-      // Rows of the other kv head (R % 2 = r % 2), and tokens past the end;
-      // padding query lanes (qh >= 2 G) take the last head's rows.
+      // Rows of the other kv heads (R % H = r % H), and tokens past the end;
+      // padding query lanes (qh >= H G) take the last head's rows.
       const int e = min(qh / G, kHeads - 1);
 #pragma unroll
       for (int g = 0; g < C::kNG; ++g)
@@ -1158,15 +1158,19 @@ int padded_group(int g) {
   return gp;
 }
 
-// kv heads per workgroup of the D = 64 base / fixed-split launch: 2 when
-// the kv head count is even and the pair's query heads fit one 16-head
-// group, else 1.  (4 heads per workgroup, 512-byte runs per token, measured
-// slower: 187.6 against 168.7 us with batch 128 and 16 kv heads, and with 8
-// kv heads the grid of 256 workgroups leaves half of each CU's slots empty.
-// Pairs at D = 128, whose rows are 256 bytes already, gained 3% on 16 kv
-// heads and lost 3-17% with 8: 979 against 814 us for batch 64, Hq 32,
-// Hkv 8, lengths up to 32768.)
+// kv heads per workgroup of the D = 64 base / fixed-split launch: 4 when the
+// kv head count is a multiple of 4 and the four heads' query heads fit one
+// 16-head group, else 2 when it is even and a pair's do, else 1.  A token's
+// rows of the workgroup's heads are then one contiguous run of 128 bytes per
+// head (512 bytes for four).  With the loader kernel, four heads beat pairs by
+// 5-7% (batch 128, 16 kv heads, lengths up to 4096: 157.6 against 165.7 us
+// base, 162.1 against 174.2 us fixed split); eight heads (32-token tiles)
+// took 262 us: the longest sequences' workgroups then set the call.  (Pairs
+// at D = 128, whose rows are 256 bytes already, lost 3-17% with 8 kv heads in
+// the kernel before the loader wavefronts: 979 against 814 us for batch 64,
+// Hq 32, Hkv 8, lengths up to 32768.)
 int heads_per_workgroup(int num_kv_heads, int G) {
+  if (num_kv_heads % 4 == 0 && 4 * G <= 16) return 4;
   return num_kv_heads % 2 == 0 && 2 * G <= 16 ? 2 : 1;
 }
 
@@ -1507,13 +1511,18 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
                   kSplitMode ? parts : 1, T, float(scale), float(scale * 1.4426950408889634)};
   // The fixed-split protocol walks each sequence in one workgroup and writes
   // every partition of it (grid.x = 1), like the base protocol.  At D = 64 a
-  // workgroup serves two adjacent kv heads when their query heads fit one
-  // 16-head group: a token's two 128-byte rows are one contiguous read.
+  // workgroup serves four or two adjacent kv heads when their query heads fit
+  // one 16-head group: a token's 128-byte rows of those heads are one
+  // contiguous read.
   const int heads = head_dim != 64 ? 1 : heads_per_workgroup(num_kv_heads, G);
-  const dim3 grid(1, heads == 2 ? num_kv_heads / 2 : num_kv_heads * hs, batch);
+  const dim3 grid(1, heads > 1 ? num_kv_heads / heads : num_kv_heads * hs, batch);
   a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   constexpr int kMode = kSplitMode ? kSplit : kBase;
+  if (heads == 4) {
+    launch_cols_loader<64, false, kMode, 4>(padded_group(4 * G), grid, st, a);
+    return launch_status(what);
+  }
   if (heads == 2) {
     launch_cols_loader<64, false, kMode, 2>(padded_group(2 * G), grid, st, a);
     return launch_status(what);

@@ -230,11 +230,12 @@ def test_fixed_split_walk_partition_sizes(dim, hq, hkv, tiles_per_partition):
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
 @pytest.mark.parametrize("hq,hkv", [(2, 2), (16, 16), (8, 4), (6, 2), (16, 2), (12, 4), (10, 2),
                                     (4, 4), (16, 4), (3, 3)])
-def test_d64_kv_head_pairs(backend, hq, hkv):
-    """At D=64 one workgroup serves two adjacent kv heads and their 2G query heads when
-    the kv head count is even and 2G <= 16 (tiles of 128 tokens of both heads); odd kv
-    head counts stay one per workgroup.  Group sizes 1 to 8 (padded to 2, 4, 8 and 16
-    query heads), lengths around the 128-token tile boundaries and the partitions,
+def test_d64_kv_head_groups(backend, hq, hkv):
+    """At D=64 one workgroup serves four adjacent kv heads and their 4G query heads when
+    the kv head count is a multiple of 4 and 4G <= 16 (tiles of 64 tokens of the four
+    heads), else two when it is even and 2G <= 16 (128-token tiles); odd kv head counts
+    stay one per workgroup.  Group sizes 1 to 8 (padded to 2, 4, 8 and 16 query heads),
+    lengths around the 64- and 128-token tile boundaries and the partitions,
     NaN-poisoned tails."""
     lengths = [0, 1, 2, 63, 64, 65, 127, 128, 129, 255, 256, 257, 383, 511, 512, 513, 1100]
     q, k, v, table, lens = make_case(lengths, hq, hkv, 64, seed=hq * 31 + hkv, capacity=1100)
