@@ -108,8 +108,8 @@ def test_fused_matched_rows_do_not_depend_on_the_batch_order():
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
 @pytest.mark.parametrize("dim,hq,hkv,batch,capacity", [
     (256, 32, 4, 128, 2048),   # 512 workgroups, one per CU, in two rounds: longest first
-    (64, 16, 16, 128, 2048),   # kv-head pairs: 1024 workgroups, longest first
-    (64, 32, 8, 64, 2048),     # kv-head pairs of 4-head groups: 256 workgroups, one per CU
+    (64, 16, 16, 128, 2048),   # four kv heads per workgroup: 512 workgroups, longest first
+    (64, 32, 8, 64, 2048),     # four kv heads of 4 query heads: 128 workgroups, one per CU
     (128, 32, 8, 40, 2048),    # 320 workgroups, one and a quarter rounds: longest first
     (128, 64, 2, 128, 1024),   # 32-head groups in two 16-head slices: 512 workgroups
 ])
