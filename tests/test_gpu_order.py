@@ -110,6 +110,7 @@ def test_fused_matched_rows_do_not_depend_on_the_batch_order():
     (256, 32, 4, 128, 2048),   # 512 workgroups, one per CU, in two rounds: longest first
     (64, 16, 16, 128, 2048),   # four kv heads per workgroup: 512 workgroups, longest first
     (64, 32, 8, 64, 2048),     # four kv heads of 4 query heads: 128 workgroups, one per CU
+    (64, 12, 6, 128, 2048),    # kv-head pairs (6 kv heads): 384 workgroups, longest first
     (128, 32, 8, 40, 2048),    # 320 workgroups, one and a quarter rounds: longest first
     (128, 64, 2, 128, 1024),   # 32-head groups in two 16-head slices: 512 workgroups
 ])
