@@ -280,7 +280,7 @@ def bandwidth_sweep(torch, seed=64, calls=20):
     return result
 
 
-def context_sweep(torch, contexts=(8192, 32768, 131072)):
+def context_sweep(torch, contexts=(8192, 32768, 65536, 131072)):
     """D256 GQA 4:1 (Hq 16, Hkv 4), B=1 at longer contexts, planner plan.  At 131072
     tokens the KV (537 MB) exceeds the 256 MB last-level cache, so the reads come
     from HBM; the shorter ones are partly cache-resident across replays."""
@@ -340,6 +340,69 @@ def paged_backend_rates(torch, seed=64):
             del res
         out[name] = row
         del q, k, v, table, lens
+        torch.cuda.empty_cache()
+    return out
+
+
+SMALL_BATCH_SHAPES = (
+    # name, Hq, Hkv, D, table capacity, context of every sequence
+    ("D256 GQA 16/4 ctx 2064", 16, 4, 256, 2112, 2064),
+    ("D128 GQA 32/8 ctx 4096", 32, 8, 128, 4096, 4096),
+)
+
+
+def small_batch_backends(torch, batches=(1, 8), seed=20261105):
+    """paged_decode hip_base / hip_splitk and matched_decode at small batch: B sequences of
+    one context each, on the headline shape (Hq 16, Hkv 4, D 256, ctx 2064) and a D128
+    shape (Hq 32, Hkv 8, ctx 4096); hot cache, 128-call graphs."""
+    from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
+    from paged_decode.runtime import allocate_resources, paged_decode
+    from paged_decode.spec import DecodeSpec
+    out = {}
+    for name, hq, hkv, dim, cap, ctx in SMALL_BATCH_SHAPES:
+        for batch in batches:
+            lengths = [ctx] * batch
+            q, k, v, table, lens = make_inputs(torch, batch, hq, hkv, dim, cap, lengths, seed)
+            spec = DecodeSpec(batch, hq, hkv, dim, cap)
+            nbytes = algorithmic_bytes(lengths, batch, hq, hkv, dim)
+            row = {}
+            for backend in ("hip_base", "hip_splitk", "matched"):
+                if backend == "matched":
+                    res = allocate_matched_resources(spec, "cuda")
+                    fn = lambda: matched_decode(q, k, v, table, lens, resources=res)
+                else:
+                    res = allocate_resources(spec, "cuda", backend)
+                    fn = lambda: paged_decode(q, k, v, table, lens, resources=res,
+                                              backend=backend)
+                us = graph_time_us(torch, fn, 256, unroll=128)
+                row[backend] = {"us_per_call": round(us, 2),
+                                "pct_peak": round(100 * nbytes / us / 1e6 / PEAK_TBPS, 1)}
+                del res
+            out[f"{name} B={batch}"] = row
+            progress(f"small batch {name} B={batch}: " + ", ".join(
+                f"{b} {r['us_per_call']} us" for b, r in row.items()))
+            del q, k, v, table, lens
+            torch.cuda.empty_cache()
+    return out
+
+
+def batch_sweep_ctx2064(torch, batches=(8, 32)):
+    """The headline shape (Hq 16, Hkv 4, D 256) at B sequences of 2064 tokens, planner plan:
+    where the call's share of peak grows with the batch (hot cache)."""
+    out = {}
+    for batch in batches:
+        case = matched_case(torch, batch, 16, 4, 256, 2112, [2064] * batch, 20261105)
+        us = graph_time_us(torch, case["full"], 256, unroll=128)
+        part_us = graph_time_us(torch, case["partition"], 256, unroll=128)
+        nbytes = algorithmic_bytes([2064] * batch, batch, 16, 4, 256)
+        pbytes = algorithmic_bytes([2064] * batch, batch, 16, 4, 256, with_output=False)
+        p = case["plan"]
+        out[f"B_{batch}"] = {"plan": f"{p.splits}x{p.tokens_per_split}",
+                             "us_per_call": round(us, 2),
+                             "pct_peak": round(100 * nbytes / us / 1e6 / PEAK_TBPS, 1),
+                             "partition_us": round(part_us, 2),
+                             "partition_pct_peak": round(100 * pbytes / part_us / 1e6 / PEAK_TBPS, 1)}
+        del case
         torch.cuda.empty_cache()
     return out
 
@@ -670,6 +733,18 @@ def ab_report(torch, args):
     print(json.dumps({k: v for k, v in report.items() if k != "rows"}))
 
 
+# Extra measurements that --section runs on their own.
+SECTIONS = {
+    "small_batch": small_batch_backends,
+    "batch_sweep": batch_sweep_ctx2064,
+    "context_sweep": context_sweep,
+    "bandwidth_sweep": bandwidth_sweep,
+    "paged_backends": paged_backend_rates,
+    "kv_write": kv_write_rates,
+    "e2e_decoder": e2e_decoder,
+}
+
+
 def benchmark_protocol_fingerprint(torch):
     from paged_decode import benchmark_protocol
     return benchmark_protocol.fingerprint(torch)
@@ -704,6 +779,9 @@ def main():
                     help="backend of the edge_d64 / edge_d256 / sweep A/B workloads")
     ap.add_argument("--ab-partition", type=int, default=1024,
                     help="partition tokens of the partitions A/B workload")
+    ap.add_argument("--section", default=None, metavar="S1,S2,...",
+                    help="only these extra measurements, printed as one JSON object: "
+                         + ", ".join(SECTIONS))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -721,6 +799,15 @@ def main():
         return
     if args.ab:
         ab_report(torch, args)
+        return
+    if args.section:
+        result = {}
+        for name in args.section.split(","):
+            if name not in SECTIONS:
+                raise SystemExit(f"unknown section {name!r}; known: {', '.join(SECTIONS)}")
+            result[name] = SECTIONS[name](torch)
+            progress(f"section {name} done")
+        print(json.dumps(result))
         return
 
     ctx, capacity = args.ctx, max(2112, args.ctx)
@@ -778,6 +865,9 @@ def main():
         progress(f"bandwidth sweep: {extra['bandwidth_sweep']['us_per_call']} us/call")
         extra["paged_decode_backends"] = paged_backend_rates(torch)
         progress("paged_decode backends done")
+        extra["small_batch_backends"] = small_batch_backends(torch)
+        extra["batch_sweep_ctx2064_d256_gqa4"] = batch_sweep_ctx2064(torch)
+        progress("small-batch backends and the batch sweep at context 2064 done")
         extra["kv_write"] = kv_write_rates(torch)
         progress("kv write done")
         extra["e2e_decoder"] = e2e_decoder(torch)

@@ -39,7 +39,7 @@ enum pd_status { PD_OK = 0, PD_EINVAL = 1, PD_ELAUNCH = 2 };
 
 #define PD_PAGE_SIZE 256      /* spec.py:6 */
 #define PD_PARTITION_SIZE 1024 /* spec.py:7 */
-#define PD_ABI_VERSION 4
+#define PD_ABI_VERSION 5
 
 /* Split-KV plan; field meanings follow SplitKVPlan (splitkv_plan.py:15-23). */
 typedef struct pd_plan {
@@ -102,18 +102,6 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
                  int32_t batch, int32_t num_heads, int32_t head_dim, int32_t splits,
                  int32_t lse_lanes, pd_stream_t stream);
 
-/* Probes how the current device deals the workgroups of a launch to its XCDs
- * and records it for pd_matched_decode.  This entry point has no counterpart
- * in the reference (its GPUs have one L2).  It launches one small kernel on the
- * default stream and waits for it, so it must not be called while a stream is
- * being captured.  *xcds receives the XCD count when workgroup i of a launch
- * runs on XCD (i + c) % count for one offset c per launch (the MI355X
- * dispatch order; c varies between launches), else -1.  From then on,
- * pd_matched_decode on this device keeps all splits of each (sequence, kv head)
- * on one XCD for single-tile plans, so their partials and merge stay in that
- * XCD's L2 (see pd_matched_decode). */
-int pd_probe_xcds(int32_t* xcds);
-
 /* int32 counters per (sequence, kv head) in pd_matched_decode's `counters`. */
 #define PD_FUSED_COUNTERS_PER_GROUP 128
 
@@ -131,15 +119,8 @@ int pd_probe_xcds(int32_t* xcds);
  * Writes partials, lse and out bf16 [batch, num_heads, head_dim].  The merge
  * sums with the plan's lse_lanes, min(next_pow2(splits), 32 if
  * head_dim % 128 == 0 else 16).
- * Where the merge runs: on a device that pd_probe_xcds found to deal
- * workgroups round-robin to its XCDs, single-tile plans run a one-dimensional
- * grid in which each workgroup reads the XCD it runs on and takes work of the
- * groups g = b * num_kv_heads + kh with g % xcds equal to it, so every split of
- * a group runs on one XCD; partials, counters and merge then stay in that
- * XCD's L2 (plain stores, loads that skip the CU's L1).  A workgroup on an XCD
- * index beyond the probed count adds 1 to counters[1], otherwise always 0.
- * Elsewhere the partials are published with device-scope stores and read
- * with device-scope loads, so the merge may run on any XCD. */
+ * The partials are published with device-scope stores and read with
+ * device-scope loads, so the merge may run on any XCD. */
 int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                       const void* k, const void* v,
                       const int32_t* table, int64_t table_stride_b, int32_t table_width,
@@ -189,13 +170,17 @@ int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h,
             int32_t head_dim, double scale, pd_stream_t stream);
 
 /* Fixed-size split-K partition: unnormalized (m, l, acc) per partition of
- * partition_size tokens, m in scaled units.  The workgroups are pd_base's:
- * each walks its sequence's context and writes every partition's (m, l, acc)
- * as it passes, empty partitions included.  Replaces _split (kernels.py:44-80) as
- * launched by paged_decode (runtime.py:111-113).  maxima/denoms f32
- * [batch, num_heads, partitions], accums f32 [batch, num_heads, partitions, D];
- * the row stride of all three is `partitions`; partitions * partition_size
- * < 2^31. */
+ * partition_size tokens, m in scaled units, every partition written (empty ones
+ * as m = -inf, l = 0, acc = 0).  When the device has at least as many CUs as
+ * pd_base has workgroups (one per kv head group and sequence), those
+ * workgroups each walk their sequence's context and write every partition as
+ * they pass it; with fewer, one workgroup runs per partition, as in the
+ * reference's grid.  Both write the same bits.  Replaces _split
+ * (kernels.py:44-80) as launched by paged_decode (runtime.py:111-113).
+ * maxima/denoms f32 [batch, num_heads, partitions], accums f32 [batch,
+ * num_heads, partitions, D]; the row stride of all three is `partitions`;
+ * partition_size a positive multiple of 16384 / head_dim; partitions *
+ * partition_size < 2^31. */
 int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                    const void* k, const void* v,
                    const int32_t* table, int64_t table_stride_b, int32_t table_width,
@@ -210,6 +195,36 @@ int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 int pd_ml_merge(const float* maxima, const float* denoms, const float* accums, void* out,
                 int32_t batch, int32_t num_heads, int32_t head_dim, int32_t partitions,
                 pd_stream_t stream);
+
+/* Small-batch split of the base and fixed-split protocols; no counterpart in
+ * the reference, whose _base and _split grids already spread a sequence over
+ * (query heads[, partitions]) programs (runtime.py:109-113).  pd_base and
+ * pd_split_fixed walk each sequence in one workgroup per kv head group, so a
+ * batch of fewer walks than half of sm_count leaves CUs idle; the walks are
+ * counted for `batch` rounded up to a power of two.  For such a batch this
+ * returns a cut of a table of `table_width` pages into *chunks >= 2 partitions
+ * of *chunk_tokens tokens (a multiple of 16384 / head_dim; about sm_count /
+ * walks of them, at most 128): run pd_split_fixed(partitions, partition_size =
+ * *chunk_tokens) and pd_ml_merge over partitions = ceil(w * 256 /
+ * *chunk_tokens) for a call whose table has w <= table_width pages.  That
+ * computes the same attention as pd_base or the 1024-token pd_split_fixed with
+ * other float32 rounding.  Partitions past a sequence's length are empty and
+ * leave the merge's bits unchanged, and each sequence's partitions are its own,
+ * so a sequence's output does not depend on w, on the other sequences, or on
+ * empty sequences padding the batch below its next power of two (a graph
+ * bucket), as long as table_width is the same.  Otherwise *chunks = 1 and
+ * *chunk_tokens = table_width * 256: run the backend itself.  Host only. */
+int pd_plan_chunks(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t table_width, int32_t sm_count, int32_t* chunks,
+                   int32_t* chunk_tokens);
+
+/* Size of a chunk workspace for pd_plan_chunks (no counterpart in the
+ * reference): *rows = the largest batch * num_heads * chunks it returns for any
+ * batch <= max_batch and any table width (0 if none is cut), so maxima and
+ * denoms of *rows floats and accums of *rows * head_dim floats serve every
+ * call (batch <= max_batch, any w).  Host only. */
+int pd_chunk_rows(int32_t max_batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                  int32_t sm_count, int64_t* rows);
 
 /* KV-cache write of token rows through a flat slot mapping; replaces the
  * store_kvcache Triton kernel of the nano-vLLM overlay

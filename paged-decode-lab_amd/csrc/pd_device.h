@@ -90,6 +90,19 @@ __device__ __forceinline__ float wave_max(float x) {
   return fmaxf(x, xor_lanes<1>(x, lane));
 }
 
+// Sum over the 64 lanes: an xor butterfly at distances 32, 16, ..., 1.  Each
+// step adds the same two values in every lane of a pair (float addition
+// commutes), so every lane ends with the same bits.
+__device__ __forceinline__ float wave_sum(float x) {
+  const int lane = __lane_id();
+  x += xor_lanes<32>(x, lane);
+  x += xor_lanes<16>(x, lane);
+  x += xor_lanes<8>(x, lane);
+  x += xor_lanes<4>(x, lane);
+  x += xor_lanes<2>(x, lane);
+  return x + xor_lanes<1>(x, lane);
+}
+
 // Reductions over the four 16-lane rows of a wavefront (lanes L, L^16, L^32,
 // L^48) with v_permlane16_swap / v_permlane32_swap: each swap returns the
 // pair {x[L], x[L^16]} (or {x[L], x[L^32]}) in some order, so a commutative
@@ -119,14 +132,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
-// Cache-policy operands of the buffer builtins (bit 0 is sc0, bit 1 nt, bit 4
+// Cache-policy operand of the buffer builtins (bit 0 is sc0, bit 1 nt, bit 4
 // sc1).  kCoherentAux (sc1): device-scope coherent accesses, written through to
 // / re-read from the coherence point beyond the XCDs' L2s, so a line another
-// XCD wrote is seen.  kL2Aux (sc0): a load that misses the CU's L1 and is
-// served by its XCD's L2, which every CU of that XCD writes through to; enough
-// for values another workgroup of the same XCD stored.
+// XCD wrote is seen.
 constexpr int kCoherentAux = 16;
-constexpr int kL2Aux = 1;
 
 // E consecutive floats at byte offset `off`, with cache policy kAux.
 // The builtins' results are bit-cast as whole vectors to float vectors before
@@ -327,8 +337,7 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
 // which writes it to wsh[128 h + p], and each lane reads its head's weights
 // four splits at a time.  Loads past the last split read past the buffer
 // (zero) and have weight 0, so they leave acc unchanged.  kAux is the cache
-// policy of the loads: kCoherentAux for values workgroups on other XCDs wrote,
-// kL2Aux for values workgroups of this XCD wrote.
+// policy of the loads: kCoherentAux for values workgroups on other XCDs wrote.
 template <int GP, int kNC, int kBatch, int kAux>
 __device__ __forceinline__ void merge_group_chunks(const float* __restrict__ pg,
                                                    const float* __restrict__ lg,

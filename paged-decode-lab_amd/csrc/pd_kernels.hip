@@ -18,8 +18,8 @@
 //                      with PV split across the wavefronts by output columns.
 //   lse_merge          one wavefront per (sequence, query head, 64 columns):
 //                      stable log-sum-exp merge of the split partials, bf16 out.
-//   ml_merge           one wavefront per (sequence, query head): merge of the
-//                      (m, l, acc) states.
+//   ml_merge           one wavefront per (sequence, query head, 64 columns):
+//                      merge of the (m, l, acc) states.
 //
 // Every kernel reads the sequence length and block table on the device and
 // never needs host-side knowledge of tensor contents, so launches are
@@ -56,7 +56,12 @@ struct MatchedShared {
 //   kSplit    the same arithmetic over fixed partitions, storing (m, l, acc)
 //             in the reference's units (kernels.py:44-80): m of the scaled
 //             scores into `maxima`, l into `lse_out`, unnormalized acc into
-//             `partials`.
+//             `partials`.  One workgroup walks every partition of its
+//             (kv head, sequence) (grid.x = 1).
+//   kSplitPart  kSplit with one workgroup per partition (grid.x = splits), as
+//             the reference launches _split (runtime.py:111-113).  Each
+//             partition's arithmetic is the walk's, so both write the same
+//             bits.
 // FP32 p goes through the bf16 MFMA as three bf16 terms hi + mid + lo (each
 // the RNE bf16 of the previous remainder), which represent p to 2^-27 of its
 // value, finer than p's own float32 rounding; with exact bf16 x bf16 products
@@ -72,19 +77,13 @@ struct MatchedShared {
 // A workgroup serves query heads [qb, qb + Gs) of kv head kh: the whole group
 // (hs = 1) when it has at most 16 heads, else 16-head slices of it (grid.y =
 // Hkv * hs), so the base and fixed-split protocols also cover G > 16.
-constexpr int kMatched = 0, kBase = 1, kSplit = 2;
+constexpr int kMatched = 0, kBase = 1, kSplit = 2, kSplitPart = 3;
 
 // Split counters of the fused launch: four per (sequence, kv head), one per
 // column slice of the single-tile kernel (the multi-tile kernels use the
 // first), each on a 128-byte line of its own, so that the atomics of
 // different slices do not queue on one line.
 constexpr int kCounterStride = 32;
-// Fused modes of the single-tile kernel: none (partition only), coherent (the
-// merge may run on another XCD: device-scope stores and loads), XCD-local (all
-// of a group's workgroups on one XCD: plain stores, loads served by its L2).
-constexpr int kFuseNone = 0, kFuseCoherent = 1, kFuseXcd = 2;
-// Hardware register holding the XCD (XCC) index of the executing wavefront.
-constexpr int kHwRegXccId = 20;
 constexpr int kCountersPerGroup = 4 * kCounterStride;
 static_assert(kCountersPerGroup == PD_FUSED_COUNTERS_PER_GROUP, "C ABI counter layout");
 
@@ -266,11 +265,14 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   __shared__ __attribute__((aligned(16))) char ps[kTerms][16 * P::kPitch];
   __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
 
-  // The fixed-split protocol walks the whole context of its (kv head,
-  // sequence) in one workgroup (grid.x = 1) and writes the (m, l, acc) of each
-  // T-token partition as the walk leaves it, so a sequence's partitions share
-  // one workgroup's start and its K / V pipeline.
+  // The fixed-split protocol writes the (m, l, acc) of each T-token partition
+  // as its tiles are done.  kSplit walks the whole context of its (kv head,
+  // sequence) in one workgroup (grid.x = 1), so a sequence's partitions share
+  // one workgroup's start and its K / V pipeline; kSplitPart runs the same
+  // code over partition blockIdx.x alone.
   constexpr bool kWalk = kMode == kSplit;
+  constexpr bool kFlush = kMode == kSplit || kMode == kSplitPart;
+  constexpr int kEmptyMode = kFlush ? kSplit : kMode;  // write_empty_partition's protocol
   const int p = kWalk ? 0 : int(blockIdx.x);
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
   const int kvh = kHeads * kh;                      // (first) kv head of this workgroup
@@ -336,9 +338,9 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       }
       lds_barrier();  // B2(ti)
       if (ti >= 2) issue(ti - 2, true);
-      if (kWalk && ti % tpp == 0) lds_barrier();  // the walk's partition flush
+      if (kFlush && ti % tpp == 0) lds_barrier();  // the partition flush
     }
-    if constexpr (!kWalk) lds_barrier();  // epilogue
+    if constexpr (!kFlush) lds_barrier();  // epilogue
     if constexpr (kFused) {
       __syncthreads();  // the split count's two barriers
       __syncthreads();
@@ -348,8 +350,8 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 
   if (!kFused && count == 0) {
     for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
-      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
-                                      maxima);
+      write_empty_partition<D, kEmptyMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out,
+                                           out, maxima);
     return;
   }
   bf16x8_t qf[C::kCH];
@@ -501,14 +503,14 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     pv_tile_cols<D, GP, kTerms>(acc, ps, vs[ti & 1], lane, w);
     if (ti > 0) read_k(ti - 1);
 
-    if constexpr (kWalk) {
-      // After tile ti, the first tile of partition ti / tpp, that partition
-      // is complete: its denominators are summed over the waves and its
-      // (m, l, acc) stored (kernels.py:77-80), and the running state restarts
-      // for the partition before it.  The copies of the next tiles stay in
-      // flight.
+    if constexpr (kFlush) {
+      // After tile ti, the first tile of partition p + ti / tpp, that
+      // partition is complete: its denominators are summed over the waves and
+      // its (m, l, acc) stored (kernels.py:77-80), and the running state
+      // restarts for the partition before it.  The copies of the next tiles
+      // stay in flight.
       if (ti % tpp == 0) {
-        const int part = ti / tpp;
+        const int part = p + ti / tpp;
         const float l = sum_rows(l_own);
         if (lane < 16) sm.lsum[w][lane] = l;
         lds_barrier();
@@ -539,10 +541,11 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   if constexpr (kWalk) {
     // Partitions past the sequence's last token are empty.
     for (int pp = (end + T - 1) / T; pp < splits; ++pp)
-      write_empty_partition<D, kMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
-                                      maxima);
+      write_empty_partition<D, kSplit>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
+                                       maxima);
     return;
   }
+  if constexpr (kFlush) return;  // partition p was written by the flush after its first tile
 
   // ---- epilogue: denominators over the waves; O needs no reduction
   const float l = sum_rows(l_own);
@@ -661,23 +664,21 @@ struct FusedMerge {
   static constexpr int kBatch = kNC == 2 ? 20 : 48 / kNC;
 };
 
-template <int D, int GP, int kFuse>
+template <int D, int GP, bool kFused>
 __global__ void __launch_bounds__(kThreads, 2)
 matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
                     const uint16_t* __restrict__ q, int tsb, int width, int qsb, int qsh, int G,
                     int Hq, int splits, const uint16_t* __restrict__ k,
                     const uint16_t* __restrict__ v, float* __restrict__ partials,
                     float* __restrict__ lse_out, int Hkv, float scale, float c,
-                    int* __restrict__ counters, uint16_t* __restrict__ out, int xcds,
-                    int groups) {
+                    int* __restrict__ counters, uint16_t* __restrict__ out) {
   using C = Matched<D, GP>;
   using P = TileP<D>;
   constexpr int TILE = C::kTile;
-  constexpr bool kFused = kFuse != kFuseNone;
-  // Cache policy of the published slices and of the merging loads.
-  constexpr int kPubAux = kFuse == kFuseXcd ? 0 : kCoherentAux;
-  constexpr int kMergeAux = kFuse == kFuseXcd ? kL2Aux : kCoherentAux;
-  constexpr int kScope = kFuse == kFuseXcd ? __HIP_MEMORY_SCOPE_WORKGROUP : __HIP_MEMORY_SCOPE_AGENT;
+  // The slices are published with device-scope (sc1) stores and read back with
+  // device-scope loads: the merging wavefront may run on another XCD, whose L2
+  // is not coherent with this one's.
+  constexpr int kScope = __HIP_MEMORY_SCOPE_AGENT;
   __shared__ float wmax[4][16];
   __shared__ float lsum[4][16];
   __shared__ __attribute__((aligned(16))) char vs[4 * C::kSlot];
@@ -685,31 +686,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
   // Fused merge: each wavefront's merge weights, [GP][128] floats.
   __shared__ __attribute__((aligned(16))) float wsm[kFused ? 4 * 128 * GP : 4];
 
-  int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-  if constexpr (kFuse == kFuseXcd) {
-    // One-dimensional grid of xcds * R workgroups.  The dispatcher deals the
-    // workgroups of a launch round-robin to the XCDs from an offset that
-    // varies between launches (workgroup i runs on XCD (i + c) % xcds, the
-    // same c for the whole launch), so each XCD runs exactly R workgroups,
-    // whose i / xcds are 0 .. R-1.  The work is chosen by the XCD the
-    // workgroup actually runs on: group g = (b, kh) belongs to XCD
-    // g % xcds, whose workgroups take its splits in turn, so all of a
-    // group's partials, its counters and its merge stay in that XCD's L2.
-    const int x = __builtin_amdgcn_s_getreg((15 << 11) | kHwRegXccId) & 0xf;
-    const int slot = blockIdx.x / xcds;
-    const int g = x + xcds * (slot / splits);
-    if (x >= xcds) {
-      // Not the device pd_probe_xcds saw: counted in an otherwise unused word
-      // (word 1 of group 0's counter line), which the tests require to stay 0.
-      if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(counters + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    if (g >= groups) return;
-    p = slot % splits;
-    kh = g % Hkv;
-    b = g / Hkv;
-  }
+  const int p = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = lane & 15, qg = lane >> 4;
@@ -736,7 +713,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
     if (old != splits - 1) return;
     const int64_t grow = int64_t(b) * Hq + kh * G;  // first query head of the group
     using M = FusedMerge<D, GP>;
-    merge_group_chunks<GP, M::kNC, M::kBatch, kMergeAux>(
+    merge_group_chunks<GP, M::kNC, M::kBatch, kCoherentAux>(
         partials + grow * splits * D, lse_out + grow * splits, out + grow * D, G, splits, D,
         plan_lse_lanes(splits, D), w * P::kCols, P::kCols, wsm + w * 128 * GP, lane);
     if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, kScope);
@@ -906,7 +883,7 @@ matched_tile_kernel(const int32_t* __restrict__ table, const int32_t* __restrict
       const int h = ch / kChunks, c4 = 4 * (ch % kChunks);
       const u32x4_t val = *reinterpret_cast<const u32x4_t*>(stage + h * P::kCols + c4);
       __builtin_amdgcn_raw_buffer_store_b128(val, rs, ((h * splits + p) * D + w * P::kCols + c4) * 4,
-                                             0, kPubAux);
+                                             0, kCoherentAux);
     }
     count_and_merge();
   }
@@ -978,10 +955,52 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
 }
 
 // ------------------------------------------------------------ m/l/acc merge
-template <int VEC>
+// The merge of the fixed-split protocol (kernels.py:83-100): M = max_p m_p
+// (-inf -> 0), f_p = exp(m_p - M), out = sum_p f_p acc_p / sum_p f_p l_p (a
+// zero total divides by 1).  Up to 128 partitions: one wavefront per (b, h)
+// row and 64-column chunk (grid rows x D/64), one column per lane, so a row's
+// accumulators are read by D/64 CUs at once.  Lane j loads m and l of
+// partitions j and j + 64; every accumulator load of a batch of kBatch
+// partitions is issued before the factors are computed (merge_splits), the
+// total is an xor-butterfly sum over the lanes, and acc = fma(f_p, acc_p, acc)
+// runs in partition order.  Loads past the row read zero and carry f = 0.
+template <int kBatch>
 __global__ void __launch_bounds__(64)
 ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
-                const float* __restrict__ accums, uint16_t* __restrict__ out, int parts) {
+                const float* __restrict__ accums, uint16_t* __restrict__ out, int parts, int D) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int col = blockIdx.y * 64 + lane;
+  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(maxima + row * parts, parts * 4);
+  const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(denoms + row * parts, parts * 4);
+  float m0[1], m1[1], l0[1], l1[1];
+  buffer_load_f32<1, 0>(rm, lane * 4, m0);
+  buffer_load_f32<1, 0>(rm, (lane + 64) * 4, m1);
+  buffer_load_f32<1, 0>(rl, lane * 4, l0);
+  buffer_load_f32<1, 0>(rl, (lane + 64) * 4, l1);
+  float f0 = 0.f, f1 = 0.f, inv = 1.f, acc[1];
+  merge_splits<1, 0, kBatch>(
+      accums + row * parts * D, D, col, parts,
+      [&] {
+        const float v0 = lane < parts ? m0[0] : -INFINITY;
+        const float v1 = lane + 64 < parts ? m1[0] : -INFINITY;
+        float mx = wave_max(fmaxf(v0, v1));
+        if (mx == -INFINITY) mx = 0.f;  // all partitions empty
+        f0 = exp_fast(v0 - mx);
+        f1 = exp_fast(v1 - mx);
+        const float total = wave_sum(fmaf(l1[0], f1, l0[0] * f0));
+        inv = 1.f / (total > 0.f ? total : 1.f);
+      },
+      [&](int s0, int j) { return wave_weight(f0, f1, s0 + j); }, acc);
+  out[row * D + col] = uint16_t(bf16_bits(acc[0] * inv));
+}
+
+// The same merge for more than 128 partitions: one wavefront per row, lane j
+// owning columns VEC j .. VEC j + VEC - 1, partitions in order.
+template <int VEC>
+__global__ void __launch_bounds__(64)
+ml_merge_loop_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
+                     const float* __restrict__ accums, uint16_t* __restrict__ out, int parts) {
   constexpr int D = VEC * 64;
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
@@ -1083,20 +1102,6 @@ int device_cu_count() {
   return n;
 }
 
-// XCD layout of each device, set by pd_probe_xcds: the number of XCDs when
-// workgroup i of a launch runs on XCD i % xcds, -1 when the dispatch does not
-// follow that order, 0 when not probed.
-std::atomic<int> g_xcd_layout[64];
-
-int xcd_layout() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    (void)hipGetLastError();
-    return 0;
-  }
-  return g_xcd_layout[dev].load(std::memory_order_relaxed);
-}
-
 // `order` of ordered_sequence (pd_device.h) for a multi-tile launch over
 // `grid` = (splits, kv heads x slices, batch), one workgroup per CU:
 // * 0 (longest first) for two to four rounds of workgroups;
@@ -1116,14 +1121,12 @@ int batch_order(dim3 grid) {
   return n <= cus || n > 4 * int64_t(cus) ? -1 : 0;
 }
 
-template <int D, int kFuse>
-void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a, int xcds,
-                   int groups) {
+template <int D, bool kFused>
+void launch_tile_d(int gp, dim3 grid, hipStream_t stream, const PartitionArgs& a) {
 #define PD_LAUNCH_TILE(GPV)                                                                    \
-  hipLaunchKernelGGL((matched_tile_kernel<D, GPV, kFuse>), grid, dim3(kThreads), 0, stream,     \
+  hipLaunchKernelGGL((matched_tile_kernel<D, GPV, kFused>), grid, dim3(kThreads), 0, stream,    \
                      a.table, a.lengths, a.q, a.tsb, a.width, a.qsb, a.qsh, a.G, a.Hq, a.splits, \
-                     a.k, a.v, a.partials, a.lse, a.Hkv, a.scale, a.c, a.counters, a.out, xcds, \
-                     groups)
+                     a.k, a.v, a.partials, a.lse, a.Hkv, a.scale, a.c, a.counters, a.out)
   switch (gp) {
     case 1: PD_LAUNCH_TILE(1); break;
     case 2: PD_LAUNCH_TILE(2); break;
@@ -1156,22 +1159,6 @@ int padded_group(int g) {
   int gp = 1;
   while (gp < g) gp <<= 1;
   return gp;
-}
-
-// kv heads per workgroup of the D = 64 base / fixed-split launch: 4 when the
-// kv head count is a multiple of 4 and the four heads' query heads fit one
-// 16-head group, else 2 when it is even and a pair's do, else 1.  A token's
-// rows of the workgroup's heads are then one contiguous run of 128 bytes per
-// head (512 bytes for four).  With the loader kernel, four heads beat pairs by
-// 5-7% (batch 128, 16 kv heads, lengths up to 4096: 157.6 against 165.7 us
-// base, 162.1 against 174.2 us fixed split); eight heads (32-token tiles)
-// took 262 us: the longest sequences' workgroups then set the call.  (Pairs
-// at D = 128, whose rows are 256 bytes already, lost 3-17% with 8 kv heads in
-// the kernel before the loader wavefronts: 979 against 814 us for batch 64,
-// Hq 32, Hkv 8, lengths up to 32768.)
-int heads_per_workgroup(int num_kv_heads, int G) {
-  if (num_kv_heads % 4 == 0 && 4 * G <= 16) return 4;
-  return num_kv_heads % 2 == 0 && 2 * G <= 16 ? 2 : 1;
 }
 
 // Validation and dispatch shared by pd_partition (fused = false) and
@@ -1217,30 +1204,13 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int gp = padded_group(G);
   if (tokens_per_split == tile_tokens) {
-    // Fused single-tile plans keep each group on one XCD when the dispatch
-    // order of this device is known (pd_probe_xcds); otherwise they publish
-    // their partials at device scope.
-    const int xcds = fused ? xcd_layout() : 0;
-    const int groups = batch * num_kv_heads;
-    int mode = fused ? (xcds > 0 ? kFuseXcd : kFuseCoherent) : kFuseNone;
-    dim3 tgrid = grid;
-    if (mode == kFuseXcd) {
-      const int64_t n = int64_t(xcds) * ((groups + xcds - 1) / xcds) * splits;
-      if (n < (int64_t(1) << 31))
-        tgrid = dim3(unsigned(n));
-      else
-        mode = kFuseCoherent;
-    }
-    switch (head_dim * 4 + mode) {
-      case 256 + kFuseNone: launch_tile_d<64, kFuseNone>(gp, tgrid, st, a, xcds, groups); break;
-      case 256 + kFuseCoherent: launch_tile_d<64, kFuseCoherent>(gp, tgrid, st, a, xcds, groups); break;
-      case 256 + kFuseXcd: launch_tile_d<64, kFuseXcd>(gp, tgrid, st, a, xcds, groups); break;
-      case 512 + kFuseNone: launch_tile_d<128, kFuseNone>(gp, tgrid, st, a, xcds, groups); break;
-      case 512 + kFuseCoherent: launch_tile_d<128, kFuseCoherent>(gp, tgrid, st, a, xcds, groups); break;
-      case 512 + kFuseXcd: launch_tile_d<128, kFuseXcd>(gp, tgrid, st, a, xcds, groups); break;
-      case 1024 + kFuseNone: launch_tile_d<256, kFuseNone>(gp, tgrid, st, a, xcds, groups); break;
-      case 1024 + kFuseCoherent: launch_tile_d<256, kFuseCoherent>(gp, tgrid, st, a, xcds, groups); break;
-      default: launch_tile_d<256, kFuseXcd>(gp, tgrid, st, a, xcds, groups); break;
+    switch (head_dim * 2 + (fused ? 1 : 0)) {
+      case 128: launch_tile_d<64, false>(gp, grid, st, a); break;
+      case 129: launch_tile_d<64, true>(gp, grid, st, a); break;
+      case 256: launch_tile_d<128, false>(gp, grid, st, a); break;
+      case 257: launch_tile_d<128, true>(gp, grid, st, a); break;
+      case 512: launch_tile_d<256, false>(gp, grid, st, a); break;
+      default: launch_tile_d<256, true>(gp, grid, st, a); break;
     }
     return launch_status(what);
   }
@@ -1340,54 +1310,6 @@ extern "C" int pd_lse_merge(const float* partials, const float* lse, void* out, 
                      lse_lanes, stream);
 }
 
-// ------------------------------------------------------------- XCD probe
-// Placement of the workgroups of one launch of kXccProbeGroups workgroups on
-// the device's XCDs, read by pd_probe_xcds.  In host code `pd_xcc_ids` names a
-// host-side stand-in; the device address comes from hipGetSymbolAddress.
-constexpr int kXccProbeGroups = 2048;
-static __device__ int pd_xcc_ids[kXccProbeGroups];
-
-__global__ void __launch_bounds__(64) xcc_probe_kernel(int* __restrict__ ids) {
-  if (threadIdx.x == 0)
-    ids[blockIdx.x] = __builtin_amdgcn_s_getreg((15 << 11) | kHwRegXccId) & 0xf;
-}
-
-extern "C" int pd_probe_xcds(int32_t* xcds) {
-  pd::clear_error();
-  if (!xcds) return pd::fail(PD_EINVAL, "null output pointer");
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    (void)hipGetLastError();
-    return pd::fail(PD_ELAUNCH, "no current HIP device (or more than 64)");
-  }
-  void* ids = nullptr;
-  if (hipGetSymbolAddress(&ids, HIP_SYMBOL(pd_xcc_ids)) != hipSuccess || !ids) {
-    const hipError_t err = hipGetLastError();
-    return pd::fail(PD_ELAUNCH, "hipGetSymbolAddress(pd_xcc_ids) failed: %s",
-                    hipGetErrorString(err));
-  }
-  hipLaunchKernelGGL(xcc_probe_kernel, dim3(kXccProbeGroups), dim3(64), 0, nullptr,
-                     static_cast<int*>(ids));
-  if (int st = launch_status("pd_probe_xcds")) return st;
-  static int host[kXccProbeGroups];
-  static std::mutex lock;
-  std::lock_guard<std::mutex> guard(lock);
-  if (hipMemcpy(host, ids, sizeof(host), hipMemcpyDeviceToHost) != hipSuccess) {
-    const hipError_t err = hipGetLastError();
-    return pd::fail(PD_ELAUNCH, "pd_probe_xcds copy failed: %s", hipGetErrorString(err));
-  }
-  int n = 1;
-  for (int i = 0; i < kXccProbeGroups; ++i) n = host[i] + 1 > n ? host[i] + 1 : n;
-  // Round-robin from one offset c: host[i] == (i + c) % n for every i.
-  const int c = host[0];
-  bool round_robin = true;
-  for (int i = 0; i < kXccProbeGroups; ++i) round_robin = round_robin && host[i] == (i + c) % n;
-  const int layout = round_robin ? n : -1;
-  g_xcd_layout[dev].store(layout, std::memory_order_relaxed);
-  *xcds = layout;
-  return PD_OK;
-}
-
 // ------------------------------------------------ allocation-free decode
 // The split workspace of pd_matched_decode_noalloc lives in this file-scope
 // device array: partials f32 [batch, num_heads, splits, head_dim] from byte 0,
@@ -1470,8 +1392,38 @@ extern "C" int pd_matched_decode_noalloc(const void* q, int64_t q_stride_b, int6
 
 namespace {
 
+// Whether pd_split_fixed runs one workgroup per partition: when the walks,
+// one per (kv head group, sequence), leave CUs of the device idle and there is
+// more than one partition.
+bool per_partition_grid(int parts, int ygrid, int batch) {
+  const int cus = device_cu_count();
+  return parts > 1 && cus > 0 && int64_t(ygrid) * batch < cus;
+}
+
+// The base / fixed-split partition kernel for one protocol, head dim and
+// kv-head grouping.
+template <int kMode>
+void launch_online_mode(int head_dim, int heads, int G, dim3 grid, hipStream_t st,
+                        const PartitionArgs& a) {
+  if (heads == 4) {
+    launch_cols_loader<64, false, kMode, 4>(padded_group(4 * G), grid, st, a);
+    return;
+  }
+  if (heads == 2) {
+    launch_cols_loader<64, false, kMode, 2>(padded_group(2 * G), grid, st, a);
+    return;
+  }
+  const int gp = padded_group(G < 16 ? G : 16);
+  switch (head_dim) {
+    case 64: launch_cols_loader<64, false, kMode>(gp, grid, st, a); break;
+    case 128: launch_cols_loader<128, false, kMode>(gp, grid, st, a); break;
+    default: launch_cols_loader<256, false, kMode>(gp, grid, st, a); break;
+  }
+}
+
 // pd_base and pd_split_fixed: the partition kernel in its base / fixed-split
-// protocol, one workgroup per (partition, kv head [, 16-head slice], sequence).
+// protocol, one workgroup per (kv head [group or 16-head slice], sequence),
+// or per (partition, kv head, sequence) for fixed splits at small grids.
 template <bool kSplitMode>
 int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const void* v,
                   const int32_t* table, int64_t tsb, int32_t width, const int32_t* lengths,
@@ -1509,29 +1461,24 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
                   int(tsb), width, lengths, accums, denoms,
                   nullptr, static_cast<uint16_t*>(out), maxima, num_heads, num_kv_heads, G, hs,
                   kSplitMode ? parts : 1, T, float(scale), float(scale * 1.4426950408889634)};
+  // At D = 64 a workgroup serves four or two adjacent kv heads when their
+  // query heads fit one 16-head group: a token's 128-byte rows of those heads
+  // are one contiguous read.
+  const int heads = head_dim != 64 ? 1 : pd::heads_per_workgroup(num_kv_heads, G);
+  const int ygrid = pd::walk_grid_y(num_heads, num_kv_heads, head_dim);
   // The fixed-split protocol walks each sequence in one workgroup and writes
-  // every partition of it (grid.x = 1), like the base protocol.  At D = 64 a
-  // workgroup serves four or two adjacent kv heads when their query heads fit
-  // one 16-head group: a token's 128-byte rows of those heads are one
-  // contiguous read.
-  const int heads = head_dim != 64 ? 1 : heads_per_workgroup(num_kv_heads, G);
-  const dim3 grid(1, heads > 1 ? num_kv_heads / heads : num_kv_heads * hs, batch);
+  // every partition of it (grid.x = 1), like the base protocol, when the walks
+  // fill the CUs.  With fewer (kv head, sequence) walks than CUs, it runs one
+  // workgroup per partition instead (the same bits), as the reference's
+  // _split grid does (runtime.py:111-113).
+  const bool per_part = kSplitMode && per_partition_grid(parts, ygrid, batch);
+  const dim3 grid(per_part ? parts : 1, ygrid, batch);
   a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  constexpr int kMode = kSplitMode ? kSplit : kBase;
-  if (heads == 4) {
-    launch_cols_loader<64, false, kMode, 4>(padded_group(4 * G), grid, st, a);
-    return launch_status(what);
-  }
-  if (heads == 2) {
-    launch_cols_loader<64, false, kMode, 2>(padded_group(2 * G), grid, st, a);
-    return launch_status(what);
-  }
-  const int gp = padded_group(G < 16 ? G : 16);
-  switch (head_dim) {
-    case 64: launch_cols_loader<64, false, kMode>(gp, grid, st, a); break;
-    case 128: launch_cols_loader<128, false, kMode>(gp, grid, st, a); break;
-    default: launch_cols_loader<256, false, kMode>(gp, grid, st, a); break;
+  if (per_part) {
+    launch_online_mode<kSplitPart>(head_dim, heads, G, grid, st, a);
+  } else {
+    launch_online_mode<kSplitMode ? kSplit : kBase>(head_dim, heads, G, grid, st, a);
   }
   return launch_status(what);
 }
@@ -1579,15 +1526,31 @@ extern "C" int pd_ml_merge(const float* maxima, const float* denoms, const float
   if (rows > 0x7fffffff) return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto* o = static_cast<uint16_t*>(out);
+  if (partitions <= 128) {
+    const dim3 grid(unsigned(rows), head_dim / 64);
+    if (partitions <= 16)
+      hipLaunchKernelGGL(ml_merge_kernel<16>, grid, dim3(64), 0, st, maxima, denoms, accums, o,
+                         partitions, head_dim);
+    else if (partitions <= 32)
+      hipLaunchKernelGGL(ml_merge_kernel<32>, grid, dim3(64), 0, st, maxima, denoms, accums, o,
+                         partitions, head_dim);
+    else
+      hipLaunchKernelGGL(ml_merge_kernel<48>, grid, dim3(64), 0, st, maxima, denoms, accums, o,
+                         partitions, head_dim);
+    return launch_status("pd_ml_merge");
+  }
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(ml_merge_kernel<1>, dim3(rows), dim3(64), 0, st, maxima, denoms, accums, o, partitions);
+      hipLaunchKernelGGL(ml_merge_loop_kernel<1>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                         accums, o, partitions);
       break;
     case 128:
-      hipLaunchKernelGGL(ml_merge_kernel<2>, dim3(rows), dim3(64), 0, st, maxima, denoms, accums, o, partitions);
+      hipLaunchKernelGGL(ml_merge_loop_kernel<2>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                         accums, o, partitions);
       break;
     default:
-      hipLaunchKernelGGL(ml_merge_kernel<4>, dim3(rows), dim3(64), 0, st, maxima, denoms, accums, o, partitions);
+      hipLaunchKernelGGL(ml_merge_loop_kernel<4>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                         accums, o, partitions);
       break;
   }
   return launch_status("pd_ml_merge");

@@ -1,5 +1,6 @@
 // Host-only parts of the C ABI: error reporting, the split-KV planner and the
 // metadata content check.  No HIP calls in this file.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -96,6 +97,71 @@ extern "C" int pd_make_plan(int32_t max_batch, int32_t num_heads, int32_t num_kv
   out->lse_lanes = int32_t(std::min<int64_t>(padded, 128 / merge_rows));
   out->sm_count = sm_count;
   out->is_explicit = num_splits ? 1 : 0;
+  return PD_OK;
+}
+
+// Small-batch split of the base and fixed-split protocols.  The walks of
+// pd_base / pd_split_fixed run one workgroup per (kv head group, sequence),
+// and one workgroup streams about 76 GB/s, so a batch with fewer walks than
+// half the CUs leaves most of the device idle.  Such a batch is cut into
+// `chunks` partitions of `chunk_tokens` tokens (a multiple of 16384 / head_dim)
+// per sequence, about sm_count / walks of them, at most 128 and at most one
+// per 16384 / head_dim tokens of the table width: run through pd_split_fixed
+// (one workgroup per partition) and merged by pd_ml_merge.  The walks are
+// counted for the batch rounded up to a power of two, so that a batch padded
+// up to a graph bucket of the same power of two gets the same plan.
+extern "C" int pd_plan_chunks(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t table_width, int32_t sm_count,
+                              int32_t* chunks, int32_t* chunk_tokens) {
+  pd::clear_error();
+  if (chunks == nullptr || chunk_tokens == nullptr)
+    return pd::fail(PD_EINVAL, "pd_plan_chunks: null output");
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0)
+    return pd::fail(PD_EINVAL, "batch and head counts must be positive");
+  if (!pd::valid_head_dim(head_dim))
+    return pd::fail(PD_EINVAL, "custom decode supports head_dim 64, 128, or 256");
+  if (num_heads % num_kv_heads)
+    return pd::fail(PD_EINVAL, "query heads must be divisible by KV heads");
+  if (table_width < 1 || table_width >= (1 << 22))
+    return pd::fail(PD_EINVAL, "table width must be in [1, 2^22)");
+  if (sm_count < 1) return pd::fail(PD_EINVAL, "positive SM count required");
+  int64_t rounded = 1;
+  while (rounded < batch) rounded <<= 1;
+  const int64_t walks = rounded * pd::walk_grid_y(num_heads, num_kv_heads, head_dim);
+  const int64_t tile = 16384 / head_dim;
+  const int64_t tiles = ceil_div(int64_t(table_width) * pd::kPageSize, tile);
+  const int64_t want = std::min<int64_t>(std::min<int64_t>(sm_count / walks, 128), tiles);
+  if (want < 2) {
+    *chunks = 1;
+    *chunk_tokens = int32_t(int64_t(table_width) * pd::kPageSize);
+    return PD_OK;
+  }
+  const int64_t per = ceil_div(tiles, want);
+  *chunks = int32_t(ceil_div(tiles, per));
+  *chunk_tokens = int32_t(per * tile);
+  return PD_OK;
+}
+
+// Bound on batch * num_heads * chunks over every batch <= max_batch and every
+// table width: pd_plan_chunks never returns more than sm_count / walks chunks.
+extern "C" int pd_chunk_rows(int32_t max_batch, int32_t num_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t sm_count, int64_t* rows) {
+  pd::clear_error();
+  if (rows == nullptr) return pd::fail(PD_EINVAL, "pd_chunk_rows: null output");
+  if (max_batch <= 0 || num_heads <= 0 || num_kv_heads <= 0)
+    return pd::fail(PD_EINVAL, "batch and head counts must be positive");
+  if (!pd::valid_head_dim(head_dim))
+    return pd::fail(PD_EINVAL, "custom decode supports head_dim 64, 128, or 256");
+  if (num_heads % num_kv_heads)
+    return pd::fail(PD_EINVAL, "query heads must be divisible by KV heads");
+  if (sm_count < 1) return pd::fail(PD_EINVAL, "positive SM count required");
+  const int64_t y = pd::walk_grid_y(num_heads, num_kv_heads, head_dim);
+  int64_t best = 0;
+  for (int64_t b = 1; b <= max_batch && b * y * 2 <= sm_count; ++b) {
+    const int64_t chunks = std::min<int64_t>(sm_count / (b * y), 128);
+    best = std::max(best, b * num_heads * chunks);
+  }
+  *rows = best;
   return PD_OK;
 }
 

@@ -33,7 +33,6 @@ SIGNATURES = {
     "pd_partition": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
                      _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_lse_merge": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
-    "pd_probe_xcds": [ctypes.POINTER(_i32)],
     "pd_matched_decode": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                           _i32, _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_matched_decode_noalloc": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp,
@@ -43,6 +42,9 @@ SIGNATURES = {
     "pd_split_fixed": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp,
                        _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_ml_merge": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
+    "pd_plan_chunks": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32),
+                       ctypes.POINTER(_i32)],
+    "pd_chunk_rows": [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i64)],
     "pd_store_kv": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _vp],
     "pd_store_kv_pages": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64,
                           _i32, _vp, _i32, _i32, _i32, _i32, _vp],
@@ -119,22 +121,6 @@ def partition(q, k, v, tables, lengths, partials, lse, num_kv_heads, splits, tok
                          tokens_per_split, tile_tokens, scale, stream_handle(q.device)), L)
 
 
-_probed = {}
-
-
-def probe_xcds(device):
-    """XCD count of ``device`` when its workgroups are dealt round-robin to its XCDs, else
-    -1 (pd_probe_xcds; once per device, never during stream capture)."""
-    index = torch.device(device).index
-    index = torch.cuda.current_device() if index is None else index
-    if index not in _probed:
-        count = _i32(0)
-        with torch.cuda.device(index):
-            check(lib().pd_probe_xcds(ctypes.byref(count)))
-        _probed[index] = count.value
-    return _probed[index]
-
-
 def matched_decode(q, k, v, tables, lengths, partials, lse, counters, out, num_kv_heads, splits,
                    tokens_per_split, tile_tokens, scale, library=None):
     b, h, d = q.shape
@@ -192,6 +178,23 @@ def ml_merge(maxima, denoms, accums, out, batch, library=None):
     L = library or lib()
     check(L.pd_ml_merge(maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(),
                         out.data_ptr(), batch, h, d, parts, stream_handle(out.device)), L)
+
+
+def plan_chunks(batch, num_heads, num_kv_heads, head_dim, table_width, sm_count):
+    """(chunks, chunk_tokens) of pd_plan_chunks: the small-batch split of the base and
+    fixed-split protocols, chunks == 1 when the backend runs as it is."""
+    chunks, tokens = _i32(0), _i32(0)
+    check(lib().pd_plan_chunks(batch, num_heads, num_kv_heads, head_dim, table_width, sm_count,
+                               ctypes.byref(chunks), ctypes.byref(tokens)))
+    return chunks.value, tokens.value
+
+
+def chunk_rows(max_batch, num_heads, num_kv_heads, head_dim, sm_count):
+    """Chunk-workspace rows that serve every call of pd_plan_chunks (pd_chunk_rows)."""
+    rows = _i64(0)
+    check(lib().pd_chunk_rows(max_batch, num_heads, num_kv_heads, head_dim, sm_count,
+                              ctypes.byref(rows)))
+    return rows.value
 
 
 def store_kv(key, value, k_cache, v_cache, slot_mapping):

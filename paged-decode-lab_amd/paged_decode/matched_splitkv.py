@@ -45,10 +45,6 @@ def allocate_matched_resources(spec, device, *, num_splits=0, fused=False):
         raise ValueError("matched resources require CUDA")
     plan = make_splitkv_plan(spec, torch.cuda.get_device_properties(device).multi_processor_count,
                              num_splits=num_splits)
-    if fused:
-        # XCD placement of the fused single-tile launch (once per device, here, outside
-        # any stream capture).
-        _native.probe_xcds(device)
     shape = (spec.max_batch, spec.num_heads, plan.splits)
     return MatchedResources(
         spec, plan,

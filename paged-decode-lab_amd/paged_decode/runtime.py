@@ -5,13 +5,26 @@ Mirrors runtime.py of the reference (src/paged_decode/runtime.py:15-117):
 ``paged_decode`` and the host-only ``_validate`` contract with the same error
 messages.  Kernels are the HIP ones in libpaged_decode.so.
 
-Tensor CONTENTS are trusted on the hot path.  Call validate_device_metadata
-once for externally supplied tables; the engine's scheduler owns its metadata.
-A call allocates nothing, never synchronizes and never reads device memory on
-the host, so it can be captured into a hipGraph (torch.cuda.graph) after the
+The launches never look at tensor contents: page ids and lengths are taken as
+given.  Tables that come from outside a scheduler should be checked once with
+validate_device_metadata, which does read them (and synchronizes).  A call
+allocates nothing, never synchronizes and never reads device memory on the
+host, so it can be captured into a hipGraph (torch.cuda.graph) after the
 resources are allocated and replayed with new lengths, pages and KV contents.
+
+Small batches.  hip_base and hip_splitk walk each sequence in one workgroup per
+kv head group.  When a batch has fewer such walks than half of the device's
+CUs, paged_decode cuts each sequence's table width into chunks
+(pd_plan_chunks), runs the fixed-split partition over them (one workgroup per
+chunk) into the resources' chunk workspace and merges the chunks into the
+output (pd_ml_merge): the same attention with other float32 rounding, within
+the one-ulp parity gate of either backend's oracle.  The cut depends on the
+batch only through its next power of two and on the capacity, not the live
+table width, so the decode graph of a padded batch bucket gives the live rows
+the bits of the eager call.  The chunk workspace has no counterpart in the
+reference; resources built without it take the walk.
 """
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 import math
 
 import torch
@@ -27,6 +40,17 @@ class Resources:
     maxima: torch.Tensor | None = None
     denoms: torch.Tensor | None = None
     accums: torch.Tensor | None = None
+    # Small-batch chunk workspace (flat float32: (m, l) per chunk row, D accumulators
+    # per row) and the CU count it was sized for; None / 0 when no batch needs it.
+    chunk_maxima: torch.Tensor | None = None
+    chunk_denoms: torch.Tensor | None = None
+    chunk_accums: torch.Tensor | None = None
+    sm_count: int = 0
+    _chunk_plans: dict = field(default_factory=dict, repr=False, compare=False)
+
+
+def _device_cus(device):
+    return torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
 
 
 def allocate_resources(spec, device, backend="hip_splitk"):
@@ -42,7 +66,43 @@ def allocate_resources(spec, device, backend="hip_splitk"):
         result.maxima = torch.empty(shape, device=device, dtype=torch.float32)
         result.denoms = torch.empty(shape, device=device, dtype=torch.float32)
         result.accums = torch.empty((*shape, spec.head_dim), device=device, dtype=torch.float32)
+    if torch.device(device).type == "cuda":
+        result.sm_count = _device_cus(device)
+        rows = _native.chunk_rows(spec.max_batch, spec.num_heads, spec.num_kv_heads,
+                                  spec.head_dim, result.sm_count)
+        if rows:
+            result.chunk_maxima = torch.empty(rows, device=device, dtype=torch.float32)
+            result.chunk_denoms = torch.empty(rows, device=device, dtype=torch.float32)
+            result.chunk_accums = torch.empty(rows * spec.head_dim, device=device,
+                                              dtype=torch.float32)
     return result
+
+
+def _chunk_plan(resources, batch, width):
+    """(chunks, chunk_tokens) for a call of ``batch`` sequences over a table of ``width``
+    pages, or None when the backend runs as it is (a batch that fills the CUs, or resources
+    without a chunk workspace large enough).  The cut is planned at the capacity's table
+    width and runs the chunks that cover ``width`` pages, so that a sequence gets the
+    same bits from the live table as from the capacity-wide one a graph was captured with
+    (pd_plan_chunks)."""
+    key = (batch, width)
+    plans = resources._chunk_plans
+    if key not in plans:
+        spec, plan = resources.spec, None
+        workspace = (resources.chunk_maxima, resources.chunk_denoms, resources.chunk_accums)
+        if resources.sm_count > 0 and all(
+                t is not None and t.dtype == torch.float32 and t.is_contiguous()
+                and t.device == resources.out.device for t in workspace):
+            full, tokens = _native.plan_chunks(batch, spec.num_heads, spec.num_kv_heads,
+                                               spec.head_dim, spec.table_width,
+                                               resources.sm_count)
+            chunks = -(-width * 256 // tokens)
+            rows = batch * spec.num_heads * chunks
+            if (full > 1 and workspace[0].numel() >= rows and workspace[1].numel() >= rows
+                    and workspace[2].numel() >= rows * spec.head_dim):
+                plan = (chunks, tokens)
+        plans[key] = plan
+    return plans[key]
 
 
 def validate_device_metadata(table, lengths, num_pages, max_context_len):
@@ -96,7 +156,7 @@ def _validate(q, k, v, tables, lengths, resources, backend, scale):
         raise ValueError("K/V storage must be 16-byte aligned")
     if tables.ndim != 2 or tables.shape[0] != batch or tables.stride(1) != 1:
         raise ValueError("block table must have shape [batch,capacity] and contiguous rows")
-    # During eager execution the scheduler provides only the live table width.
+    # An eager caller may pass a table narrower than the capacity (its live pages only).
     if not 0 < tables.shape[1] <= spec.table_width:
         raise ValueError("block table width outside configured capacity")
     if lengths.shape != (batch,) or not lengths.is_contiguous():
@@ -118,17 +178,32 @@ def _validate(q, k, v, tables, lengths, resources, backend, scale):
 
 
 def paged_decode(q, k, v, tables, lengths, *, resources, backend="hip_base", scale=None):
-    """Return borrowed [B,H,D] output. Next launch using resources overwrites it.
+    """Attention of one query token per sequence; returns ``resources.out[:B]``.
 
-    Resources must not overlap live inputs or be used concurrently across streams.
-    Live table entries must be valid pages; 0 <= lengths <= max_context_len and
-    ceil(length/256) <= table width. Padding table entries may contain -1.
+    The returned tensor is a view of the resources' output buffer, so the next call with
+    the same resources overwrites it.  The resources may not share memory with the inputs,
+    and two streams may not use them at once.  Contract on contents (not checked here):
+    every live table entry names a page of K/V, each length lies in [0, max_context_len]
+    and needs at most the table's width of pages; entries past a row's live pages may be
+    -1.
     """
     scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     backend = canonical_backend(backend)
     _validate(q, k, v, tables, lengths, resources, backend, scale)
     spec = resources.spec
     b = q.shape[0]
+    chunked = _chunk_plan(resources, b, tables.shape[1])
+    if chunked is not None:
+        chunks, tokens = chunked
+        rows = b * spec.num_heads * chunks
+        shape = (b, spec.num_heads, chunks)
+        maxima = resources.chunk_maxima[:rows].view(shape)
+        denoms = resources.chunk_denoms[:rows].view(shape)
+        accums = resources.chunk_accums[:rows * spec.head_dim].view(*shape, spec.head_dim)
+        _native.split_fixed(q, k, v, tables, lengths, maxima, denoms, accums, spec.num_kv_heads,
+                            chunks, tokens, scale)
+        _native.ml_merge(maxima, denoms, accums, resources.out, b)
+        return resources.out[:b]
     if backend == "hip_base":
         _native.base(q, k, v, tables, lengths, resources.out, spec.num_kv_heads, scale)
     else:

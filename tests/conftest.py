@@ -21,7 +21,7 @@ def pytest_terminal_summary(terminalreporter):
     if not RECORDS:
         return
     keys = ("max_ulps_sizable", "one_ulp", "beyond_one_ulp", "max_abs_vs_oracle", "max_abs_vs_dense",
-            "rmse_vs_dense", "max_abs")
+            "rmse_vs_dense", "max_abs", "pool_pages")
     rows = {}
     for test, _, stats in RECORDS:
         module = test.split("::")[0].rsplit("/", 1)[-1] or "?"

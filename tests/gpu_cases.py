@@ -16,6 +16,25 @@ def to_np(t):
     return t.detach().float().cpu().numpy()
 
 
+def poison(*tensors):
+    """Fills float tensors with NaN (the reference's check that a launch writes what it
+    should, tools/resident_experiment.py:117-121): a slot a kernel should have written but
+    did not then shows as NaN in the output or the workspace."""
+    for t in tensors:
+        if t is not None:
+            t.fill_(float("nan"))
+
+
+WORKSPACE_FIELDS = ("out", "partials", "lse", "maxima", "denoms", "accums", "chunk_maxima",
+                    "chunk_denoms", "chunk_accums")
+
+
+def poison_workspace(res):
+    """NaN into the output and every float workspace of paged_decode or matched_decode
+    resources (never the fused counters, which must stay zero between calls)."""
+    poison(*(getattr(res, name, None) for name in WORKSPACE_FIELDS))
+
+
 def assert_within_one_ulp(actual, expected, where="", ambiguity=None):
     """Parity gate of tests/parity.py (one bf16 ulp beyond the oracle's rounding-ambiguity
     bound, at most 1% of outputs beyond one ulp)."""

@@ -23,8 +23,9 @@ import torch
 if not torch.cuda.is_available():
     pytest.skip("needs an MI355X GPU", allow_module_level=True)
 
-from gpu_cases import (assert_close_dense, assert_within_one_ulp, host_rows, pooled_case,
-                       to_np, torch_dense)
+from gpu_cases import (assert_close_dense, assert_within_one_ulp, host_rows, poison_workspace,
+                       pooled_case, to_np, torch_dense)
+from parity import record
 from oracle import matched as OM
 from oracle import splitk as OS
 from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
@@ -38,10 +39,15 @@ PAGE_BYTES = 256 * 8 * 128 * 2
 
 
 def _sweep_pool_pages():
-    """The 200 GB pool (K and V), capped at 80% of the free device memory."""
+    """The 200 GB pool (K and V), capped at 80% of the free device memory.  A device with
+    250 GB free (an MI355X has 288 GB) must hold the whole pool; the size used goes into the
+    run's parity summary (pool_pages)."""
     free, _ = torch.cuda.mem_get_info()
     pages = min(SWEEP["pool_pages"], int(0.8 * free) // (2 * PAGE_BYTES))
+    if free >= 250e9:
+        assert pages == SWEEP["pool_pages"], f"{free / 1e9:.0f} GB free, pool cut to {pages}"
     print(f"bandwidth-sweep pool: {pages} pages per cache ({2 * pages * PAGE_BYTES / 1e9:.1f} GB)")
+    record("bandwidth-sweep pool", pool_pages=pages)
     return pages
 
 
@@ -105,7 +111,9 @@ def _check_exact_properties(call, q, k, v, table, lens):
     return first
 
 
-def _check_graph_replay(call, q, k, v, table, lens):
+def _check_graph_replay(call, reset, q, k, v, table, lens):
+    """Graph replays with new lengths equal eager calls; ``reset`` NaN-poisons the output
+    and workspaces (outside the capture) before every replay and eager call."""
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     live = lens.clone()
@@ -119,8 +127,10 @@ def _check_graph_replay(call, q, k, v, table, lens):
     # New lengths stay within each row's live pages (tensor contents are trusted).
     for values in (live // 3, torch.clamp(live - 255, min=0), live):
         lens.copy_(values)
+        reset()
         graph.replay()
         captured = out.clone()
+        reset()
         eager = call(q, k, v, table, lens).clone()
         assert torch.equal(_bits(captured), _bits(eager)), "graph replay"
     lens.copy_(live)
@@ -133,6 +143,7 @@ def test_bandwidth_sweep_matched_full_size():
     spec = DecodeSpec(SWEEP["batch"], SWEEP["hq"], SWEEP["hkv"], SWEEP["dim"], SWEEP["capacity"])
     res = allocate_matched_resources(spec, "cuda")
     assert res.plan.splits == 1 and res.plan.tokens_per_split == 32768
+    poison_workspace(res)
 
     def call(*args):
         return matched_decode(*args, resources=res)
@@ -148,7 +159,7 @@ def test_bandwidth_sweep_matched_full_size():
     out = call(*g)
     assert_within_one_ulp(out[rows], expected, f"sweep rows {rows}", bound)
     np.testing.assert_allclose(to_np(res.lse[rows]), lse, atol=2e-5, rtol=1e-6)
-    _check_graph_replay(call, *g)
+    _check_graph_replay(call, lambda: poison_workspace(res), *g)
 
 
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
@@ -158,6 +169,7 @@ def test_bandwidth_sweep_paged_backends_full_size(backend):
                     _sweep_pool_pages(), seed=65)
     spec = DecodeSpec(SWEEP["batch"], SWEEP["hq"], SWEEP["hkv"], SWEEP["dim"], SWEEP["capacity"])
     res = allocate_resources(spec, "cuda", backend)
+    poison_workspace(res)
 
     def call(*args):
         return paged_decode(*args, resources=res, backend=backend)
@@ -171,7 +183,7 @@ def test_bandwidth_sweep_paged_backends_full_size(backend):
     else:
         expected = OS.ml_merge(*OS.split_partitions(*host, spec.partitions))
     assert_within_one_ulp(call(*g)[rows], expected, f"{backend} sweep rows {rows}")
-    _check_graph_replay(call, *g)
+    _check_graph_replay(call, lambda: poison_workspace(res), *g)
 
 
 @pytest.mark.parametrize("dim,hq,hkv", [(64, 16, 16), (256, 32, 4)])
@@ -185,6 +197,7 @@ def test_edge_coverage_full_batch_all_backends(dim, hq, hkv):
     empty = torch.from_numpy(lengths == 0).cuda()
     for splits in (0, 3, 6):
         res = allocate_matched_resources(spec, "cuda", num_splits=splits)
+        poison_workspace(res)
         out = matched_decode(*g, resources=res)
         assert_close_dense(out, dense)
         assert torch.count_nonzero(out[empty]) == 0
@@ -194,6 +207,7 @@ def test_edge_coverage_full_batch_all_backends(dim, hq, hkv):
         assert_within_one_ulp(out[rows], expected, f"matched {plan.splits} splits", bound)
     for backend in ("hip_base", "hip_splitk"):
         res = allocate_resources(spec, "cuda", backend)
+        poison_workspace(res)
         out = paged_decode(*g, resources=res, backend=backend)
         assert_close_dense(out, dense)
         assert torch.count_nonzero(out[empty]) == 0

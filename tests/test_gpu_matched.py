@@ -12,8 +12,8 @@ if not torch.cuda.is_available():
     pytest.skip("needs an MI355X GPU", allow_module_level=True)
 
 from cases import make_case, poison_tails
-from gpu_cases import (assert_close_dense, assert_within_one_ulp, to_gpu, to_np,
-                       torch_dense)
+from gpu_cases import (assert_close_dense, assert_within_one_ulp, poison, poison_workspace,
+                       to_gpu, to_np, torch_dense)
 from oracle import matched as OM
 from paged_decode import _native
 from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
@@ -31,6 +31,7 @@ def oracle_for(case, plan, scale=None):
 def run(case, spec, num_splits=0, scale=None):
     g = to_gpu(case)
     res = allocate_matched_resources(spec, "cuda", num_splits=num_splits)
+    poison_workspace(res)
     out = matched_decode(*g, resources=res, scale=scale)
     torch.cuda.synchronize()
     return g, res, out
@@ -66,9 +67,9 @@ def test_d256_fixed_1024_token_partitions():
     """Same kernels with 1024-token partitions (the fixed-partition geometry)."""
     case = make_case([2064], 16, 4, 256, seed=20261105, capacity=2112)
     g = to_gpu(case)
-    partials = torch.empty((1, 16, 3, 256), device="cuda", dtype=torch.float32)
-    lse = torch.empty((1, 16, 3), device="cuda", dtype=torch.float32)
-    out = torch.empty((1, 16, 256), device="cuda", dtype=torch.bfloat16)
+    partials = torch.full((1, 16, 3, 256), float("nan"), device="cuda", dtype=torch.float32)
+    lse = torch.full((1, 16, 3), float("nan"), device="cuda", dtype=torch.float32)
+    out = torch.full((1, 16, 256), float("nan"), device="cuda", dtype=torch.bfloat16)
     _native.partition(*g, partials, lse, 4, 3, 1024, 64, 256 ** -0.5)
     _native.lse_merge(partials, lse, out, 4)
     torch.cuda.synchronize()
@@ -111,6 +112,7 @@ def test_graph_replay_and_empty_partitions():
         k.normal_()
         v.normal_()
         table.copy_(table.flip(1))
+        poison_workspace(res)
         graph.replay()
         captured = out.clone()
         torch.cuda.synchronize()
@@ -118,6 +120,7 @@ def test_graph_replay_and_empty_partitions():
         expected, _, _, bound, _ = oracle_for(host, res.plan)
         assert_within_one_ulp(captured, expected, f"replay {values}", bound)
         assert_close_dense(captured, torch_dense(*g))
+        poison_workspace(res)
         eager = matched_decode(*g, resources=res)
         torch.testing.assert_close(captured, eager, atol=0, rtol=0)
         if not any(values):
@@ -150,6 +153,8 @@ def test_fused_decode_matches_two_launches(lengths, hq, hkv, dim, cap, splits):
                                      num_splits=splits, fused=True)
     two = _two_kernel_resources(res)
     for _ in range(3):
+        poison_workspace(res)
+        poison_workspace(two)
         fused = matched_decode(*g, resources=res).clone()
         split = matched_decode(*g, resources=two).clone()
         torch.cuda.synchronize()
@@ -157,34 +162,6 @@ def test_fused_decode_matches_two_launches(lengths, hq, hkv, dim, cap, splits):
         assert torch.count_nonzero(res.counters) == 0
         assert torch.equal(_bits(fused), _bits(split))
         assert torch.equal(_bits(res.partials), _bits(two.partials))
-
-
-@pytest.mark.parametrize("lengths,hq,hkv,dim,cap", [
-    ([500, 0, 1300], 12, 3, 128, 2048),          # 9 groups: XCDs hold 2, 1, 1, ... groups
-    ([2064], 16, 4, 256, 2112),                  # the headline: 4 groups on 4 XCDs
-    ([17] * 20, 8, 8, 64, 256)])                 # 160 groups, 1 split each
-def test_xcd_local_fused_decode(lengths, hq, hkv, dim, cap):
-    """Single-tile plans on a device whose workgroups are dealt round-robin to its XCDs run
-    the XCD-local fused launch (every split of a group on one XCD).  Outputs, partials and
-    LSEs equal the two launches bit for bit, and no workgroup reports a placement other
-    than the one the grid assumes (word 1 of each group's counter line stays 0)."""
-    xcds = _native.probe_xcds("cuda")
-    assert xcds == -1 or 1 <= xcds <= 16
-    if xcds < 1:
-        pytest.skip("this device does not deal workgroups round-robin to its XCDs")
-    g = to_gpu(make_case(lengths, hq, hkv, dim, seed=44, capacity=cap))
-    res = allocate_matched_resources(DecodeSpec(len(lengths), hq, hkv, dim, cap), "cuda",
-                                     fused=True)
-    assert res.plan.tokens_per_split == res.plan.tile_tokens
-    two = _two_kernel_resources(res)
-    for _ in range(3):
-        fused = matched_decode(*g, resources=res).clone()
-        split = matched_decode(*g, resources=two).clone()
-        torch.cuda.synchronize()
-        assert torch.count_nonzero(res.counters) == 0
-        assert torch.equal(_bits(fused), _bits(split))
-        assert torch.equal(_bits(res.partials), _bits(two.partials))
-        assert torch.equal(_bits(res.lse), _bits(two.lse))
 
 
 def test_fused_counters_return_to_zero_across_graph_replays():
@@ -203,6 +180,7 @@ def test_fused_counters_return_to_zero_across_graph_replays():
             out = matched_decode(*g, resources=res)
     expected = matched_decode(*g, resources=_two_kernel_resources(res)).clone()
     for _ in range(5):
+        poison_workspace(res)
         graph.replay()
         torch.cuda.synchronize()
         assert torch.count_nonzero(res.counters) == 0
@@ -274,6 +252,7 @@ def test_custom_scale_and_strided_query():
     strided = wide[:, 1:9]            # stride(0) = 1280, stride(1) = 128
     assert not strided.is_contiguous()
     res = allocate_matched_resources(DecodeSpec(3, 8, 2, 128, 2048), "cuda")
+    poison_workspace(res)
     out = matched_decode(strided, k, v, table, lengths, resources=res, scale=0.0625)
     torch.cuda.synchronize()
     check_all(case, (q, k, v, table, lengths), res, out, scale=0.0625)
@@ -307,6 +286,7 @@ def test_d256_tile_counts_of_the_loader_kernel(fused):
     res = allocate_matched_resources(DecodeSpec(len(lengths), 16, 4, 256, 512), "cuda",
                                      num_splits=1, fused=fused)
     assert res.plan.tokens_per_split == 512
+    poison_workspace(res)
     out = matched_decode(*g, resources=res)
     torch.cuda.synchronize()
     check_all(case, g, res, out, where=f"fused={fused}")
@@ -333,8 +313,8 @@ def test_d256_partials_of_a_sequence_alone_and_in_a_batch(splits, tokens, length
     g = to_gpu(case)
 
     def partition(qq, tt, ll):
-        partials = torch.empty((qq.shape[0], hq, splits, 256), device="cuda")
-        lse = torch.empty((qq.shape[0], hq, splits), device="cuda")
+        partials = torch.full((qq.shape[0], hq, splits, 256), float("nan"), device="cuda")
+        lse = torch.full((qq.shape[0], hq, splits), float("nan"), device="cuda")
         _native.partition(qq, g[1], g[2], tt, ll, partials, lse, hkv, splits, tokens, 64,
                           256 ** -0.5)
         return partials, lse
@@ -367,8 +347,8 @@ def test_single_tile_and_multi_tile_kernels_agree_on_one_tile(dim, hq, hkv):
     g = to_gpu((q, k, v, table, lens))
     out = {}
     for tokens in (tile, 2 * tile):
-        partials = torch.empty((len(lengths), hq, 1, dim), device="cuda")
-        lse = torch.empty((len(lengths), hq, 1), device="cuda")
+        partials = torch.full((len(lengths), hq, 1, dim), float("nan"), device="cuda")
+        lse = torch.full((len(lengths), hq, 1), float("nan"), device="cuda")
         _native.partition(*g, partials, lse, hkv, 1, tokens, tile, dim ** -0.5)
         torch.cuda.synchronize()
         out[tokens] = (partials, lse)

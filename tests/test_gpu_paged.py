@@ -2,6 +2,13 @@
 
 Restates the reference's tests/test_gpu.py:51-128 and adds oracle parity at one
 bf16 ulp against oracle/splitk.py (the reference kernels.py restated).
+
+Most cases run twice, once per grid of paged_decode: the walk (one workgroup per
+kv head group and sequence, resources without the chunk workspace) and the
+small-batch chunks (the table width cut into partitions of one workgroup each,
+then merged), which every batch of fewer walks than half the CUs takes.  Every
+output and workspace is NaN-poisoned before a call, as the reference does
+(tools/resident_experiment.py:117-121).
 """
 import numpy as np
 import pytest
@@ -11,14 +18,34 @@ if not torch.cuda.is_available():
     pytest.skip("needs an MI355X GPU", allow_module_level=True)
 
 from cases import make_case, poison_tails
-from gpu_cases import assert_close_dense, assert_within_one_ulp, to_gpu, to_np, torch_dense
+from gpu_cases import (assert_close_dense, assert_within_one_ulp, poison, poison_workspace,
+                       to_gpu, to_np, torch_dense)
 from oracle import splitk as OS
-from paged_decode.runtime import allocate_resources, paged_decode, validate_device_metadata
+from paged_decode import _native
+from paged_decode.runtime import (_chunk_plan, allocate_resources, paged_decode,
+                                  validate_device_metadata)
 from paged_decode.spec import DecodeSpec, canonical_backend
 
 pytestmark = pytest.mark.gpu
 
 BACKENDS = ["hip_base", "hip_splitk", "triton_base", "triton_splitk"]
+GRIDS = ["walk", "chunks"]
+
+
+def resources_for(spec, backend, grid):
+    """Resources whose calls take ``grid``: "walk" drops the chunk workspace (so every
+    batch takes the walk), "chunks" keeps it.  Output and workspaces are NaN."""
+    res = allocate_resources(spec, "cuda", backend)
+    if grid == "walk":
+        res.chunk_maxima = res.chunk_denoms = res.chunk_accums = None
+    poison_workspace(res)
+    return res
+
+
+def assert_grid(res, g, grid):
+    """The call of case ``g`` on ``res`` takes ``grid``."""
+    chunked = _chunk_plan(res, g[0].shape[0], g[3].shape[1]) is not None
+    assert chunked == (grid == "chunks"), f"expected the {grid} grid"
 
 
 def oracle_for(case, backend, spec, scale=None):
@@ -27,9 +54,10 @@ def oracle_for(case, backend, spec, scale=None):
     return OS.ml_merge(*OS.split_partitions(*case, spec.partitions, scale=scale))
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (128, 4, 2), (64, 2, 2), (256, 8, 2)])
-def test_boundaries_gqa_and_padding(backend, dim, hq, hkv):
+def test_boundaries_gqa_and_padding(backend, dim, hq, hkv, grid):
     lengths = [0, 1, 255, 256, 257, 1023, 1024, 1025]
     q, k, v, table, lens = make_case(lengths, hq, hkv, dim, seed=19, capacity=1025)
     poison_tails(k, v, table, lens)
@@ -37,22 +65,25 @@ def test_boundaries_gqa_and_padding(backend, dim, hq, hkv):
     g = to_gpu(case)
     validate_device_metadata(g[3], g[4], len(k), 1025)
     spec = DecodeSpec(len(lengths), hq, hkv, dim, 1025)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     actual = paged_decode(*g, resources=res, backend=backend).clone()
     torch.cuda.synchronize()
     assert_close_dense(actual, torch_dense(*g))
-    assert_within_one_ulp(actual, oracle_for(case, backend, spec), backend)
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec), f"{backend} {grid}")
     assert torch.count_nonzero(actual[0]) == 0
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
 @pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (256, 4, 1), (64, 8, 2)])
-def test_graph_replay_changes_lengths_pages_and_kv(backend, dim, hq, hkv):
+def test_graph_replay_changes_lengths_pages_and_kv(backend, dim, hq, hkv, grid):
     case = make_case([255, 1023, 0], hq, hkv, dim, seed=19, capacity=2048)
     g = to_gpu(case)
     q, k, v, table, lens = g
     spec = DecodeSpec(3, hq, hkv, dim, 2048)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -68,12 +99,15 @@ def test_graph_replay_changes_lengths_pages_and_kv(backend, dim, hq, hkv):
         k.normal_()
         v.normal_()
         table.copy_(table.flip(1))
+        poison_workspace(res)
         graph.replay()
         captured = output.clone()
         torch.cuda.synchronize()
         host = (to_np(q), to_np(k), to_np(v), table.cpu().numpy(), lens.cpu().numpy())
         assert_close_dense(captured, torch_dense(*g))
-        assert_within_one_ulp(captured, oracle_for(host, backend, spec), f"replay {lengths}")
+        assert_within_one_ulp(captured, oracle_for(host, backend, spec),
+                              f"{grid} replay {lengths}")
+        poison_workspace(res)
         eager = paged_decode(*g, resources=res, backend=backend).clone()
         torch.testing.assert_close(captured, eager, atol=0, rtol=0)
 
@@ -92,37 +126,44 @@ def test_public_contract_rejects_bad_dtype_and_missing_workspace():
         allocate_resources(DecodeSpec(1, 4, 1, 64, 2048), "cuda", "flash_attn")
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", ["hip_splitk"])
 @pytest.mark.parametrize("dim", [64, 256])
-def test_non_power_of_two_split_count(dim, backend):
+def test_non_power_of_two_split_count(dim, backend, grid):
     # Three real partitions (reference tests/test_gpu.py:121-128).
     case = make_case([0, 2051, 2049, 1025], 4, 1, dim, seed=19, capacity=2051)
     g = to_gpu(case)
     spec = DecodeSpec(4, 4, 1, dim, 2051)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     actual = paged_decode(*g, resources=res, backend=backend)
     torch.cuda.synchronize()
     assert_close_dense(actual, torch_dense(*g))
     assert_within_one_ulp(actual, oracle_for(case, backend, spec))
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
-def test_eager_partial_batch_and_live_table_width(backend):
+def test_eager_partial_batch_and_live_table_width(backend, grid):
     # The scheduler may pass fewer rows than max_batch and only the live width.
     case = make_case([300, 5, 511], 8, 2, 128, seed=7, capacity=512)
     g = to_gpu(case)
     spec = DecodeSpec(6, 8, 2, 128, 4096)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     actual = paged_decode(*g, resources=res, backend=backend, scale=0.1)
     torch.cuda.synchronize()
     assert actual.shape == (3, 8, 128)
+    # Rows past the live batch are never written: they keep the NaN poison.
+    assert torch.isnan(res.out[3:].float()).all()
     assert_close_dense(actual, torch_dense(*g, scale=0.1))
     assert_within_one_ulp(actual, oracle_for(case, backend, spec, scale=0.1))
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
 @pytest.mark.parametrize("dim,hq,hkv", [(64, 16, 16), (256, 32, 4)])
-def test_edge_coverage_config_c4(backend, dim, hq, hkv):
+def test_edge_coverage_config_c4(backend, dim, hq, hkv, grid):
     rng = np.random.default_rng(404)
     lengths = rng.integers(1, 4097, size=32)
     lengths[:8] = 0
@@ -130,7 +171,8 @@ def test_edge_coverage_config_c4(backend, dim, hq, hkv):
     case = make_case(list(lengths.astype(np.int32)), hq, hkv, dim, seed=5, capacity=4096)
     g = to_gpu(case)
     spec = DecodeSpec(32, hq, hkv, dim, 4096)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     actual = paged_decode(*g, resources=res, backend=backend)
     torch.cuda.synchronize()
     assert_close_dense(actual, torch_dense(*g))
@@ -138,13 +180,16 @@ def test_edge_coverage_config_c4(backend, dim, hq, hkv):
     assert torch.count_nonzero(actual[:8]) == 0
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
-def test_context_beyond_the_prefetched_table_window(backend):
-    # hip_base walks 80 pages in one workgroup, past its 64-entry table window.
+def test_context_beyond_the_prefetched_table_window(backend, grid):
+    # The walk reads 80 pages in one workgroup, past its 128-entry table window's
+    # first half; the chunks start their windows at their own first pages.
     case = make_case([20480, 17000, 3], 4, 1, 128, seed=9, capacity=20480)
     g = to_gpu(case)
     spec = DecodeSpec(3, 4, 1, 128, 20480)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     actual = paged_decode(*g, resources=res, backend=backend)
     torch.cuda.synchronize()
     assert_close_dense(actual, torch_dense(*g))
@@ -152,9 +197,10 @@ def test_context_beyond_the_prefetched_table_window(backend):
 
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
 @pytest.mark.parametrize("dim,hq,hkv", [(128, 32, 1), (64, 24, 1), (256, 40, 2), (128, 17, 1)])
-def test_groups_larger_than_16_heads(backend, dim, hq, hkv):
+def test_groups_larger_than_16_heads(backend, dim, hq, hkv, grid):
     """A kv head with more than 16 query heads is served in 16-head slices (the reference
     grid has no group limit for these backends)."""
     lengths = [0, 1, 300, 1100]
@@ -163,16 +209,19 @@ def test_groups_larger_than_16_heads(backend, dim, hq, hkv):
     case = (q, k, v, table, lens)
     g = to_gpu(case)
     spec = DecodeSpec(len(lengths), hq, hkv, dim, 1100)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     actual = paged_decode(*g, resources=res, backend=backend).clone()
     torch.cuda.synchronize()
     assert_close_dense(actual, torch_dense(*g))
-    assert_within_one_ulp(actual, oracle_for(case, backend, spec), f"{backend} G={hq // hkv}")
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec),
+                          f"{backend} {grid} G={hq // hkv}")
     assert torch.count_nonzero(actual[0]) == 0
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
-def test_d256_tile_counts_of_the_loader_kernel(backend):
+def test_d256_tile_counts_of_the_loader_kernel(backend, grid):
     """D=256 runs cols_loader_kernel for both backends: whole contexts (base) and
     1024-token partitions (split) of 1 to 20 tiles, full and partial: the loader
     wavefronts' prologue and waits differ for one, two and more tiles."""
@@ -182,23 +231,47 @@ def test_d256_tile_counts_of_the_loader_kernel(backend):
     case = (q, k, v, table, lens)
     g = to_gpu(case)
     spec = DecodeSpec(len(lengths), 8, 2, 256, 1280)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     actual = paged_decode(*g, resources=res, backend=backend).clone()
     torch.cuda.synchronize()
     assert_close_dense(actual, torch_dense(*g))
-    assert_within_one_ulp(actual, oracle_for(case, backend, spec), backend)
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec), f"{backend} {grid}")
+
+
+def split_fixed_rows(g, hkv, parts, part, rows=None):
+    """pd_split_fixed over case ``g`` with its batch padded by empty sequences (-1 tables,
+    zero queries) to ``rows`` rows (None: as it is); the (m, l, acc) of the case's own rows.
+    The workspaces start NaN."""
+    q, k, v, table, lens = g
+    b = q.shape[0]
+    if rows is not None and rows > b:
+        q = torch.cat([q, torch.zeros((rows - b, *q.shape[1:]), device="cuda", dtype=q.dtype)])
+        table = torch.cat([table, torch.full((rows - b, table.shape[1]), -1, device="cuda",
+                                             dtype=table.dtype)])
+        lens = torch.cat([lens, torch.zeros(rows - b, device="cuda", dtype=lens.dtype)])
+    n, hq, dim = q.shape
+    maxima = torch.full((n, hq, parts), float("nan"), device="cuda")
+    denoms = torch.full_like(maxima, float("nan"))
+    accums = torch.full((n, hq, parts, dim), float("nan"), device="cuda")
+    _native.split_fixed(q, k, v, table, lens, maxima, denoms, accums, hkv, parts, part,
+                        dim ** -0.5)
+    return maxima[:b], denoms[:b], accums[:b]
 
 
 @pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (128, 8, 2), (256, 8, 2), (64, 32, 2),
-                                         (64, 8, 2), (64, 6, 6), (64, 16, 16), (64, 12, 4)])
+                                         (64, 8, 2), (64, 6, 6), (64, 16, 16), (64, 12, 4),
+                                         (256, 40, 2)])
 @pytest.mark.parametrize("tiles_per_partition", [1, 2, 3, 5])
-def test_fixed_split_walk_partition_sizes(dim, hq, hkv, tiles_per_partition):
-    """pd_split_fixed walks each sequence in one workgroup and writes every partition as
-    the walk leaves it.  Partition sizes of 1, 2, 3 and 5 tiles, lengths at and around
+def test_fixed_split_grids_and_partition_sizes(dim, hq, hkv, tiles_per_partition):
+    """pd_split_fixed runs one workgroup per partition when its walks (one workgroup per kv
+    head group and sequence) are fewer than the CUs, as here, and one walking workgroup per
+    (kv head group, sequence), writing every partition as it leaves it, when the walks fill
+    the CUs (the same sequences followed by empty ones).  Both grids must write the same
+    (m, l, acc) bits.  Partition sizes of 1, 2, 3 and 5 tiles, lengths at and around
     partition and page boundaries, the empty partitions past each sequence's end, and
-    NaN-poisoned tails: the (m, l, acc) workspace against oracle/splitk.py, and the merged
-    output at one bf16 ulp."""
-    from paged_decode import _native
+    NaN-poisoned tails: the workspace against oracle/splitk.py, and the merged output at
+    one bf16 ulp."""
     tile = 16384 // dim
     part = tiles_per_partition * tile
     cap = 4 * part + 3 * tile
@@ -209,11 +282,12 @@ def test_fixed_split_walk_partition_sizes(dim, hq, hkv, tiles_per_partition):
     case = (q, k, v, table, lens)
     g = to_gpu(case)
     parts = -(-cap // part)
-    maxima = torch.empty((len(lengths), hq, parts), device="cuda")
-    denoms = torch.empty_like(maxima)
-    accums = torch.empty((len(lengths), hq, parts, dim), device="cuda")
-    out = torch.empty((len(lengths), hq, dim), device="cuda", dtype=torch.bfloat16)
-    _native.split_fixed(*g, maxima, denoms, accums, hkv, parts, part, dim ** -0.5)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    maxima, denoms, accums = split_fixed_rows(g, hkv, parts, part)
+    walked = split_fixed_rows(g, hkv, parts, part, rows=cus)
+    for one, other in zip((maxima, denoms, accums), walked):
+        assert torch.equal(one.view(torch.int32), other.view(torch.int32))
+    out = torch.full((len(lengths), hq, dim), float("nan"), device="cuda", dtype=torch.bfloat16)
     _native.ml_merge(maxima, denoms, accums, out, len(lengths))
     torch.cuda.synchronize()
     m_ref, l_ref, a_ref = OS.split_partitions(*case, parts, part_size=part)
@@ -227,10 +301,11 @@ def test_fixed_split_walk_partition_sizes(dim, hq, hkv, tiles_per_partition):
     assert torch.count_nonzero(out[0]) == 0
 
 
+@pytest.mark.parametrize("grid", GRIDS)
 @pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
 @pytest.mark.parametrize("hq,hkv", [(2, 2), (16, 16), (8, 4), (6, 2), (16, 2), (12, 4), (10, 2),
                                     (4, 4), (16, 4), (3, 3)])
-def test_d64_kv_head_groups(backend, hq, hkv):
+def test_d64_kv_head_groups(backend, hq, hkv, grid):
     """At D=64 one workgroup serves four adjacent kv heads and their 4G query heads when
     the kv head count is a multiple of 4 and 4G <= 16 (tiles of 64 tokens of the four
     heads), else two when it is even and 2G <= 16 (128-token tiles); odd kv head counts
@@ -243,9 +318,73 @@ def test_d64_kv_head_groups(backend, hq, hkv):
     case = (q, k, v, table, lens)
     g = to_gpu(case)
     spec = DecodeSpec(len(lengths), hq, hkv, 64, 1100)
-    res = allocate_resources(spec, "cuda", backend)
+    res = resources_for(spec, backend, grid)
+    assert_grid(res, g, grid)
     actual = paged_decode(*g, resources=res, backend=backend).clone()
     torch.cuda.synchronize()
-    assert_close_dense(actual, torch_dense(*g), f"{backend} {hq}/{hkv}")
-    assert_within_one_ulp(actual, oracle_for(case, backend, spec), f"{backend} {hq}/{hkv}")
+    assert_close_dense(actual, torch_dense(*g), f"{backend} {grid} {hq}/{hkv}")
+    assert_within_one_ulp(actual, oracle_for(case, backend, spec), f"{backend} {grid} {hq}/{hkv}")
     assert torch.count_nonzero(actual[0]) == 0
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("hq,hkv,dim,cap,ctx", [(16, 4, 256, 2112, 2064),
+                                                 (32, 8, 128, 4096, 4096)])
+def test_small_batch_chunks_on_benchmark_shapes(backend, batch, hq, hkv, dim, cap, ctx):
+    """The small-batch shapes of the benchmark (D256 GQA 16/4 at context 2064, D128 GQA 32/8
+    at 4096; B = 1 and 8) take the chunks: the table width cut into ~256 / (B x kv heads)
+    partitions of one workgroup each, merged by pd_ml_merge.  The output passes the
+    backend's oracle gate (base: one online softmax over the context; splitk: 1024-token
+    partitions merged) and the dense gate, like the walk's, from NaN-poisoned workspaces."""
+    rng = np.random.default_rng(batch * 7 + dim)
+    lengths = [ctx] + [int(x) for x in rng.integers(0, ctx + 1, size=batch - 1)]
+    q, k, v, table, lens = make_case(lengths, hq, hkv, dim, seed=batch + dim, capacity=cap)
+    poison_tails(k, v, table, lens)
+    case = (q, k, v, table, lens)
+    g = to_gpu(case)
+    spec = DecodeSpec(batch, hq, hkv, dim, cap)
+    expected = oracle_for(case, backend, spec)
+    dense = torch_dense(*g)
+    outputs = {}
+    for grid in GRIDS:
+        res = resources_for(spec, backend, grid)
+        assert_grid(res, g, grid)
+        outputs[grid] = paged_decode(*g, resources=res, backend=backend).clone()
+        torch.cuda.synchronize()
+        where = f"{backend} {grid} B={batch} D{dim} {hq}/{hkv} ctx {ctx}"
+        assert_close_dense(outputs[grid], dense, where)
+        assert_within_one_ulp(outputs[grid], expected, where)
+    chunks, tokens = _chunk_plan(res, batch, g[3].shape[1])
+    print(f"B={batch} D{dim} {hq}/{hkv}: {chunks} chunks of {tokens} tokens")
+
+
+@pytest.mark.parametrize("backend", ["hip_base", "hip_splitk"])
+@pytest.mark.parametrize("hq,hkv,dim", [(16, 4, 256), (16, 16, 64), (8, 2, 128)])
+def test_chunks_do_not_depend_on_padding_or_the_live_width(backend, hq, hkv, dim):
+    """The small-batch chunks give a sequence the same bits whether it runs in the live
+    batch with the live table width (an eager engine step) or in a batch padded with empty
+    sequences up to its next power of two over capacity-wide tables (the step's decode
+    graph bucket), which run more, trailing empty, chunks."""
+    lengths = [1000, 700, 1]
+    case = make_case(lengths, hq, hkv, dim, seed=hq + dim, capacity=1000)
+    poison_tails(*case[1:])
+    g = to_gpu(case)
+    q, k, v, table, lens = g
+    spec = DecodeSpec(8, hq, hkv, dim, 2112)
+    res = resources_for(spec, backend, "chunks")
+    live = paged_decode(*g, resources=res, backend=backend).clone()
+    bucket, width = 4, spec.table_width
+    qp = torch.zeros((bucket, hq, dim), device="cuda", dtype=q.dtype)
+    qp[:3] = q
+    tp = torch.full((bucket, width), -1, device="cuda", dtype=torch.int32)
+    tp[:3, :table.shape[1]] = table
+    lp = torch.zeros(bucket, device="cuda", dtype=torch.int32)
+    lp[:3] = lens
+    assert _chunk_plan(res, 3, table.shape[1])[0] < _chunk_plan(res, bucket, width)[0]
+    poison_workspace(res)
+    padded = paged_decode(qp, k, v, tp, lp, resources=res, backend=backend).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(padded[:3].view(torch.int16), live.view(torch.int16))
+    assert torch.count_nonzero(padded[3]) == 0
+    assert_within_one_ulp(live, oracle_for(case, backend, spec), f"{backend} D{dim} {hq}/{hkv}")

@@ -7,9 +7,11 @@ boundaries, a table capacity up to 2600 tokens, NaN-poisoned tails and -1 table
 padding, sometimes a custom softmax scale, and one backend:
 * the matched protocol with the planner's plan, an explicit split count, or the
   single-launch (fused) merge, which must equal the two launches bit for bit;
-* the base protocol (hip_base) and the fixed 1024-token protocol (hip_splitk).
+* the base protocol (hip_base) and the fixed 1024-token protocol (hip_splitk),
+  alternately through the walk (resources without the chunk workspace) and through
+  whatever grid paged_decode picks (the small-batch chunks at these batches).
 Every output passes the oracle's one-ulp gate and the dense 2e-2 gate; matched
-LSEs match the oracle's.
+LSEs match the oracle's.  Outputs and workspaces start NaN-poisoned.
 """
 import numpy as np
 import pytest
@@ -19,7 +21,8 @@ if not torch.cuda.is_available():
     pytest.skip("needs an MI355X GPU", allow_module_level=True)
 
 from cases import make_case, poison_tails
-from gpu_cases import assert_close_dense, assert_within_one_ulp, to_gpu, to_np, torch_dense
+from gpu_cases import (assert_close_dense, assert_within_one_ulp, poison_workspace, to_gpu,
+                       to_np, torch_dense)
 from oracle import matched as OM
 from oracle import splitk as OS
 from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
@@ -73,11 +76,13 @@ def test_random_case(index):
     if backend.startswith("matched"):
         res = allocate_matched_resources(spec, "cuda",
                                          num_splits=c["splits"] if backend == "matched_splits" else 0)
+        poison_workspace(res)
         plan = res.plan
         out = matched_decode(*g, resources=res, scale=scale).clone()
         lse = res.lse.clone()
         if backend == "matched_fused":
             fused = allocate_matched_resources(spec, "cuda", fused=True)
+            poison_workspace(fused)
             single = matched_decode(*g, resources=fused, scale=scale)
             torch.cuda.synchronize()
             assert torch.equal(single.view(torch.int16), out.view(torch.int16)), where
@@ -88,6 +93,9 @@ def test_random_case(index):
         assert_within_one_ulp(out, expected, where, bound)
     else:
         res = allocate_resources(spec, "cuda", backend)
+        if (index // len(BACKENDS)) % 2:
+            res.chunk_maxima = res.chunk_denoms = res.chunk_accums = None   # the walk
+        poison_workspace(res)
         out = paged_decode(*g, resources=res, backend=backend, scale=scale).clone()
         torch.cuda.synchronize()
         if backend == "hip_base":

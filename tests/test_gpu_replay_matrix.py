@@ -9,7 +9,8 @@ four states:
   last page NaN;
 * three more length states, with the page table reversed on odd steps, and new
   Q, K and V each time (the last state is all zero lengths).
-At every state, for the two-launch and the single-launch (fused) decode:
+At every state, for the two-launch and the single-launch (fused) decode, with the
+output and workspaces NaN-poisoned before every replay and eager call:
 * the replayed output equals an eager call bit for bit;
 * it is within the oracle's one-ulp gate and within 2e-2 of the float32 dense
   reference (max-abs and RMSE are recorded for the run's parity summary);
@@ -24,7 +25,8 @@ import torch
 if not torch.cuda.is_available():
     pytest.skip("needs an MI355X GPU", allow_module_level=True)
 
-from gpu_cases import assert_close_dense, assert_within_one_ulp, to_np, torch_dense
+from gpu_cases import (assert_close_dense, assert_within_one_ulp, poison_workspace, to_np,
+                       torch_dense)
 from oracle import matched as OM
 from paged_decode.matched_splitkv import allocate_matched_resources, matched_decode
 from paged_decode.spec import DecodeSpec
@@ -89,10 +91,12 @@ def test_replay_matrix(hq, hkv, splits):
         for name, res in paths.items():
             graph, out = graphs[name]
             for _ in range(3):
+                poison_workspace(res)
                 graph.replay()
             torch.cuda.synchronize()
             replayed = out.clone()
             saved = (replayed, res.partials.clone(), res.lse.clone())
+            poison_workspace(res)
             eager = matched_decode(*tensors, resources=res).clone()
             where = f"Hq {hq} Hkv {hkv} splits {plan.splits} step {step} {name}"
             assert torch.equal(replayed.view(torch.int16), eager.view(torch.int16)), where
