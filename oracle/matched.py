@@ -47,7 +47,7 @@ def _cdiv(a, b):
     return -(-a // b)
 
 
-AMBIGUITY_ULPS = 128   # fp32 ulps around a bf16 rounding midpoint treated as ambiguous
+AMBIGUITY_ULPS = 32   # fp32 ulps around a bf16 rounding midpoint treated as ambiguous
 
 
 def _ambiguous_ulp(p):
@@ -69,13 +69,15 @@ def _ambiguous_ulp(p):
 
 def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile, scale=None,
                          with_ambiguity=False):
-    """Returns (partials [B,Hq,S,D] f32, lse [B,Hq,S] f32[, ambiguity [B,Hq,S,D] f32]).
+    """Returns (partials [B,Hq,S,D] f32, lse [B,Hq,S] f32[, ambiguity [B,Hq,S,D] f32,
+    ambiguous_p [B,Hq] int64]).
 
     With ``with_ambiguity`` the third result bounds how far a faithful
     implementation's normalized partial can move because of p values whose
     bf16 rounding is ambiguous (see ``_ambiguous_ulp``): the sum over those
     tokens of ulp_bf16(p) * |v|, rescaled by the same alpha factors as the
-    accumulator and divided by the denominator.
+    accumulator and divided by the denominator.  The fourth counts those p
+    values per (sequence, head) over all splits.
     """
     q = np.asarray(q, dtype=F32)
     B, Hq, D = q.shape
@@ -88,6 +90,7 @@ def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile
     partials = np.zeros((B, Hq, splits, D), dtype=F32)
     lse = np.full((B, Hq, splits), -np.inf, dtype=F32)
     ambiguity = np.zeros((B, Hq, splits, D), dtype=F32) if with_ambiguity else None
+    ambiguous_p = np.zeros((B, Hkv, G), dtype=np.int64)
     table = np.asarray(table)
     for b in range(B):
         length = int(lengths[b])
@@ -120,7 +123,9 @@ def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile
                 pv = np.matmul(bf16_round(p_[..., :nv]), vt.transpose(1, 0, 2))
                 acc = (acc * alpha[..., None] + pv).astype(F32)
                 if with_ambiguity:
-                    flips = np.matmul(_ambiguous_ulp(p_[..., :nv]), np.abs(vt).transpose(1, 0, 2))
+                    ulp = _ambiguous_ulp(p_[..., :nv])
+                    ambiguous_p[b] += np.count_nonzero(ulp, axis=-1)
+                    flips = np.matmul(ulp, np.abs(vt).transpose(1, 0, 2))
                     amb = (amb * alpha[..., None] + flips).astype(F32)
                 m = m_next
             denom = ((lanes[..., 0] + lanes[..., 2]) + (lanes[..., 1] + lanes[..., 3])).astype(F32)
@@ -132,7 +137,7 @@ def normalized_partition(q, k, v, table, lengths, splits, tokens_per_split, tile
                 lse_p = np.where(denom > 0, fma32(m, s32, ln32(safe)), F32(-np.inf))
             lse[b, :, p] = lse_p.reshape(Hq)
     if with_ambiguity:
-        return partials, lse, ambiguity
+        return partials, lse, ambiguity, ambiguous_p.reshape(B, Hq)
     return partials, lse
 
 
@@ -179,18 +184,19 @@ def matched_decode(q, k, v, table, lengths, splits, tokens_per_split, tile, lse_
 
 
 def matched_decode_with_bounds(q, k, v, table, lengths, splits, tokens_per_split, tile,
-                               lse_lanes, scale=None):
-    """Returns (out, partials, lse, out_ambiguity, partial_ambiguity).
+                               lse_lanes, scale=None, counts=False):
+    """Returns (out, partials, lse, out_ambiguity, partial_ambiguity[, ambiguous_p]).
 
     ``partial_ambiguity[b, h, p, d]`` bounds how far a faithful implementation's
     normalized partial can move because of ambiguous bf16 roundings of p, and
     ``out_ambiguity[b, h, d]`` bounds the change of the float32 output before
     its final bf16 rounding: the merge-weighted (exp(lse_p - L)) sum of the
     partial bounds.  Denominators and LSEs use the unrounded p, so they carry
-    no such term.
+    no such term.  With ``counts``, ``ambiguous_p[b, h]`` is the number of p
+    values behind row (b, h)'s bound.
     """
-    partials, lse, amb = normalized_partition(q, k, v, table, lengths, splits, tokens_per_split,
-                                              tile, scale, with_ambiguity=True)
+    partials, lse, amb, ambiguous_p = normalized_partition(
+        q, k, v, table, lengths, splits, tokens_per_split, tile, scale, with_ambiguity=True)
     out = lse_merge(partials, lse, lse_lanes)
     with np.errstate(invalid="ignore", over="ignore"):
         top = np.max(lse, axis=-1, keepdims=True)
@@ -199,6 +205,8 @@ def matched_decode_with_bounds(q, k, v, table, lengths, splits, tokens_per_split
         total = weights.sum(axis=-1, keepdims=True)
         weights = np.where(total > 0, weights / np.where(total > 0, total, 1), 0)
     out_amb = (weights[..., None] * amb).sum(axis=-2).astype(F32)
+    if counts:
+        return out, partials, lse, out_amb, amb, ambiguous_p
     return out, partials, lse, out_amb, amb
 
 

@@ -958,19 +958,20 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
 // The merge of the fixed-split protocol (kernels.py:83-100): M = max_p m_p
 // (-inf -> 0), f_p = exp(m_p - M), out = sum_p f_p acc_p / sum_p f_p l_p (a
 // zero total divides by 1).  Up to 128 partitions: one wavefront per (b, h)
-// row and 64-column chunk (grid rows x D/64), one column per lane, so a row's
-// accumulators are read by D/64 CUs at once.  Lane j loads m and l of
-// partitions j and j + 64; every accumulator load of a batch of kBatch
-// partitions is issued before the factors are computed (merge_splits), the
-// total is an xor-butterfly sum over the lanes, and acc = fma(f_p, acc_p, acc)
-// runs in partition order.  Loads past the row read zero and carry f = 0.
-template <int kBatch>
+// row and 64 E columns (grid rows x D / (64 E)), E consecutive columns per
+// lane; E = 1 spreads a row over D / 64 CUs when there are few rows.  Lane j
+// loads m and l of partitions j and j + 64; every accumulator load of a batch
+// of kBatch partitions is issued before the factors are computed
+// (merge_splits), the total is an xor-butterfly sum over the lanes, and
+// acc = fma(f_p, acc_p, acc) runs in partition order.  Loads past the row read
+// zero and carry f = 0, so neither E nor kBatch changes the result's bits.
+template <int E, int kBatch>
 __global__ void __launch_bounds__(64)
 ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
                 const float* __restrict__ accums, uint16_t* __restrict__ out, int parts, int D) {
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x;
-  const int col = blockIdx.y * 64 + lane;
+  const int col = (blockIdx.y * 64 + lane) * E;
   const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(maxima + row * parts, parts * 4);
   const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(denoms + row * parts, parts * 4);
   float m0[1], m1[1], l0[1], l1[1];
@@ -978,8 +979,8 @@ ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ deno
   buffer_load_f32<1, 0>(rm, (lane + 64) * 4, m1);
   buffer_load_f32<1, 0>(rl, lane * 4, l0);
   buffer_load_f32<1, 0>(rl, (lane + 64) * 4, l1);
-  float f0 = 0.f, f1 = 0.f, inv = 1.f, acc[1];
-  merge_splits<1, 0, kBatch>(
+  float f0 = 0.f, f1 = 0.f, inv = 1.f, acc[E];
+  merge_splits<E, 0, kBatch>(
       accums + row * parts * D, D, col, parts,
       [&] {
         const float v0 = lane < parts ? m0[0] : -INFINITY;
@@ -992,7 +993,8 @@ ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ deno
         inv = 1.f / (total > 0.f ? total : 1.f);
       },
       [&](int s0, int j) { return wave_weight(f0, f1, s0 + j); }, acc);
-  out[row * D + col] = uint16_t(bf16_bits(acc[0] * inv));
+#pragma unroll
+  for (int e = 0; e < E; ++e) out[row * D + col + e] = uint16_t(bf16_bits(acc[e] * inv));
 }
 
 // The same merge for more than 128 partitions: one wavefront per row, lane j
@@ -1527,16 +1529,31 @@ extern "C" int pd_ml_merge(const float* maxima, const float* denoms, const float
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto* o = static_cast<uint16_t*>(out);
   if (partitions <= 128) {
-    const dim3 grid(unsigned(rows), head_dim / 64);
-    if (partitions <= 16)
-      hipLaunchKernelGGL(ml_merge_kernel<16>, grid, dim3(64), 0, st, maxima, denoms, accums, o,
-                         partitions, head_dim);
-    else if (partitions <= 32)
-      hipLaunchKernelGGL(ml_merge_kernel<32>, grid, dim3(64), 0, st, maxima, denoms, accums, o,
-                         partitions, head_dim);
-    else
-      hipLaunchKernelGGL(ml_merge_kernel<48>, grid, dim3(64), 0, st, maxima, denoms, accums, o,
-                         partitions, head_dim);
+    // One wavefront per row (E = D / 64 columns per lane, 16-byte aligned
+    // accumulators) once the rows alone give 2048 wavefronts or more; otherwise a
+    // row's 64-column chunks on as many wavefronts.  Load batches of 4 to 48
+    // partitions (at most 16 of E > 1 columns).
+    const int E = rows >= 2048 && aligned16(accums) ? head_dim / 64 : 1;
+    int batch = 4;
+    while (batch < partitions && batch < (E == 1 ? 48 : 16)) batch = batch < 32 ? 2 * batch : 48;
+    const dim3 grid(unsigned(rows), head_dim / (64 * E));
+#define PD_LAUNCH_ML(EV, KB)                                                                   \
+  hipLaunchKernelGGL((ml_merge_kernel<EV, KB>), grid, dim3(64), 0, st, maxima, denoms, accums, \
+                     o, partitions, head_dim)
+    switch (E * 100 + batch) {
+      case 104: PD_LAUNCH_ML(1, 4); break;
+      case 108: PD_LAUNCH_ML(1, 8); break;
+      case 116: PD_LAUNCH_ML(1, 16); break;
+      case 132: PD_LAUNCH_ML(1, 32); break;
+      case 148: PD_LAUNCH_ML(1, 48); break;
+      case 204: PD_LAUNCH_ML(2, 4); break;
+      case 208: PD_LAUNCH_ML(2, 8); break;
+      case 216: PD_LAUNCH_ML(2, 16); break;
+      case 404: PD_LAUNCH_ML(4, 4); break;
+      case 408: PD_LAUNCH_ML(4, 8); break;
+      default: PD_LAUNCH_ML(4, 16); break;
+    }
+#undef PD_LAUNCH_ML
     return launch_status("pd_ml_merge");
   }
   switch (head_dim) {

@@ -22,14 +22,19 @@ def pytest_terminal_summary(terminalreporter):
         return
     keys = ("max_ulps_sizable", "one_ulp", "beyond_one_ulp", "max_abs_vs_oracle", "max_abs_vs_dense",
             "rmse_vs_dense", "max_abs", "pool_pages")
-    rows = {}
-    for test, _, stats in RECORDS:
+    rows, worst, worst_sizable = {}, {}, {}
+    for test, where, stats in RECORDS:
         module = test.split("::")[0].rsplit("/", 1)[-1] or "?"
         row = rows.setdefault(module, {"checks": 0})
         row["checks"] += 1
         for key in keys:
             if key in stats:
                 row[key] = max(row.get(key, float("-inf")), stats[key])
+        for kind, table in (("worst", worst), ("worst_sizable", worst_sizable)):
+            w = stats.get(kind)
+            if w and (module not in table or (w["ulps"], w["abs_diff"]) >
+                      (table[module][1]["ulps"], table[module][1]["abs_diff"])):
+                table[module] = (f"{test.split('::')[-1]} {where}", w)
     write = terminalreporter.write_line
     write("")
     write("parity summary (maxima over the passed checks of each file):")
@@ -43,3 +48,15 @@ def pytest_terminal_summary(terminalreporter):
                                           for k, v in row.items()))
     write("parity overall: " + ", ".join(f"{k}={v:.3g}" if isinstance(v, float) else f"{k}={v}"
                                          for k, v in total.items()))
+    for title, table in (("worst output beyond one ulp per file", worst),
+                         ("worst output of magnitude >= 2^-10 beyond one ulp per file",
+                          worst_sizable)):
+        if not table:
+            continue
+        write(f"{title} (A = the oracle's rounding-ambiguity bound there, allowed = A + ulp + "
+              "2^-18, ambiguous_p = ambiguous p values of its row):")
+        for module, (check, w) in sorted(table.items()):
+            write(f"  {module}: {w['ulps']} ulps, |diff| {w['abs_diff']:.3g}, A {w['bound']:.3g}, "
+                  f"allowed {w['allowed']:.3g}, oracle {w['oracle']:.4g}"
+                  + (f", ambiguous_p {w['ambiguous_p']}" if "ambiguous_p" in w else "")
+                  + f" ({check[:120]})")

@@ -18,6 +18,13 @@ the sum of that quantity over every p within 128 float32 ulps of a midpoint.
 The 2^-18 term covers float32 accumulation-order noise on outputs that are
 close to zero.  Planted protocol mistakes (forward tile walk, no bf16(p)) fail
 this gate (tests/test_oracle_matched.py::test_parity_gate_rejects_protocol_mistakes).
+
+Attribution.  Each passed check records its worst output beyond one ulp (most ulps,
+then largest difference): its ulps, |difference|, the bound A at that element, the
+allowance A + ulp + 2^-18 it met, the oracle value and, where the caller passes the
+oracle's counts, the number of ambiguous p values behind its row; and the same for
+the worst among outputs of magnitude 2^-10 or more.  An element with A = 0 passed on
+the 2^-18 floor alone (an output that cancels to near zero).
 """
 import os
 
@@ -46,7 +53,26 @@ def bf16_ulp_of(x):
     return np.where(x > 0, np.ldexp(1.0, e - 8), 0.0)
 
 
-def parity_stats(actual, expected, ambiguity=None):
+def worst_beyond_one_ulp(ulps, diff, amb, allowed, expected, ambiguous_p=None, among=None):
+    """The output beyond one ulp with the most ulps (ties: largest difference), among the
+    outputs ``among`` selects (all by default), and what admitted it; None when every such
+    output is within one ulp."""
+    beyond = ulps > 1
+    if among is not None:
+        beyond = beyond & among
+    if not beyond.any():
+        return None
+    where = np.argwhere(beyond)
+    order = np.lexsort((diff[beyond], ulps[beyond]))
+    i = tuple(int(x) for x in where[order[-1]])
+    worst = dict(ulps=int(ulps[i]), abs_diff=float(diff[i]), bound=float(amb[i]),
+                 allowed=float(allowed[i]), oracle=float(expected[i]), index=i)
+    if ambiguous_p is not None:
+        worst["ambiguous_p"] = int(np.asarray(ambiguous_p)[i[:-1]])
+    return worst
+
+
+def parity_stats(actual, expected, ambiguity=None, ambiguous_p=None):
     actual = np.asarray(actual, dtype=np.float32)
     expected = np.asarray(expected, dtype=np.float32)
     amb = np.zeros(expected.shape) if ambiguity is None else np.asarray(ambiguity, np.float64)
@@ -63,12 +89,17 @@ def parity_stats(actual, expected, ambiguity=None):
                 beyond_one_ulp=float((ulps > 1).mean()),
                 one_ulp=float((ulps == 1).mean()),
                 max_abs=float(diff.max(initial=0.0)),
-                ambiguous_elements=float((amb > 0).mean()))
+                ambiguous_elements=float((amb > 0).mean()),
+                worst=worst_beyond_one_ulp(ulps, diff, amb, allowed, expected, ambiguous_p),
+                worst_sizable=worst_beyond_one_ulp(ulps, diff, amb, allowed, expected,
+                                                   ambiguous_p, sizable))
 
 
-def assert_parity(actual, expected, where="", ambiguity=None):
-    stats = parity_stats(actual, expected, ambiguity)
+def assert_parity(actual, expected, where="", ambiguity=None, ambiguous_p=None):
+    stats = parity_stats(actual, expected, ambiguity, ambiguous_p)
     ok = stats.pop("ok")
+    worst = stats.pop("worst")
+    worst_sizable = stats.pop("worst_sizable")
     summary = ", ".join(f"{k}={v:.3g}" for k, v in stats.items())
     if not ok.all():
         i = tuple(np.argwhere(~ok)[0])
@@ -78,8 +109,9 @@ def assert_parity(actual, expected, where="", ambiguity=None):
                              f"oracle {expected[i]!r}{extra}")
     if stats["beyond_one_ulp"] > MAX_FRACTION_BEYOND_ONE_ULP:
         raise AssertionError(f"{where}: too many outputs beyond one bf16 ulp ({summary})")
-    print(f"parity {where}: {summary}")
+    print(f"parity {where}: {summary}" + (f"; worst beyond one ulp {worst}" if worst else ""))
     record(where, max_ulps_sizable=stats["max_ulps_sizable"],
            beyond_one_ulp=stats["beyond_one_ulp"],
-           one_ulp=stats["one_ulp"], max_abs_vs_oracle=stats["max_abs"])
+           one_ulp=stats["one_ulp"], max_abs_vs_oracle=stats["max_abs"], worst=worst,
+           worst_sizable=worst_sizable)
     return stats

@@ -154,10 +154,11 @@ def test_bandwidth_sweep_matched_full_size():
     rows = _sample_rows(lengths)
     host = host_rows(*g, rows)
     plan = res.plan
-    expected, _, lse, bound, _ = OM.matched_decode_with_bounds(
-        *host, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes)
+    expected, _, lse, bound, _, counts = OM.matched_decode_with_bounds(
+        *host, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes,
+        counts=True)
     out = call(*g)
-    assert_within_one_ulp(out[rows], expected, f"sweep rows {rows}", bound)
+    assert_within_one_ulp(out[rows], expected, f"sweep rows {rows}", bound, counts)
     np.testing.assert_allclose(to_np(res.lse[rows]), lse, atol=2e-5, rtol=1e-6)
     _check_graph_replay(call, lambda: poison_workspace(res), *g)
 
@@ -202,9 +203,11 @@ def test_edge_coverage_full_batch_all_backends(dim, hq, hkv):
         assert_close_dense(out, dense)
         assert torch.count_nonzero(out[empty]) == 0
         plan = res.plan
-        expected, _, _, bound, _ = OM.matched_decode_with_bounds(
-            *host, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes)
-        assert_within_one_ulp(out[rows], expected, f"matched {plan.splits} splits", bound)
+        expected, _, _, bound, _, counts = OM.matched_decode_with_bounds(
+            *host, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes,
+            counts=True)
+        assert_within_one_ulp(out[rows], expected, f"matched {plan.splits} splits", bound,
+                              counts)
     for backend in ("hip_base", "hip_splitk"):
         res = allocate_resources(spec, "cuda", backend)
         poison_workspace(res)

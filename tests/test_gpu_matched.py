@@ -25,7 +25,7 @@ pytestmark = pytest.mark.gpu
 def oracle_for(case, plan, scale=None):
     """(out, partials, lse, rounding-ambiguity bound of out) from the oracle."""
     return OM.matched_decode_with_bounds(*case, plan.splits, plan.tokens_per_split,
-                                         plan.tile_tokens, plan.lse_lanes, scale)
+                                         plan.tile_tokens, plan.lse_lanes, scale, counts=True)
 
 
 def run(case, spec, num_splits=0, scale=None):
@@ -45,8 +45,8 @@ def assert_partials(actual, expected, bound):
 
 
 def check_all(case, g, res, out, scale=None, where=""):
-    expected, partials, lse, bound, partial_bound = oracle_for(case, res.plan, scale)
-    frac = assert_within_one_ulp(out, expected, where, bound)
+    expected, partials, lse, bound, partial_bound, counts = oracle_for(case, res.plan, scale)
+    frac = assert_within_one_ulp(out, expected, where, bound, counts)
     np.testing.assert_allclose(to_np(res.lse), lse, atol=2e-5, rtol=1e-6)
     assert_partials(res.partials, partials, partial_bound)
     assert_close_dense(out, torch_dense(*g, scale=scale))
@@ -73,8 +73,9 @@ def test_d256_fixed_1024_token_partitions():
     _native.partition(*g, partials, lse, 4, 3, 1024, 64, 256 ** -0.5)
     _native.lse_merge(partials, lse, out, 4)
     torch.cuda.synchronize()
-    expected, _, exp_lse, bound, _ = OM.matched_decode_with_bounds(*case, 3, 1024, 64, 4)
-    assert_within_one_ulp(out, expected, "1024-token partitions", bound)
+    expected, _, exp_lse, bound, _, counts = OM.matched_decode_with_bounds(*case, 3, 1024, 64,
+                                                                           4, counts=True)
+    assert_within_one_ulp(out, expected, "1024-token partitions", bound, counts)
     np.testing.assert_allclose(to_np(lse), exp_lse, atol=2e-5, rtol=1e-6)
 
 
@@ -117,8 +118,8 @@ def test_graph_replay_and_empty_partitions():
         captured = out.clone()
         torch.cuda.synchronize()
         host = (to_np(q), to_np(k), to_np(v), table.cpu().numpy(), lengths.cpu().numpy())
-        expected, _, _, bound, _ = oracle_for(host, res.plan)
-        assert_within_one_ulp(captured, expected, f"replay {values}", bound)
+        expected, _, _, bound, _, counts = oracle_for(host, res.plan)
+        assert_within_one_ulp(captured, expected, f"replay {values}", bound, counts)
         assert_close_dense(captured, torch_dense(*g))
         poison_workspace(res)
         eager = matched_decode(*g, resources=res)

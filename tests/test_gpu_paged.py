@@ -388,3 +388,42 @@ def test_chunks_do_not_depend_on_padding_or_the_live_width(backend, hq, hkv, dim
     assert torch.equal(padded[:3].view(torch.int16), live.view(torch.int16))
     assert torch.count_nonzero(padded[3]) == 0
     assert_within_one_ulp(live, oracle_for(case, backend, spec), f"{backend} D{dim} {hq}/{hkv}")
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+@pytest.mark.parametrize("parts", [1, 3, 4, 5, 9, 16, 17, 33, 48, 49, 100, 128, 129, 200])
+def test_ml_merge_rows_partitions_and_alignment(dim, parts):
+    """pd_ml_merge over seeded (m, l, acc) states with empty partitions (m = -inf, l = 0,
+    acc = 0) and an all-empty row, against the oracle's merge at one bf16 ulp.  Up to 128
+    partitions the kernel takes one wavefront per row (rows >= 2048, 16-byte aligned
+    accumulators) or per 64 columns, and loads in batches sized to the partition count:
+    the same rows give the same bits alone, among 2048 rows, and from unaligned
+    accumulators."""
+    rng = np.random.default_rng(parts * 3 + dim)
+    b, hq = 2, 4
+    m = (rng.normal(size=(b, hq, parts)) * 3).astype(np.float32)
+    l = rng.uniform(0.5, 40, size=(b, hq, parts)).astype(np.float32)
+    acc = (rng.normal(size=(b, hq, parts, dim)) * l[..., None]).astype(np.float32)
+    empty = rng.random((b, hq, parts)) < 0.3
+    empty[1, 2] = True                                    # an all-empty row
+    m[empty], l[empty], acc[empty] = -np.inf, 0, 0
+    expected = OS.ml_merge(m, l, acc)
+
+    def merge(mm, ll, aa, rows_b):
+        out = torch.full((rows_b, hq, dim), float("nan"), device="cuda", dtype=torch.bfloat16)
+        _native.ml_merge(mm, ll, aa, out, rows_b)
+        return out
+
+    gm, gl, ga = (torch.from_numpy(x).cuda() for x in (m, l, acc))
+    alone = merge(gm, gl, ga, b)
+    reps = 2048 // (b * hq)
+    many = merge(gm.repeat(reps, 1, 1), gl.repeat(reps, 1, 1), ga.repeat(reps, 1, 1, 1), b * reps)
+    storage = torch.empty(ga.numel() + 1, device="cuda")
+    unaligned = storage[1:].view(ga.shape)
+    unaligned.copy_(ga)
+    odd = merge(gm, gl, unaligned, b)
+    torch.cuda.synchronize()
+    assert_within_one_ulp(alone, expected, f"ml_merge D{dim} {parts} partitions")
+    assert torch.count_nonzero(alone[1, 2]) == 0
+    for other in (many[:b], many[-b:], odd):
+        assert torch.equal(other.view(torch.int16), alone.view(torch.int16))

@@ -87,10 +87,11 @@ def test_random_case(index):
             torch.cuda.synchronize()
             assert torch.equal(single.view(torch.int16), out.view(torch.int16)), where
         torch.cuda.synchronize()
-        expected, _, lse_ref, bound, _ = OM.matched_decode_with_bounds(
-            *case, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes, scale)
+        expected, _, lse_ref, bound, _, counts = OM.matched_decode_with_bounds(
+            *case, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes, scale,
+            counts=True)
         np.testing.assert_allclose(to_np(lse), lse_ref, atol=2e-5, rtol=1e-6, err_msg=where)
-        assert_within_one_ulp(out, expected, where, bound)
+        assert_within_one_ulp(out, expected, where, bound, counts)
     else:
         res = allocate_resources(spec, "cuda", backend)
         if (index // len(BACKENDS)) % 2:

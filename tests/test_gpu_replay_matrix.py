@@ -85,8 +85,9 @@ def test_replay_matrix(hq, hkv, splits):
             v.normal_()
         dense = torch_dense(*tensors)
         host = (to_np(q), to_np(k), to_np(v), table.cpu().numpy(), lengths.cpu().numpy())
-        expected, _, _, bound, _ = OM.matched_decode_with_bounds(
-            *host, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes)
+        expected, _, _, bound, _, counts = OM.matched_decode_with_bounds(
+            *host, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes,
+            counts=True)
         values = {}
         for name, res in paths.items():
             graph, out = graphs[name]
@@ -101,7 +102,7 @@ def test_replay_matrix(hq, hkv, splits):
             where = f"Hq {hq} Hkv {hkv} splits {plan.splits} step {step} {name}"
             assert torch.equal(replayed.view(torch.int16), eager.view(torch.int16)), where
             assert_close_dense(replayed, dense, where)
-            assert_within_one_ulp(replayed, expected, where, bound)
+            assert_within_one_ulp(replayed, expected, where, bound, counts)
             if not any(state):
                 assert torch.count_nonzero(replayed) == 0, where
             values[name] = saved
