@@ -1,4 +1,5 @@
-"""Validated launches and reusable output / split workspace.
+"""Host side of the paged_decode backends: argument checks, HIP launches, and the
+preallocated output and split workspace they write.
 
 Mirrors runtime.py of the reference (src/paged_decode/runtime.py:15-117):
 ``Resources``, ``allocate_resources``, ``validate_device_metadata``,
@@ -106,7 +107,10 @@ def _chunk_plan(resources, batch, width):
 
 
 def validate_device_metadata(table, lengths, num_pages, max_context_len):
-    """Debug check: deliberately synchronizes; NEVER call in capture/hot path."""
+    """Check table and length contents on the host.
+
+    The contents are copied off the device, so this synchronizes: call it once for
+    tables from outside a scheduler, never inside graph capture or the decode loop."""
     if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
         raise RuntimeError("metadata content validation cannot run during graph capture")
     if table.dim() != 2 or lengths.dim() != 1 or table.shape[0] != lengths.shape[0]:

@@ -14,7 +14,8 @@ midpoint can round up on one side and down on the other; that moves the
 output by ulp_bf16(p) * |v| / denom times the split's merge weight.  Such
 flips cannot be removed by any implementation that is not bit-identical in
 its fp32 arithmetic.  oracle.matched.matched_decode_with_bounds returns A as
-the sum of that quantity over every p within 128 float32 ulps of a midpoint.
+the sum of that quantity over every p within AMBIGUITY_ULPS (32) float32 ulps of a
+midpoint.
 The 2^-18 term covers float32 accumulation-order noise on outputs that are
 close to zero.  Planted protocol mistakes (forward tile walk, no bf16(p)) fail
 this gate (tests/test_oracle_matched.py::test_parity_gate_rejects_protocol_mistakes).

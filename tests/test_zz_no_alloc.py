@@ -105,3 +105,55 @@ def test_oversized_workspace_is_rejected():
     # 64 * 32 * 32 splits * 257 floats = 67 MB > 16 MiB.
     with pytest.raises(ValueError, match="static scratch"):
         _native.matched_decode_noalloc(q, kv, kv, table, lens, out, 8, 32, 1024, 64, 0.0625)
+
+
+NOALLOC_CAPTURE_FIRST = r"""
+import sys
+sys.path[:0] = {paths!r}
+import torch
+from cases import make_case
+from gpu_cases import to_gpu
+from paged_decode import _native
+from paged_decode.matched_splitkv import allocate_matched_resources
+from paged_decode.spec import DecodeSpec
+lengths, hq, hkv, dim, cap = [2064, 0, 1000, 1], 16, 4, 256, 2112
+spec = DecodeSpec(len(lengths), hq, hkv, dim, cap)
+g = to_gpu(make_case(lengths, hq, hkv, dim, seed=5, capacity=cap))
+plan = allocate_matched_resources(spec, "cuda").plan   # host planner and buffers only
+q, k, v, table, lens = g
+out = torch.full((len(lengths), hq, dim), float("nan"), device="cuda", dtype=torch.bfloat16)
+torch.cuda.synchronize()
+stream = torch.cuda.Stream()
+stream.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=stream):    # the library's first launch in this process
+    _native.matched_decode_noalloc(q, k, v, table, lens, out, hkv, plan.splits,
+                                   plan.tokens_per_split, plan.tile_tokens, dim ** -0.5)
+graph.replay()
+torch.cuda.synchronize()
+captured = out.clone()
+out.fill_(float("nan"))
+_native.matched_decode_noalloc(q, k, v, table, lens, out, hkv, plan.splits,
+                               plan.tokens_per_split, plan.tile_tokens, dim ** -0.5)
+torch.cuda.synchronize()
+assert torch.equal(captured.view(torch.int16), out.view(torch.int16)), "replay != eager"
+assert not captured[1].any(), "zero-length row is not exactly zero"
+print("noalloc capture-first ok")
+"""
+
+
+def test_first_call_of_the_process_under_graph_capture():
+    """A fresh process whose first library launch is pd_matched_decode_noalloc inside a
+    graph capture: the per-device scratch lookup then happens during the capture, which
+    must still succeed, and the replay must equal an eager call bit for bit."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    paths = [here, root, os.path.join(root, "paged-decode-lab_amd")]
+    print("noalloc capture-first subprocess: B=4 Hq=16 Hkv=4 D=256", flush=True)
+    res = subprocess.run([sys.executable, "-c", NOALLOC_CAPTURE_FIRST.format(paths=paths)],
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr[-3000:]
+    assert "noalloc capture-first ok" in res.stdout
