@@ -545,9 +545,10 @@ AB_WORKLOADS = ("headline", "partitions", "edge_d64", "edge_d256", "sweep")
 
 def ab_variants_paged(torch, q, k, v, table, lens, spec, backend, libraries):
     """One call per variant of a paged_decode backend (hip_base: pd_base; hip_splitk:
-    pd_split_fixed + pd_ml_merge) through this build ("current") or another one.  All
-    variants share one workspace and output, so that they differ in the library only
-    (the placement of a workspace alone moves these times by a few percent)."""
+    pd_split_decode, or pd_split_fixed + pd_ml_merge for a build without it) through this
+    build ("current") or another one.  All variants share one workspace and output, so
+    that they differ in the library only (the placement of a workspace alone moves these
+    times by a few percent)."""
     from paged_decode import _native
     from paged_decode.runtime import allocate_resources
     scale = spec.head_dim ** -0.5
@@ -558,6 +559,11 @@ def ab_variants_paged(torch, q, k, v, table, lens, spec, backend, libraries):
             def call(library=library):
                 _native.base(q, k, v, table, lens, res.out, spec.num_kv_heads, scale,
                              library=library)
+        elif hasattr(library or _native.lib(), "pd_split_decode"):
+            def call(library=library):
+                _native.split_decode(q, k, v, table, lens, res.maxima, res.denoms, res.accums,
+                                     res.out, spec.num_kv_heads, spec.partitions, 1024, scale,
+                                     library=library)
         else:
             def call(library=library):
                 _native.split_fixed(q, k, v, table, lens, res.maxima, res.denoms, res.accums,

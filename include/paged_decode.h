@@ -39,7 +39,7 @@ enum pd_status { PD_OK = 0, PD_EINVAL = 1, PD_ELAUNCH = 2 };
 
 #define PD_PAGE_SIZE 256      /* spec.py:6 */
 #define PD_PARTITION_SIZE 1024 /* spec.py:7 */
-#define PD_ABI_VERSION 5
+#define PD_ABI_VERSION 6
 
 /* Split-KV plan; field meanings follow SplitKVPlan (splitkv_plan.py:15-23). */
 typedef struct pd_plan {
@@ -178,9 +178,9 @@ int pd_base(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * reference's grid.  Both write the same bits.  Replaces _split
  * (kernels.py:44-80) as launched by paged_decode (runtime.py:111-113).
  * maxima/denoms f32 [batch, num_heads, partitions], accums f32 [batch,
- * num_heads, partitions, D]; the row stride of all three is `partitions`;
- * partition_size a positive multiple of 16384 / head_dim; partitions *
- * partition_size < 2^31. */
+ * num_heads, partitions, D] (16-byte aligned); the row stride of all three is
+ * `partitions`; partition_size a positive multiple of 16384 / head_dim;
+ * partitions * partition_size < 2^31. */
 int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                    const void* k, const void* v,
                    const int32_t* table, int64_t table_stride_b, int32_t table_width,
@@ -191,10 +191,31 @@ int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                    pd_stream_t stream);
 
 /* m/l/acc merge; replaces _merge (kernels.py:83-100) as launched by
- * paged_decode (runtime.py:114-116).  Writes out rows [0, batch). */
+ * paged_decode (runtime.py:114-116).  The reference's formula (M = max m_p,
+ * f_p = exp(m_p - M), out = sum f_p acc_p / sum f_p l_p, a zero total
+ * dividing by 1) is computed with a running maximum over the partitions from
+ * the last to the first, skipping empty ones (m_p = -inf): the order in which
+ * the fixed-split walk completes them, so pd_split_decode's in-kernel merge
+ * gives the same bits.  Writes out rows [0, batch). */
 int pd_ml_merge(const float* maxima, const float* denoms, const float* accums, void* out,
                 int32_t batch, int32_t num_heads, int32_t head_dim, int32_t partitions,
                 pd_stream_t stream);
+
+/* pd_split_fixed followed by pd_ml_merge into out: both launches of the
+ * reference's fixed-split backend (runtime.py:111-116) in one call.  When the
+ * walks fill the device, the walking workgroups merge their sequence's
+ * partitions as they complete them and write out directly, with
+ * pd_ml_merge's arithmetic (one launch); otherwise one workgroup runs per
+ * partition and pd_ml_merge follows.  Both write the same workspace and
+ * output bits. */
+int pd_split_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                    const void* k, const void* v,
+                    const int32_t* table, int64_t table_stride_b, int32_t table_width,
+                    const int32_t* lengths,
+                    float* maxima, float* denoms, float* accums, void* out,
+                    int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                    int32_t partitions, int32_t partition_size, double scale,
+                    pd_stream_t stream);
 
 /* Small-batch split of the base and fixed-split protocols; no counterpart in
  * the reference, whose _base and _split grids already spread a sequence over

@@ -322,6 +322,81 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
   }
 }
 
+// ------------------------------------------------ (m, l, acc) online merge
+// The merge of the fixed-split protocol's partition states, in the order the
+// fixed-split walk completes them: p = P - 1 down to 0.  A partition with
+// m_p = -inf holds no token and is skipped.  For the others, with M the
+// maximum of the partitions merged so far (-inf before the first):
+//   M' = max(M, m_p), a = exp(M - M'), b = exp(m_p - M'),
+//   acc = fma(acc_p, b, acc * a), total = fma(l_p, b, total * a), M = M',
+// and the output is acc * (1 / (total > 0 ? total : 1)).  This is the
+// reference's merge (kernels.py:83-100: maximum first, then the factors
+// exp(m_p - M)) computed as a running maximum, with its own float32 rounding.
+// ml_merge_kernel and the walk's in-kernel merge (cols_loader_kernel) both
+// use ml_step, so the two give the same bits.
+struct MlStep {
+  float a, b;  // factor of the running state and of the partition
+  bool live;   // m_p > -inf
+};
+
+__device__ __forceinline__ MlStep ml_step(float m_p, float& M) {
+  if (m_p == -INFINITY) return MlStep{1.f, 0.f, false};
+  const float mn = fmaxf(M, m_p);
+  const MlStep st{exp_fast(M - mn), exp_fast(m_p - mn), true};
+  M = mn;
+  return st;
+}
+
+// x of lane L + k, or -inf past lane 63 (k > 0, wavefront-uniform).
+__device__ __forceinline__ float lane_down_or_neg_inf(float x, int k, int lane) {
+  const float y = __int_as_float(__builtin_amdgcn_ds_bpermute((lane + k) << 2, __float_as_int(x)));
+  return lane + k < 64 ? y : -INFINITY;
+}
+
+// Inclusive suffix maximum over the lanes: max of x over lanes >= L.
+__device__ __forceinline__ float suffix_max(float x, int lane) {
+  x = fmaxf(x, lane_down_or_neg_inf(x, 1, lane));
+  x = fmaxf(x, lane_down_or_neg_inf(x, 2, lane));
+  x = fmaxf(x, lane_down_or_neg_inf(x, 4, lane));
+  x = fmaxf(x, lane_down_or_neg_inf(x, 8, lane));
+  x = fmaxf(x, lane_down_or_neg_inf(x, 16, lane));
+  return fmaxf(x, lane_down_or_neg_inf(x, 32, lane));
+}
+
+// ml_step of every partition of a row at once, for up to 128 partitions: lane
+// L holds partitions L and L + 64 (m0 / m1; partitions at or past `parts`
+// count as empty).  The running maximum before partition p is the maximum of
+// the partitions after it (a suffix maximum), so each lane computes its
+// partitions' steps without the chain: the same fmaxf / exp_fast operations
+// on the same values as ml_step in order, hence the same bits.
+__device__ __forceinline__ void ml_steps_of(float m0, float m1, int parts, int lane, MlStep& s0,
+                                            MlStep& s1) {
+  const float v0 = lane < parts ? m0 : -INFINITY;
+  const float v1 = lane + 64 < parts ? m1 : -INFINITY;
+  const float hi = suffix_max(v1, lane);  // max over partitions >= L + 64
+  const float hi_all = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(hi)));
+  const float lo = fmaxf(suffix_max(v0, lane), hi_all);
+  // The maximum of the partitions after p (-inf after the last).  Every lane
+  // takes part in the lane moves: a move written inside `lane < 63 ? ... :`
+  // was compiled under that lane mask, and lane 62 then read the disabled
+  // lane 63.
+  const float after1 = lane_down_or_neg_inf(hi, 1, lane);
+  const float after0 = fmaxf(lane_down_or_neg_inf(lo, 1, lane), lane == 63 ? hi_all : -INFINITY);
+  float M0 = after0, M1 = after1;
+  s0 = ml_step(v0, M0);
+  s1 = ml_step(v1, M1);
+}
+
+// Step p of a row from ml_steps_of's per-lane steps (p wavefront-uniform).
+__device__ __forceinline__ MlStep wave_step(const MlStep& s0, const MlStep& s1, int p) {
+  const MlStep& src = p < 64 ? s0 : s1;
+  const int lane = p & 63;
+  return MlStep{
+      __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src.a), lane)),
+      __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src.b), lane)),
+      __builtin_amdgcn_readlane(int(src.live), lane) != 0};
+}
+
 // One wavefront merges columns [c0, c0 + C) (C a multiple of 4) of the G <= GP
 // query heads of a GQA group over all `splits` splits, with the arithmetic of
 // lse_merge_kernel: merge weights per head from lse_weights, then
@@ -640,6 +715,14 @@ __device__ __forceinline__ short4_t lds_read_tr_at(uint32_t base) {
 __device__ __forceinline__ u32x4_t lds_read16_at(uint32_t addr) {
   u32x4_t r;
   asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+// 4 bytes at an LDS byte address (ds_read_b32), from inline asm like
+// lds_read16_at; the result passes through lds_wait before use.
+__device__ __forceinline__ uint32_t lds_read4_at(uint32_t addr) {
+  uint32_t r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
   return r;
 }
 

@@ -234,9 +234,9 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<D>::kNBW],
 // tensor's copies: V between B1 and B2, K between B2 and the next B1,
 // alongside P V and QK.  A first barrier B0 covers K(count - 1), issued with
 // V(count - 1) and K(count - 2) before it.  Both halves pass the same
-// barriers: B0, B1 and B2 of every tile, the fixed-split walk's barrier after
-// each partition it completes, the one before the epilogue and the fused
-// split count's two.
+// barriers: B0, B1 and B2 of every tile, the fixed-split protocols' barrier
+// after the last partition (ti = 0), the one before the epilogue and the
+// fused split count's two.
 template <int D, int GP, bool kFused, int kMode, int kHeads = 1>
 __global__ void __launch_bounds__(2 * kThreads, 1)
 cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict__ lengths,
@@ -270,8 +270,21 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   // sequence) in one workgroup (grid.x = 1), so a sequence's partitions share
   // one workgroup's start and its K / V pipeline; kSplitPart runs the same
   // code over partition blockIdx.x alone.
+  //
+  // A completed partition goes to global memory through the loader
+  // wavefronts: the compute wavefronts leave its acc in `fb` (query head h at
+  // fb[h * kFbPitch + c]), its maxima in `fm` and their denominator shares in
+  // sm.lsum, and the loaders read them back and store them with 16-byte
+  // stores after issuing their next K copies.  A compute wavefront that
+  // stored them itself stood still for about 1-2 us per partition (its stores
+  // wait behind the loaders' copies), which every wavefront then waited for
+  // at the next barrier.
   constexpr bool kWalk = kMode == kSplit;
   constexpr bool kFlush = kMode == kSplit || kMode == kSplitPart;
+  constexpr int kFbPitch = D + 4;                 // floats per head row of fb
+  constexpr int kFbPasses = GP * D >= 1024 ? GP * D / 1024 : 1;  // 16-byte stores per loader lane
+  __shared__ __attribute__((aligned(16))) float fb[kFlush ? GP * kFbPitch : 4];
+  __shared__ float fm[16];
   constexpr int kEmptyMode = kFlush ? kSplit : kMode;  // write_empty_partition's protocol
   const int p = kWalk ? 0 : int(blockIdx.x);
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
@@ -328,17 +341,67 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       }
       lds_barrier();  // B0
     }
+    // The partition flush: loader w's share of a completed partition, read
+    // from LDS (inline asm reads: a compiler-placed wait before a plain LDS
+    // read would count the copies in flight) and stored after the next K
+    // copies are issued.  In-order completion then lets the next wait for K
+    // cover the stores too.
+    u32x4_t fx[kFbPasses];
+    uint32_t fmx = 0, fl[4] = {0, 0, 0, 0};
+    auto flush_read = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < kFbPasses; ++i) {
+        const int f = (i * 256 + w * 64 + lane) * 4;
+        const int h = min(f / D, GP - 1);  // rows past GP are never stored
+        fx[i] = lds_read16_at(lds_address(reinterpret_cast<const char*>(fb)) +
+                              uint32_t(h * kFbPitch + f % D) * 4);
+      }
+      if (w == 0) {
+        const int h = lane & 15;
+        fmx = lds_read4_at(lds_address(reinterpret_cast<const char*>(fm)) + h * 4);
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+          fl[x] = lds_read4_at(lds_address(reinterpret_cast<const char*>(&sm.lsum[x][h])));
+      }
+      lds_wait(fx);
+      asm volatile("" : "+v"(fmx), "+v"(fl[0]), "+v"(fl[1]), "+v"(fl[2]), "+v"(fl[3]));
+    };
+    auto flush_store = [&](int part) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < kFbPasses; ++i) {
+        const int f = (i * 256 + w * 64 + lane) * 4;
+        const int h = f / D;
+        if (h < Gs) {
+          const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + part;
+          *reinterpret_cast<u32x4_t*>(partials + orow * D + f % D) = fx[i];
+        }
+      }
+      if (w == 0 && lane < Gs) {
+        const int64_t orow = (int64_t(b) * Hq + qb + lane) * splits + part;
+        maxima[orow] = __uint_as_float(fmx);
+        lse_out[orow] = (__uint_as_float(fl[0]) + __uint_as_float(fl[1])) +
+                        (__uint_as_float(fl[2]) + __uint_as_float(fl[3]));
+      }
+    };
     for (int ti = count - 1; ti >= 0; --ti) {
       lds_barrier();  // B1(ti)
+      // The partition that ended with tile ti + 1 is in LDS since B1(ti).
+      const bool flushed = kFlush && ti + 1 < count && (ti + 1) % tpp == 0;
+      if (ti >= 1) issue(ti - 1, false);
+      if (flushed) flush_read();
       if (ti >= 1) {
-        issue(ti - 1, false);
         wait_vmcnt<kCopies>();
       } else {
         wait_vmcnt<0>();
       }
       lds_barrier();  // B2(ti)
       if (ti >= 2) issue(ti - 2, true);
-      if (kFlush && ti % tpp == 0) lds_barrier();  // the partition flush
+      if (flushed) flush_store(p + (ti + 1) / tpp);
+      if (kFlush && ti == 0) {
+        lds_barrier();  // the last partition's flush
+        flush_read();
+        flush_store(p);
+      }
     }
     if constexpr (!kFlush) lds_barrier();  // epilogue
     if constexpr (kFused) {
@@ -352,6 +415,10 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
       write_empty_partition<D, kEmptyMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out,
                                            out, maxima);
+    // The walk's merged output of an empty sequence is 0 (no live partition).
+    if (kWalk && out != nullptr)
+      write_empty_partition<D, kBase>(tid, b, Hq, qb, Gs, splits, 0, partials, lse_out, out,
+                                      maxima);
     return;
   }
   bf16x8_t qf[C::kCH];
@@ -390,6 +457,37 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
   float m_own = -INFINITY;  // running max of head qh
   float l_own = 0.f;        // this lane's share of head qh's denominator
+  // The walk with an output (out != nullptr) also merges the partitions as it
+  // completes them, with ml_merge_kernel's arithmetic (ml_step): running
+  // maxima mM of heads 4 qg + r, merged accumulators mO (the lane's columns of
+  // acc) and totals mT.  A partition's denominator needs every wavefront's
+  // share (sm.lsum), so its steps mS wait (`pending`) for the next barrier
+  // every wavefront passes: B1 of the next tile, or the last partition's own.
+  // The next flush writes sm.lsum after B2 of the following tile, when these
+  // reads (before the wavefront reaches B2) are done.
+  const bool merge_out = kWalk && out != nullptr;
+  bool pending = false;
+  floatx4_t mO[P::kNBW];
+  float mM[4], mT[4];
+  MlStep mS[4];
+  if (kWalk) {
+#pragma unroll
+    for (int j = 0; j < P::kNBW; ++j) mO[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      mM[r] = -INFINITY;
+      mT[r] = 0.f;
+      mS[r] = MlStep{1.f, 0.f, false};
+    }
+  }
+  auto merge_denominators = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * qg + r;
+      const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
+      if (mS[r].live) mT[r] = fmaf(den, mS[r].b, mT[r] * mS[r].a);
+    }
+  };
 
   if (count > 0) {
     lds_barrier();  // B0
@@ -441,6 +539,14 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     float (*wm)[16] = sm.wmax[ti & 1];
     if (lane < 16) wm[w][lane] = mx;
     lds_barrier();  // B1(ti)
+    if constexpr (kWalk) {
+      // The denominators of the partition flushed after the previous tile
+      // were written to LDS before this barrier.
+      if (pending) {
+        merge_denominators();
+        pending = false;
+      }
+    }
 
     // ---- probabilities, P to LDS (lo, mid, hi for the FP32 probabilities of
     // the base / split protocols), rescale of O
@@ -505,28 +611,40 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 
     if constexpr (kFlush) {
       // After tile ti, the first tile of partition p + ti / tpp, that
-      // partition is complete: its denominators are summed over the waves and
-      // its (m, l, acc) stored (kernels.py:77-80), and the running state
-      // restarts for the partition before it.  The copies of the next tiles
-      // stay in flight.
+      // partition is complete: its (m, l, acc) go to LDS for the loaders to
+      // store (kernels.py:77-80), l as per-wavefront shares, and the running
+      // state restarts for the partition before it.  The copies of the next
+      // tiles stay in flight, and only the last partition takes a barrier of
+      // its own.
       if (ti % tpp == 0) {
-        const int part = p + ti / tpp;
         const float l = sum_rows(l_own);
         if (lane < 16) sm.lsum[w][lane] = l;
-        lds_barrier();
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int h = 4 * qg + r;
           if (h >= Gs) break;
-          const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
-          const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + part;
-          const int col = w * P::kCols + qh;
+          float* row = fb + h * kFbPitch + w * P::kCols + qh;
 #pragma unroll
-          for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r];
-          if (w == 0 && qh == 0) {
-            maxima[orow] = m4[r];
-            lse_out[orow] = den;
+          for (int j = 0; j < P::kNBW; ++j) row[16 * j] = acc[j][r];
+          if (w == 0 && qh == 0) fm[h] = m4[r];
+        }
+        if (merge_out) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            mS[r] = ml_step(m4[r], mM[r]);
+            if (mS[r].live) {
+#pragma unroll
+              for (int j = 0; j < P::kNBW; ++j) mO[j][r] = fmaf(acc[j][r], mS[r].b, mO[j][r] * mS[r].a);
+            }
           }
+        }
+        // The loaders store the partition after the next tile's B1 barrier,
+        // or after one more barrier for the last partition; the merged
+        // totals take its denominators then too.
+        pending = merge_out;
+        if (ti == 0) {
+          lds_barrier();
+          if (merge_out) merge_denominators();
         }
 #pragma unroll
         for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
@@ -543,6 +661,17 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     for (int pp = (end + T - 1) / T; pp < splits; ++pp)
       write_empty_partition<D, kSplit>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
                                        maxima);
+    if (merge_out) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * qg + r;
+        if (h >= Gs) break;
+        const float inv = 1.f / (mT[r] > 0.f ? mT[r] : 1.f);
+        uint16_t* dst = out + (int64_t(b) * Hq + qb + h) * D + w * P::kCols + qh;
+#pragma unroll
+        for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = uint16_t(bf16_bits(mO[j][r] * inv));
+      }
+    }
     return;
   }
   if constexpr (kFlush) return;  // partition p was written by the flush after its first tile
@@ -955,16 +1084,17 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
 }
 
 // ------------------------------------------------------------ m/l/acc merge
-// The merge of the fixed-split protocol (kernels.py:83-100): M = max_p m_p
-// (-inf -> 0), f_p = exp(m_p - M), out = sum_p f_p acc_p / sum_p f_p l_p (a
-// zero total divides by 1).  Up to 128 partitions: one wavefront per (b, h)
-// row and 64 E columns (grid rows x D / (64 E)), E consecutive columns per
-// lane; E = 1 spreads a row over D / 64 CUs when there are few rows.  Lane j
-// loads m and l of partitions j and j + 64; every accumulator load of a batch
-// of kBatch partitions is issued before the factors are computed
-// (merge_splits), the total is an xor-butterfly sum over the lanes, and
-// acc = fma(f_p, acc_p, acc) runs in partition order.  Loads past the row read
-// zero and carry f = 0, so neither E nor kBatch changes the result's bits.
+// The merge of the fixed-split protocol (kernels.py:83-100) in the online
+// form of ml_step (pd_device.h): partitions p = P - 1 down to 0, empty ones
+// skipped, a running maximum, out = acc / total (a zero total divides by 1).
+// Up to 128 partitions: one wavefront per (b, h) row and 64 E columns (grid
+// rows x D / (64 E)), E consecutive columns per lane; E = 1 spreads a row over
+// D / 64 CUs when there are few rows.  Lane j loads m and l of partitions j
+// and j + 64 and computes their steps (ml_steps_of); the accumulator loads of
+// the first kBatch partitions (from the top) are issued before that, later
+// batches as the chain reaches them.  Loads past the row read zero and belong
+// to no partition, so neither E nor kBatch changes the result's bits, and the
+// walk's in-kernel merge (cols_loader_kernel, kSplit) gives the same bits.
 template <int E, int kBatch>
 __global__ void __launch_bounds__(64)
 ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
@@ -974,31 +1104,50 @@ ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ deno
   const int col = (blockIdx.y * 64 + lane) * E;
   const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(maxima + row * parts, parts * 4);
   const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(denoms + row * parts, parts * 4);
+  const int bytes = parts * D * 4;
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(accums + row * parts * D, bytes);
   float m0[1], m1[1], l0[1], l1[1];
   buffer_load_f32<1, 0>(rm, lane * 4, m0);
   buffer_load_f32<1, 0>(rm, (lane + 64) * 4, m1);
   buffer_load_f32<1, 0>(rl, lane * 4, l0);
   buffer_load_f32<1, 0>(rl, (lane + 64) * 4, l1);
-  float f0 = 0.f, f1 = 0.f, inv = 1.f, acc[E];
-  merge_splits<E, 0, kBatch>(
-      accums + row * parts * D, D, col, parts,
-      [&] {
-        const float v0 = lane < parts ? m0[0] : -INFINITY;
-        const float v1 = lane + 64 < parts ? m1[0] : -INFINITY;
-        float mx = wave_max(fmaxf(v0, v1));
-        if (mx == -INFINITY) mx = 0.f;  // all partitions empty
-        f0 = exp_fast(v0 - mx);
-        f1 = exp_fast(v1 - mx);
-        const float total = wave_sum(fmaf(l1[0], f1, l0[0] * f0));
-        inv = 1.f / (total > 0.f ? total : 1.f);
-      },
-      [&](int s0, int j) { return wave_weight(f0, f1, s0 + j); }, acc);
+  float x[kBatch][E];
+  auto load = [&](int top) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int p = top - 1 - j;
+      buffer_load_f32<E, 0>(ra, p >= 0 ? (p * D + col) * 4 : bytes, x[j]);
+    }
+  };
+  load(parts);
+  __builtin_amdgcn_sched_barrier(0);
+  MlStep s0, s1;
+  ml_steps_of(m0[0], m1[0], parts, lane, s0, s1);
+  float acc[E], total = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  for (int top = parts; top > 0; top -= kBatch) {
+    if (top != parts) load(top);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int p = top - 1 - j;
+      if (p < 0) break;
+      const MlStep st = wave_step(s0, s1, p);
+      if (!st.live) continue;
+      const float lp = wave_weight(l0[0], l1[0], p);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = fmaf(x[j][e], st.b, acc[e] * st.a);
+      total = fmaf(lp, st.b, total * st.a);
+    }
+  }
+  const float inv = 1.f / (total > 0.f ? total : 1.f);
 #pragma unroll
   for (int e = 0; e < E; ++e) out[row * D + col + e] = uint16_t(bf16_bits(acc[e] * inv));
 }
 
 // The same merge for more than 128 partitions: one wavefront per row, lane j
-// owning columns VEC j .. VEC j + VEC - 1, partitions in order.
+// owning columns VEC j .. VEC j + VEC - 1, ml_step in partition order from
+// the last.
 template <int VEC>
 __global__ void __launch_bounds__(64)
 ml_merge_loop_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
@@ -1008,19 +1157,16 @@ ml_merge_loop_kernel(const float* __restrict__ maxima, const float* __restrict__
   const int lane = threadIdx.x;
   const float* mrow = maxima + int64_t(row) * parts;
   const float* lrow = denoms + int64_t(row) * parts;
-  float mx = -INFINITY;
-  for (int p = lane; p < parts; p += 64) mx = fmaxf(mx, mrow[p]);
-  mx = wave_max(mx);
-  if (mx == -INFINITY) mx = 0.f;  // all partitions empty
-  float total = 0.f, acc[VEC];
+  float M = -INFINITY, total = 0.f, acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
   const float* arow = accums + int64_t(row) * parts * D + lane * VEC;
-  for (int p = 0; p < parts; ++p) {
-    const float f = exp_fast(mrow[p] - mx);
-    total += lrow[p] * f;
+  for (int p = parts - 1; p >= 0; --p) {
+    const MlStep st = ml_step(mrow[p], M);
+    if (!st.live) continue;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] = fmaf(arow[int64_t(p) * D + e], f, acc[e]);
+    for (int e = 0; e < VEC; ++e) acc[e] = fmaf(arow[int64_t(p) * D + e], st.b, acc[e] * st.a);
+    total = fmaf(lrow[p], st.b, total * st.a);
   }
   const float inv = 1.f / (total > 0.f ? total : 1.f);
   uint16_t* dst = out + int64_t(row) * D + lane * VEC;
@@ -1394,6 +1540,54 @@ extern "C" int pd_matched_decode_noalloc(const void* q, int64_t q_stride_b, int6
 
 namespace {
 
+// ml_merge_kernel (up to 128 partitions) or ml_merge_loop_kernel over `rows`
+// (b, h) rows; arguments checked by the caller.
+void launch_ml_merge(const float* maxima, const float* denoms, const float* accums, uint16_t* o,
+                     int64_t rows, int head_dim, int partitions, hipStream_t st) {
+  if (partitions <= 128) {
+    // One wavefront per row (E = D / 64 columns per lane, 16-byte aligned
+    // accumulators) once the rows alone give 2048 wavefronts or more; otherwise a
+    // row's 64-column chunks on as many wavefronts.  Load batches of 4 to 48
+    // partitions (at most 16 of E > 1 columns).
+    const int E = rows >= 2048 && aligned16(accums) ? head_dim / 64 : 1;
+    int batch = 4;
+    while (batch < partitions && batch < (E == 1 ? 48 : 16)) batch = batch < 32 ? 2 * batch : 48;
+    const dim3 grid(unsigned(rows), head_dim / (64 * E));
+#define PD_LAUNCH_ML(EV, KB)                                                                   \
+  hipLaunchKernelGGL((ml_merge_kernel<EV, KB>), grid, dim3(64), 0, st, maxima, denoms, accums, \
+                     o, partitions, head_dim)
+    switch (E * 100 + batch) {
+      case 104: PD_LAUNCH_ML(1, 4); break;
+      case 108: PD_LAUNCH_ML(1, 8); break;
+      case 116: PD_LAUNCH_ML(1, 16); break;
+      case 132: PD_LAUNCH_ML(1, 32); break;
+      case 148: PD_LAUNCH_ML(1, 48); break;
+      case 204: PD_LAUNCH_ML(2, 4); break;
+      case 208: PD_LAUNCH_ML(2, 8); break;
+      case 216: PD_LAUNCH_ML(2, 16); break;
+      case 404: PD_LAUNCH_ML(4, 4); break;
+      case 408: PD_LAUNCH_ML(4, 8); break;
+      default: PD_LAUNCH_ML(4, 16); break;
+    }
+#undef PD_LAUNCH_ML
+    return;
+  }
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL(ml_merge_loop_kernel<1>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                         accums, o, partitions);
+      break;
+    case 128:
+      hipLaunchKernelGGL(ml_merge_loop_kernel<2>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                         accums, o, partitions);
+      break;
+    default:
+      hipLaunchKernelGGL(ml_merge_loop_kernel<4>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                         accums, o, partitions);
+      break;
+  }
+}
+
 // Whether pd_split_fixed runs one workgroup per partition: when the walks,
 // one per (kv head group, sequence), leave CUs of the device idle and there is
 // more than one partition.
@@ -1443,6 +1637,8 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
     return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
   const int tile = 16384 / head_dim;
   if (kSplitMode) {
+    if (batch > 0 && int64_t(batch) * num_heads > 0x7fffffff)
+      return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
     if (parts < 1) return pd::fail(PD_EINVAL, "partitions must be positive");
     if (part_size <= 0 || part_size % tile)
       return pd::fail(PD_EINVAL, "partition_size must be a positive multiple of %d", tile);
@@ -1450,6 +1646,8 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
       return pd::fail(PD_EINVAL, "partitions * partition_size must stay below 2^31");
     if (!maxima || !denoms || !accums)
       return pd::fail(PD_EINVAL, "invalid or missing preallocated split-K workspace");
+    if (!aligned16(accums))
+      return pd::fail(PD_EINVAL, "split-K accumulators must be 16-byte aligned");
   } else if (!out) {
     return pd::fail(PD_EINVAL, "invalid output buffer");
   }
@@ -1478,7 +1676,15 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (per_part) {
+    // One workgroup per partition; with an output, ml_merge_kernel merges
+    // them after (the walk's in-kernel merge has the same arithmetic).
+    a.out = nullptr;
     launch_online_mode<kSplitPart>(head_dim, heads, G, grid, st, a);
+    if (int s = launch_status(what)) return s;
+    if (out) {
+      launch_ml_merge(maxima, denoms, accums, static_cast<uint16_t*>(out), int64_t(batch) * num_heads,
+                      head_dim, parts, st);
+    }
   } else {
     launch_online_mode<kSplitMode ? kSplit : kBase>(head_dim, heads, G, grid, st, a);
   }
@@ -1526,49 +1732,22 @@ extern "C" int pd_ml_merge(const float* maxima, const float* denoms, const float
     return pd::fail(PD_EINVAL, "invalid or missing preallocated split-K workspace");
   const int64_t rows = int64_t(batch) * num_heads;
   if (rows > 0x7fffffff) return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
-  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  auto* o = static_cast<uint16_t*>(out);
-  if (partitions <= 128) {
-    // One wavefront per row (E = D / 64 columns per lane, 16-byte aligned
-    // accumulators) once the rows alone give 2048 wavefronts or more; otherwise a
-    // row's 64-column chunks on as many wavefronts.  Load batches of 4 to 48
-    // partitions (at most 16 of E > 1 columns).
-    const int E = rows >= 2048 && aligned16(accums) ? head_dim / 64 : 1;
-    int batch = 4;
-    while (batch < partitions && batch < (E == 1 ? 48 : 16)) batch = batch < 32 ? 2 * batch : 48;
-    const dim3 grid(unsigned(rows), head_dim / (64 * E));
-#define PD_LAUNCH_ML(EV, KB)                                                                   \
-  hipLaunchKernelGGL((ml_merge_kernel<EV, KB>), grid, dim3(64), 0, st, maxima, denoms, accums, \
-                     o, partitions, head_dim)
-    switch (E * 100 + batch) {
-      case 104: PD_LAUNCH_ML(1, 4); break;
-      case 108: PD_LAUNCH_ML(1, 8); break;
-      case 116: PD_LAUNCH_ML(1, 16); break;
-      case 132: PD_LAUNCH_ML(1, 32); break;
-      case 148: PD_LAUNCH_ML(1, 48); break;
-      case 204: PD_LAUNCH_ML(2, 4); break;
-      case 208: PD_LAUNCH_ML(2, 8); break;
-      case 216: PD_LAUNCH_ML(2, 16); break;
-      case 404: PD_LAUNCH_ML(4, 4); break;
-      case 408: PD_LAUNCH_ML(4, 8); break;
-      default: PD_LAUNCH_ML(4, 16); break;
-    }
-#undef PD_LAUNCH_ML
-    return launch_status("pd_ml_merge");
-  }
-  switch (head_dim) {
-    case 64:
-      hipLaunchKernelGGL(ml_merge_loop_kernel<1>, dim3(rows), dim3(64), 0, st, maxima, denoms,
-                         accums, o, partitions);
-      break;
-    case 128:
-      hipLaunchKernelGGL(ml_merge_loop_kernel<2>, dim3(rows), dim3(64), 0, st, maxima, denoms,
-                         accums, o, partitions);
-      break;
-    default:
-      hipLaunchKernelGGL(ml_merge_loop_kernel<4>, dim3(rows), dim3(64), 0, st, maxima, denoms,
-                         accums, o, partitions);
-      break;
-  }
+  launch_ml_merge(maxima, denoms, accums, static_cast<uint16_t*>(out), rows, head_dim, partitions,
+                  reinterpret_cast<hipStream_t>(stream));
   return launch_status("pd_ml_merge");
+}
+
+extern "C" int pd_split_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                               const void* k, const void* v, const int32_t* table,
+                               int64_t table_stride_b, int32_t table_width,
+                               const int32_t* lengths, float* maxima, float* denoms,
+                               float* accums, void* out, int32_t batch, int32_t num_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t partitions,
+                               int32_t partition_size, double scale, pd_stream_t stream) {
+  pd::clear_error();
+  if (!out) return pd::fail(PD_EINVAL, "invalid output buffer");
+  return launch_online<true>(q, q_stride_b, q_stride_h, k, v, table, table_stride_b,
+                             table_width, lengths, out, maxima, denoms, accums, batch, num_heads,
+                             num_kv_heads, head_dim, partitions, partition_size, scale, stream,
+                             "pd_split_decode");
 }

@@ -42,6 +42,8 @@ SIGNATURES = {
     "pd_split_fixed": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp,
                        _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_ml_merge": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
+    "pd_split_decode": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
+                        _i32, _i32, _i32, _i32, _i32, _i32, _dbl, _vp],
     "pd_plan_chunks": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32),
                        ctypes.POINTER(_i32)],
     "pd_chunk_rows": [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i64)],
@@ -178,6 +180,18 @@ def ml_merge(maxima, denoms, accums, out, batch, library=None):
     L = library or lib()
     check(L.pd_ml_merge(maxima.data_ptr(), denoms.data_ptr(), accums.data_ptr(),
                         out.data_ptr(), batch, h, d, parts, stream_handle(out.device)), L)
+
+
+def split_decode(q, k, v, tables, lengths, maxima, denoms, accums, out, num_kv_heads,
+                 partitions, partition_size, scale, library=None):
+    """pd_split_decode: the fixed-split partitions and their merge into ``out``."""
+    b, h, d = q.shape
+    L = library or lib()
+    check(L.pd_split_decode(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                            tables.data_ptr(), tables.stride(0), tables.shape[1],
+                            lengths.data_ptr(), maxima.data_ptr(), denoms.data_ptr(),
+                            accums.data_ptr(), out.data_ptr(), b, h, num_kv_heads, d,
+                            partitions, partition_size, scale, stream_handle(q.device)), L)
 
 
 def plan_chunks(batch, num_heads, num_kv_heads, head_dim, table_width, sm_count):

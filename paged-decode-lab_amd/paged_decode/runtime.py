@@ -211,8 +211,9 @@ def paged_decode(q, k, v, tables, lengths, *, resources, backend="hip_base", sca
     if backend == "hip_base":
         _native.base(q, k, v, tables, lengths, resources.out, spec.num_kv_heads, scale)
     else:
-        _native.split_fixed(q, k, v, tables, lengths, resources.maxima, resources.denoms,
-                            resources.accums, spec.num_kv_heads, spec.partitions,
-                            PARTITION_SIZE, scale)
-        _native.ml_merge(resources.maxima, resources.denoms, resources.accums, resources.out, b)
+        # _split + _merge (runtime.py:111-116 of the reference) in one call: the walking
+        # workgroups merge their partitions themselves when they fill the device.
+        _native.split_decode(q, k, v, tables, lengths, resources.maxima, resources.denoms,
+                             resources.accums, resources.out, spec.num_kv_heads,
+                             spec.partitions, PARTITION_SIZE, scale)
     return resources.out[:b]

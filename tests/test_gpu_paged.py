@@ -239,10 +239,11 @@ def test_d256_tile_counts_of_the_loader_kernel(backend, grid):
     assert_within_one_ulp(actual, oracle_for(case, backend, spec), f"{backend} {grid}")
 
 
-def split_fixed_rows(g, hkv, parts, part, rows=None):
+def split_fixed_rows(g, hkv, parts, part, rows=None, decode=False):
     """pd_split_fixed over case ``g`` with its batch padded by empty sequences (-1 tables,
     zero queries) to ``rows`` rows (None: as it is); the (m, l, acc) of the case's own rows.
-    The workspaces start NaN."""
+    With ``decode``, pd_split_decode instead, and its merged output as a fourth value.
+    The workspaces and the output start NaN."""
     q, k, v, table, lens = g
     b = q.shape[0]
     if rows is not None and rows > b:
@@ -254,9 +255,14 @@ def split_fixed_rows(g, hkv, parts, part, rows=None):
     maxima = torch.full((n, hq, parts), float("nan"), device="cuda")
     denoms = torch.full_like(maxima, float("nan"))
     accums = torch.full((n, hq, parts, dim), float("nan"), device="cuda")
-    _native.split_fixed(q, k, v, table, lens, maxima, denoms, accums, hkv, parts, part,
-                        dim ** -0.5)
-    return maxima[:b], denoms[:b], accums[:b]
+    if not decode:
+        _native.split_fixed(q, k, v, table, lens, maxima, denoms, accums, hkv, parts, part,
+                            dim ** -0.5)
+        return maxima[:b], denoms[:b], accums[:b]
+    out = torch.full((n, hq, dim), float("nan"), device="cuda", dtype=torch.bfloat16)
+    _native.split_decode(q, k, v, table, lens, maxima, denoms, accums, out, hkv, parts, part,
+                         dim ** -0.5)
+    return maxima[:b], denoms[:b], accums[:b], out[:b]
 
 
 @pytest.mark.parametrize("dim,hq,hkv", [(64, 4, 1), (128, 8, 2), (256, 8, 2), (64, 32, 2),
@@ -268,10 +274,12 @@ def test_fixed_split_grids_and_partition_sizes(dim, hq, hkv, tiles_per_partition
     head group and sequence) are fewer than the CUs, as here, and one walking workgroup per
     (kv head group, sequence), writing every partition as it leaves it, when the walks fill
     the CUs (the same sequences followed by empty ones).  Both grids must write the same
-    (m, l, acc) bits.  Partition sizes of 1, 2, 3 and 5 tiles, lengths at and around
-    partition and page boundaries, the empty partitions past each sequence's end, and
-    NaN-poisoned tails: the workspace against oracle/splitk.py, and the merged output at
-    one bf16 ulp."""
+    (m, l, acc) bits.  pd_split_decode on either grid (one workgroup per partition, then
+    pd_ml_merge; or the walk, whose workgroups merge their own partitions) must write the
+    same workspace and the same output bits as pd_ml_merge over the workspace.  Partition
+    sizes of 1, 2, 3 and 5 tiles, lengths at and around partition and page boundaries,
+    the empty partitions past each sequence's end, and NaN-poisoned tails: the workspace
+    against oracle/splitk.py, and the merged output at one bf16 ulp."""
     tile = 16384 // dim
     part = tiles_per_partition * tile
     cap = 4 * part + 3 * tile
@@ -289,6 +297,13 @@ def test_fixed_split_grids_and_partition_sizes(dim, hq, hkv, tiles_per_partition
         assert torch.equal(one.view(torch.int32), other.view(torch.int32))
     out = torch.full((len(lengths), hq, dim), float("nan"), device="cuda", dtype=torch.bfloat16)
     _native.ml_merge(maxima, denoms, accums, out, len(lengths))
+    for rows in (None, cus):
+        *workspace, merged = split_fixed_rows(g, hkv, parts, part, rows=rows, decode=True)
+        for one, other in zip((maxima, denoms, accums), workspace):
+            assert torch.equal(one.view(torch.int32), other.view(torch.int32)), rows
+        assert torch.equal(merged.view(torch.int16), out.view(torch.int16)), \
+            f"pd_split_decode ({'walk' if rows else 'one workgroup per partition'}) " \
+            "differs from pd_ml_merge"
     torch.cuda.synchronize()
     m_ref, l_ref, a_ref = OS.split_partitions(*case, parts, part_size=part)
     np.testing.assert_array_equal(np.isinf(to_np(maxima)), np.isinf(m_ref))
