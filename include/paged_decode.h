@@ -191,23 +191,22 @@ int pd_split_fixed(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                    pd_stream_t stream);
 
 /* m/l/acc merge; replaces _merge (kernels.py:83-100) as launched by
- * paged_decode (runtime.py:114-116).  The reference's formula (M = max m_p,
- * f_p = exp(m_p - M), out = sum f_p acc_p / sum f_p l_p, a zero total
- * dividing by 1) is computed with a running maximum over the partitions from
- * the last to the first, skipping empty ones (m_p = -inf): the order in which
- * the fixed-split walk completes them, so pd_split_decode's in-kernel merge
- * gives the same bits.  Writes out rows [0, batch). */
+ * paged_decode (runtime.py:114-116): M = max m_p (-inf -> 0), f_p =
+ * exp(m_p - M), out = sum f_p acc_p / sum f_p l_p (a zero total divides by
+ * 1), the sums in partition order.  Writes out rows [0, batch). */
 int pd_ml_merge(const float* maxima, const float* denoms, const float* accums, void* out,
                 int32_t batch, int32_t num_heads, int32_t head_dim, int32_t partitions,
                 pd_stream_t stream);
 
-/* pd_split_fixed followed by pd_ml_merge into out: both launches of the
- * reference's fixed-split backend (runtime.py:111-116) in one call.  When the
- * walks fill the device, the walking workgroups merge their sequence's
- * partitions as they complete them and write out directly, with
- * pd_ml_merge's arithmetic (one launch); otherwise one workgroup runs per
- * partition and pd_ml_merge follows.  Both write the same workspace and
- * output bits. */
+/* The reference's fixed-split backend in one call (_split + _merge,
+ * runtime.py:111-116): the workspace as pd_split_fixed writes it, and the
+ * merged output in out.  When the walks fill the device, the walking
+ * workgroups merge their sequence's partitions as they complete them (from
+ * the last to the first, with a running maximum: the same formula as
+ * pd_ml_merge in another order and float32 rounding) and write out directly,
+ * in one launch; otherwise one workgroup runs per partition and a merge
+ * kernel with the walk's order and arithmetic follows.  Both grids write the
+ * same workspace and output bits. */
 int pd_split_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                     const void* k, const void* v,
                     const int32_t* table, int64_t table_stride_b, int32_t table_width,

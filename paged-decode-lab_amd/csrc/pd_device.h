@@ -332,22 +332,29 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ row, int 
 // and the output is acc * (1 / (total > 0 ? total : 1)).  This is the
 // reference's merge (kernels.py:83-100: maximum first, then the factors
 // exp(m_p - M)) computed as a running maximum, with its own float32 rounding.
-// ml_merge_kernel and the walk's in-kernel merge (cols_loader_kernel) both
-// use ml_step, so the two give the same bits.
+// ml_online_merge_kernel and the walk's in-kernel merge (cols_loader_kernel)
+// both use ml_step in that order, so the two give the same bits.
 struct MlStep {
   float a, b;  // factor of the running state and of the partition
   bool live;   // m_p > -inf
 };
 
 __device__ __forceinline__ MlStep ml_step(float m_p, float& M) {
-  if (m_p == -INFINITY) return MlStep{1.f, 0.f, false};
+  // Without a branch: both exponentials are computed and selected away for an
+  // empty partition (where M - mn may be -inf - (-inf)).
+  const bool live = m_p != -INFINITY;
   const float mn = fmaxf(M, m_p);
-  const MlStep st{exp_fast(M - mn), exp_fast(m_p - mn), true};
-  M = mn;
+  const float ea = exp_fast(M - mn), eb = exp_fast(m_p - mn);
+  const MlStep st{live ? ea : 1.f, live ? eb : 0.f, live};
+  M = live ? mn : M;
   return st;
 }
 
-// x of lane L + k, or -inf past lane 63 (k > 0, wavefront-uniform).
+
+
+// x of lane L + k, or -inf past lane 63 (k > 0, wavefront-uniform).  The
+// lane move runs in every lane: call it outside any lane-dependent branch (a
+// move compiled under a lane mask reads disabled lanes).
 __device__ __forceinline__ float lane_down_or_neg_inf(float x, int k, int lane) {
   const float y = __int_as_float(__builtin_amdgcn_ds_bpermute((lane + k) << 2, __float_as_int(x)));
   return lane + k < 64 ? y : -INFINITY;
@@ -376,25 +383,12 @@ __device__ __forceinline__ void ml_steps_of(float m0, float m1, int parts, int l
   const float hi = suffix_max(v1, lane);  // max over partitions >= L + 64
   const float hi_all = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(hi)));
   const float lo = fmaxf(suffix_max(v0, lane), hi_all);
-  // The maximum of the partitions after p (-inf after the last).  Every lane
-  // takes part in the lane moves: a move written inside `lane < 63 ? ... :`
-  // was compiled under that lane mask, and lane 62 then read the disabled
-  // lane 63.
+  // The maximum of the partitions after p (-inf after the last).
   const float after1 = lane_down_or_neg_inf(hi, 1, lane);
   const float after0 = fmaxf(lane_down_or_neg_inf(lo, 1, lane), lane == 63 ? hi_all : -INFINITY);
   float M0 = after0, M1 = after1;
   s0 = ml_step(v0, M0);
   s1 = ml_step(v1, M1);
-}
-
-// Step p of a row from ml_steps_of's per-lane steps (p wavefront-uniform).
-__device__ __forceinline__ MlStep wave_step(const MlStep& s0, const MlStep& s1, int p) {
-  const MlStep& src = p < 64 ? s0 : s1;
-  const int lane = p & 63;
-  return MlStep{
-      __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src.a), lane)),
-      __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src.b), lane)),
-      __builtin_amdgcn_readlane(int(src.live), lane) != 0};
 }
 
 // One wavefront merges columns [c0, c0 + C) (C a multiple of 4) of the G <= GP

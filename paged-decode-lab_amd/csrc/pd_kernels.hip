@@ -26,6 +26,7 @@
 // graph-capturable and replay correctly with new lengths, pages and KV.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdint>
@@ -62,6 +63,11 @@ struct MatchedShared {
 //             the reference launches _split (runtime.py:111-113).  Each
 //             partition's arithmetic is the walk's, so both write the same
 //             bits.
+//   kMatchedWalk  kMatched over `wf` consecutive splits of one (kv head,
+//             sequence) per workgroup (grid.x = ceil(splits / wf)), for
+//             plans with more workgroups than CUs: one resident round of
+//             workgroups instead of several.  Each split's arithmetic is
+//             kMatched's, so partials and LSEs are the same bits.
 // FP32 p goes through the bf16 MFMA as three bf16 terms hi + mid + lo (each
 // the RNE bf16 of the previous remainder), which represent p to 2^-27 of its
 // value, finer than p's own float32 rounding; with exact bf16 x bf16 products
@@ -77,7 +83,7 @@ struct MatchedShared {
 // A workgroup serves query heads [qb, qb + Gs) of kv head kh: the whole group
 // (hs = 1) when it has at most 16 heads, else 16-head slices of it (grid.y =
 // Hkv * hs), so the base and fixed-split protocols also cover G > 16.
-constexpr int kMatched = 0, kBase = 1, kSplit = 2, kSplitPart = 3;
+constexpr int kMatched = 0, kBase = 1, kSplit = 2, kSplitPart = 3, kMatchedWalk = 4;
 
 // Split counters of the fused launch: four per (sequence, kv head), one per
 // column slice of the single-tile kernel (the multi-tile kernels use the
@@ -245,15 +251,17 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
                    const uint16_t* __restrict__ v, float* __restrict__ partials,
                    float* __restrict__ lse_out, int* __restrict__ counters,
                    uint16_t* __restrict__ out, float* __restrict__ maxima, int Hkv, int splits,
-                   float scale, float c) {
+                   float scale, float c, int wf) {
   static_assert(kMode == kMatched || !kFused, "only the matched protocol has a fused merge");
-  static_assert(kHeads == 1 || kMode != kMatched, "kv-head groups change the tile of the protocol");
+  // The matched protocol's arithmetic (bf16 p, exp2, normalized partial + LSE).
+  constexpr bool kMatchedArith = kMode == kMatched || kMode == kMatchedWalk;
+  static_assert(kHeads == 1 || !kMatchedArith, "kv-head groups change the tile of the protocol");
   static_assert(kHeads == 1 || ((kHeads == 2 || kHeads == 4) && D == 64), "kv-head groups at D = 64 only");
   using C = Matched<D, GP>;
   using P = TileP<D>;
   constexpr int TILE = C::kTile;        // tile rows: TILE / kHeads tokens of kHeads kv heads
   constexpr int TTOK = TILE / kHeads;   // tokens per tile
-  constexpr int kTerms = kMode == kMatched ? 1 : 3;
+  constexpr int kTerms = kMatchedArith ? 1 : 3;
   constexpr int kStage = TILE * D * 2;  // bytes of one K or V stage
   constexpr int kCopies = C::kDma;      // 1 KiB copies per loader, tensor and tile
   constexpr int kPieces = D / 8;        // 16-byte pieces per K row
@@ -279,14 +287,17 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   // stored them itself stood still for about 1-2 us per partition (its stores
   // wait behind the loaders' copies), which every wavefront then waited for
   // at the next barrier.
-  constexpr bool kWalk = kMode == kSplit;
-  constexpr bool kFlush = kMode == kSplit || kMode == kSplitPart;
+  // kWalk: several partitions per workgroup, [p, p_end) (all of the
+  // sequence's for kSplit, whose launch passes wf = splits).
+  constexpr bool kWalk = kMode == kSplit || kMode == kMatchedWalk;
+  constexpr bool kFlush = kMode == kSplit || kMode == kSplitPart || kMode == kMatchedWalk;
   constexpr int kFbPitch = D + 4;                 // floats per head row of fb
   constexpr int kFbPasses = GP * D >= 1024 ? GP * D / 1024 : 1;  // 16-byte stores per loader lane
   __shared__ __attribute__((aligned(16))) float fb[kFlush ? GP * kFbPitch : 4];
   __shared__ float fm[16];
-  constexpr int kEmptyMode = kFlush ? kSplit : kMode;  // write_empty_partition's protocol
-  const int p = kWalk ? 0 : int(blockIdx.x);
+  constexpr int kEmptyMode = kMatchedArith ? kMatched : (kFlush ? kSplit : kMode);  // write_empty_partition's
+  const int p = kWalk ? int(blockIdx.x) * wf : int(blockIdx.x);
+  const int p_end = kWalk ? min(p + wf, splits) : p + 1;  // partitions [p, p_end) of this workgroup
   const int kh = blockIdx.y / hs, slice = blockIdx.y % hs;
   const int kvh = kHeads * kh;                      // (first) kv head of this workgroup
   const int qb = kvh * G + 16 * slice;              // first query head of this workgroup
@@ -303,7 +314,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   PageWindow<2> pw;
   if (loader) pw.load(table + int64_t(b) * tsb, width, start >> 8, lane);
   const int length = order >= 0 ? seq.length : lengths[b];
-  const int end = min(kWalk ? splits * T : start + T, length);
+  const int end = min(p_end * T, length);
   const int count = end > start ? (end - start + TTOK - 1) / TTOK : 0;
   const int tpp = T / TTOK;  // tiles per partition of the walk
   const int64_t RS = int64_t(Hkv) * D;
@@ -347,6 +358,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     // copies are issued.  In-order completion then lets the next wait for K
     // cover the stores too.
     u32x4_t fx[kFbPasses];
+    u32x4_t fd[kMatchedArith ? kFbPasses : 1];  // denominator shares of the pass's head
     uint32_t fmx = 0, fl[4] = {0, 0, 0, 0};
     auto flush_read = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -355,6 +367,12 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
         const int h = min(f / D, GP - 1);  // rows past GP are never stored
         fx[i] = lds_read16_at(lds_address(reinterpret_cast<const char*>(fb)) +
                               uint32_t(h * kFbPitch + f % D) * 4);
+        if constexpr (kMatchedArith) {
+          const int hh = h & 15;
+#pragma unroll
+          for (int x = 0; x < 4; ++x)
+            fd[i][x] = lds_read4_at(lds_address(reinterpret_cast<const char*>(&sm.lsum[x][hh])));
+        }
       }
       if (w == 0) {
         const int h = lane & 15;
@@ -364,6 +382,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
           fl[x] = lds_read4_at(lds_address(reinterpret_cast<const char*>(&sm.lsum[x][h])));
       }
       lds_wait(fx);
+      if constexpr (kMatchedArith) lds_wait(fd);
       asm volatile("" : "+v"(fmx), "+v"(fl[0]), "+v"(fl[1]), "+v"(fl[2]), "+v"(fl[3]));
     };
     auto flush_store = [&](int part) __attribute__((always_inline)) {
@@ -373,14 +392,30 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
         const int h = f / D;
         if (h < Gs) {
           const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + part;
+          if constexpr (kMatchedArith) {
+            // partial = acc * rcp(denominator), as the epilogue below.
+            const float den = (__uint_as_float(fd[i][0]) + __uint_as_float(fd[i][1])) +
+                              (__uint_as_float(fd[i][2]) + __uint_as_float(fd[i][3]));
+            const float inv = rcp_fast(den > 0.f ? den : 1.f);
+            fx[i] = u32x4_t{__float_as_uint(__uint_as_float(fx[i][0]) * inv),
+                            __float_as_uint(__uint_as_float(fx[i][1]) * inv),
+                            __float_as_uint(__uint_as_float(fx[i][2]) * inv),
+                            __float_as_uint(__uint_as_float(fx[i][3]) * inv)};
+          }
           *reinterpret_cast<u32x4_t*>(partials + orow * D + f % D) = fx[i];
         }
       }
       if (w == 0 && lane < Gs) {
         const int64_t orow = (int64_t(b) * Hq + qb + lane) * splits + part;
-        maxima[orow] = __uint_as_float(fmx);
-        lse_out[orow] = (__uint_as_float(fl[0]) + __uint_as_float(fl[1])) +
-                        (__uint_as_float(fl[2]) + __uint_as_float(fl[3]));
+        const float den = (__uint_as_float(fl[0]) + __uint_as_float(fl[1])) +
+                          (__uint_as_float(fl[2]) + __uint_as_float(fl[3]));
+        if constexpr (kMatchedArith) {
+          const float safe = den > 0.f ? den : 1.f;
+          lse_out[orow] = den > 0.f ? fmaf(__uint_as_float(fmx), scale, ln_fast(safe)) : -INFINITY;
+        } else {
+          maxima[orow] = __uint_as_float(fmx);
+          lse_out[orow] = den;
+        }
       }
     };
     for (int ti = count - 1; ti >= 0; --ti) {
@@ -412,11 +447,11 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   }
 
   if (!kFused && count == 0) {
-    for (int pp = p; pp < (kWalk ? splits : p + 1); ++pp)
+    for (int pp = p; pp < p_end; ++pp)
       write_empty_partition<D, kEmptyMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out,
                                            out, maxima);
     // The walk's merged output of an empty sequence is 0 (no live partition).
-    if (kWalk && out != nullptr)
+    if (kMode == kSplit && out != nullptr)
       write_empty_partition<D, kBase>(tid, b, Hq, qb, Gs, splits, 0, partials, lse_out, out,
                                       maxima);
     return;
@@ -458,19 +493,19 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   float m_own = -INFINITY;  // running max of head qh
   float l_own = 0.f;        // this lane's share of head qh's denominator
   // The walk with an output (out != nullptr) also merges the partitions as it
-  // completes them, with ml_merge_kernel's arithmetic (ml_step): running
+  // completes them, with ml_online_merge_kernel's arithmetic (ml_step): running
   // maxima mM of heads 4 qg + r, merged accumulators mO (the lane's columns of
   // acc) and totals mT.  A partition's denominator needs every wavefront's
   // share (sm.lsum), so its steps mS wait (`pending`) for the next barrier
   // every wavefront passes: B1 of the next tile, or the last partition's own.
   // The next flush writes sm.lsum after B2 of the following tile, when these
   // reads (before the wavefront reaches B2) are done.
-  const bool merge_out = kWalk && out != nullptr;
+  const bool merge_out = kMode == kSplit && out != nullptr;
   bool pending = false;
   floatx4_t mO[P::kNBW];
   float mM[4], mT[4];
   MlStep mS[4];
-  if (kWalk) {
+  if (kMode == kSplit) {
 #pragma unroll
     for (int j = 0; j < P::kNBW; ++j) mO[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -507,7 +542,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
             __builtin_bit_cast(bf16x8_t, kr[g * C::kCH + ch]), qf[ch], s[g], 0, 0, 0);
     }
     mfma_result_barrier(s);
-    if constexpr (kMode != kMatched) {
+    if constexpr (!kMatchedArith) {
       // Scores in the reference's units: dot(q, k) * SCALE (kernels.py:30).
 #pragma unroll
       for (int g = 0; g < C::kNG; ++g)
@@ -539,7 +574,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     float (*wm)[16] = sm.wmax[ti & 1];
     if (lane < 16) wm[w][lane] = mx;
     lds_barrier();  // B1(ti)
-    if constexpr (kWalk) {
+    if constexpr (kMode == kSplit) {
       // The denominators of the partition flushed after the previous tile
       // were written to LDS before this barrier.
       if (pending) {
@@ -558,12 +593,12 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       const float tm = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
       const float mn = fmaxf(m4[r], tm);
       moved |= mn != m4[r];
-      alpha[r] = kMode == kMatched ? exp2_fast((m4[r] - mn) * c) : exp_fast(m4[r] - mn);
+      alpha[r] = kMatchedArith ? exp2_fast((m4[r] - mn) * c) : exp_fast(m4[r] - mn);
       m4[r] = mn;
     }
     const float tm = fmaxf(fmaxf(wm[0][qh], wm[1][qh]), fmaxf(wm[2][qh], wm[3][qh]));
     const float mn = fmaxf(m_own, tm);
-    const float a_own = kMode == kMatched ? exp2_fast((m_own - mn) * c) : exp_fast(m_own - mn);
+    const float a_own = kMatchedArith ? exp2_fast((m_own - mn) * c) : exp_fast(m_own - mn);
     m_own = mn;
     const float neg_mc = -(mn * c);
     float psum = 0.f;
@@ -572,13 +607,13 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       float pr[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pr[r] = kMode == kMatched ? exp2_fast(fmaf(s[g][r], c, neg_mc)) : exp_fast(s[g][r] - mn);
+        pr[r] = kMatchedArith ? exp2_fast(fmaf(s[g][r], c, neg_mc)) : exp_fast(s[g][r] - mn);
         psum += pr[r];
       }
       // P[head qh][tile rows kTW w + 16g + 4qg .. +3] into row qh of each
       // term's LDS tile.
       const int pofs = qh * P::kPitch + (w * C::kTW + 16 * g + 4 * qg) * 2;
-      if constexpr (kMode == kMatched) {
+      if constexpr (kMatchedArith) {
         *reinterpret_cast<u32x2_t*>(ps[0] + pofs) =
             u32x2_t{qh < Gs ? pack_bf16(pr[0], pr[1]) : 0u, qh < Gs ? pack_bf16(pr[2], pr[3]) : 0u};
       } else {
@@ -658,9 +693,9 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 
   if constexpr (kWalk) {
     // Partitions past the sequence's last token are empty.
-    for (int pp = (end + T - 1) / T; pp < splits; ++pp)
-      write_empty_partition<D, kSplit>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out, out,
-                                       maxima);
+    for (int pp = (end + T - 1) / T; pp < p_end; ++pp)
+      write_empty_partition<D, kEmptyMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out,
+                                           out, maxima);
     if (merge_out) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1084,20 +1119,98 @@ lse_merge_kernel(const float* __restrict__ partials, const float* __restrict__ l
 }
 
 // ------------------------------------------------------------ m/l/acc merge
-// The merge of the fixed-split protocol (kernels.py:83-100) in the online
-// form of ml_step (pd_device.h): partitions p = P - 1 down to 0, empty ones
-// skipped, a running maximum, out = acc / total (a zero total divides by 1).
-// Up to 128 partitions: one wavefront per (b, h) row and 64 E columns (grid
-// rows x D / (64 E)), E consecutive columns per lane; E = 1 spreads a row over
-// D / 64 CUs when there are few rows.  Lane j loads m and l of partitions j
-// and j + 64 and computes their steps (ml_steps_of); the accumulator loads of
-// the first kBatch partitions (from the top) are issued before that, later
-// batches as the chain reaches them.  Loads past the row read zero and belong
-// to no partition, so neither E nor kBatch changes the result's bits, and the
-// walk's in-kernel merge (cols_loader_kernel, kSplit) gives the same bits.
+// The merge of the fixed-split protocol (kernels.py:83-100): M = max_p m_p
+// (-inf -> 0), f_p = exp(m_p - M), out = sum_p f_p acc_p / sum_p f_p l_p (a
+// zero total divides by 1).  Up to 128 partitions: one wavefront per (b, h)
+// row and 64 E columns (grid rows x D / (64 E)), E consecutive columns per
+// lane; E = 1 spreads a row over D / 64 CUs when there are few rows.  Lane j
+// loads m and l of partitions j and j + 64; every accumulator load of a batch
+// of kBatch partitions is issued before the factors are computed
+// (merge_splits), the total is an xor-butterfly sum over the lanes, and
+// acc = fma(f_p, acc_p, acc) runs in partition order.  Loads past the row read
+// zero and carry f = 0, so neither E nor kBatch changes the result's bits.
 template <int E, int kBatch>
 __global__ void __launch_bounds__(64)
 ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
+                const float* __restrict__ accums, uint16_t* __restrict__ out, int parts, int D) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int col = (blockIdx.y * 64 + lane) * E;
+  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(maxima + row * parts, parts * 4);
+  const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(denoms + row * parts, parts * 4);
+  float m0[1], m1[1], l0[1], l1[1];
+  buffer_load_f32<1, 0>(rm, lane * 4, m0);
+  buffer_load_f32<1, 0>(rm, (lane + 64) * 4, m1);
+  buffer_load_f32<1, 0>(rl, lane * 4, l0);
+  buffer_load_f32<1, 0>(rl, (lane + 64) * 4, l1);
+  float f0 = 0.f, f1 = 0.f, inv = 1.f, acc[E];
+  merge_splits<E, 0, kBatch>(
+      accums + row * parts * D, D, col, parts,
+      [&] {
+        const float v0 = lane < parts ? m0[0] : -INFINITY;
+        const float v1 = lane + 64 < parts ? m1[0] : -INFINITY;
+        float mx = wave_max(fmaxf(v0, v1));
+        if (mx == -INFINITY) mx = 0.f;  // all partitions empty
+        f0 = exp_fast(v0 - mx);
+        f1 = exp_fast(v1 - mx);
+        const float total = wave_sum(fmaf(l1[0], f1, l0[0] * f0));
+        inv = 1.f / (total > 0.f ? total : 1.f);
+      },
+      [&](int s0, int j) { return wave_weight(f0, f1, s0 + j); }, acc);
+#pragma unroll
+  for (int e = 0; e < E; ++e) out[row * D + col + e] = uint16_t(bf16_bits(acc[e] * inv));
+}
+
+// The same merge for more than 128 partitions: one wavefront per row, lane j
+// owning columns VEC j .. VEC j + VEC - 1, partitions in order.
+template <int VEC>
+__global__ void __launch_bounds__(64)
+ml_merge_loop_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
+                     const float* __restrict__ accums, uint16_t* __restrict__ out, int parts) {
+  constexpr int D = VEC * 64;
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* mrow = maxima + int64_t(row) * parts;
+  const float* lrow = denoms + int64_t(row) * parts;
+  float mx = -INFINITY;
+  for (int p = lane; p < parts; p += 64) mx = fmaxf(mx, mrow[p]);
+  mx = wave_max(mx);
+  if (mx == -INFINITY) mx = 0.f;  // all partitions empty
+  float total = 0.f, acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  const float* arow = accums + int64_t(row) * parts * D + lane * VEC;
+  for (int p = 0; p < parts; ++p) {
+    const float f = exp_fast(mrow[p] - mx);
+    total += lrow[p] * f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = fmaf(arow[int64_t(p) * D + e], f, acc[e]);
+  }
+  const float inv = 1.f / (total > 0.f ? total : 1.f);
+  uint16_t* dst = out + int64_t(row) * D + lane * VEC;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) dst[e] = uint16_t(bf16_bits(acc[e] * inv));
+}
+
+// ----------------------------------------------------- online m/l/acc merge
+// The merge of pd_split_decode's one-workgroup-per-partition grid: the
+// fixed-split merge (kernels.py:83-100) in the online form of ml_step (pd_device.h): partitions p = P - 1 down to 0, empty ones
+// skipped, a running maximum, out = acc / total (a zero total divides by 1).
+// Up to 128 partitions: one wavefront per (b, h) row and 64 E columns (grid
+// rows x D / (64 E)), E consecutive columns per lane; E = 1 spreads a row over
+// D / 64 CUs when there are few rows.  The accumulator loads of kBatch
+// partitions (from the top) are issued first; lane j loads m and l of
+// partitions j and j + 64 and computes their steps' factors (ml_steps_of)
+// while they arrive.  The chain acc = fma(acc_p, b, acc * a) then takes each
+// partition's factors with v_readlane, eight partitions at a time.  An empty
+// partition's a = 1, b = 0 over its zero accumulators (as the partition
+// kernels write them) leave acc and total unchanged, as skipping it does, and
+// so do the padding steps past partition 0 over zero loads: the chain has no
+// branch.  Neither E nor kBatch changes the result's bits, and the walk's
+// in-kernel merge (cols_loader_kernel, kSplit) gives the same bits.
+template <int E, int kBatch>
+__global__ void __launch_bounds__(64)
+ml_online_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
                 const float* __restrict__ accums, uint16_t* __restrict__ out, int parts, int D) {
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x;
@@ -1123,23 +1236,36 @@ ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ deno
   __builtin_amdgcn_sched_barrier(0);
   MlStep s0, s1;
   ml_steps_of(m0[0], m1[0], parts, lane, s0, s1);
+  // Loads past the row read zero, so the l of a padding partition is 0.
   float acc[E], total = 0.f;
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  for (int top = parts; top > 0; top -= kBatch) {
+  // A do-while (parts >= 1): a loop guard in front would let the compiler
+  // sink the first batch's loads past the factors' computation.
+  int top = parts;
+  do {
     if (top != parts) load(top);
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
+      if (j % 8 == 0) __builtin_amdgcn_sched_barrier(0);  // bounds the readlanes in flight
       const int p = top - 1 - j;
-      if (p < 0) break;
-      const MlStep st = wave_step(s0, s1, p);
-      if (!st.live) continue;
-      const float lp = wave_weight(l0[0], l1[0], p);
+      const int src = p & 63;
+      const bool upper = p >= 64;
+      // Read unconditionally, then select: a lane read under a branch would
+      // need the branch.
+      const float ra = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, upper ? s1.a : s0.a), src));
+      const float rb = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, upper ? s1.b : s0.b), src));
+      const float rl_ = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, upper ? l1[0] : l0[0]), src));
+      const float a = p < 0 ? 1.f : ra, bp = p < 0 ? 0.f : rb, lp = p < 0 ? 0.f : rl_;
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] = fmaf(x[j][e], st.b, acc[e] * st.a);
-      total = fmaf(lp, st.b, total * st.a);
+      for (int e = 0; e < E; ++e) acc[e] = fmaf(x[j][e], bp, acc[e] * a);
+      total = fmaf(lp, bp, total * a);
     }
-  }
+    top -= kBatch;
+  } while (top > 0);
   const float inv = 1.f / (total > 0.f ? total : 1.f);
 #pragma unroll
   for (int e = 0; e < E; ++e) out[row * D + col + e] = uint16_t(bf16_bits(acc[e] * inv));
@@ -1150,7 +1276,7 @@ ml_merge_kernel(const float* __restrict__ maxima, const float* __restrict__ deno
 // the last.
 template <int VEC>
 __global__ void __launch_bounds__(64)
-ml_merge_loop_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
+ml_online_merge_loop_kernel(const float* __restrict__ maxima, const float* __restrict__ denoms,
                      const float* __restrict__ accums, uint16_t* __restrict__ out, int parts) {
   constexpr int D = VEC * 64;
   const int row = blockIdx.x;
@@ -1229,6 +1355,7 @@ struct PartitionArgs {
   int Hq, Hkv, G, hs, splits, T;
   float scale, c;
   int order = -1;  // batch order of the multi-tile kernels (batch_order)
+  int wf = 1;      // partitions per workgroup of the walks (kSplit, kMatchedWalk)
 };
 
 // Compute units of the current device, queried once per device.
@@ -1292,7 +1419,7 @@ void launch_cols_loader(int gp, dim3 grid, hipStream_t stream, const PartitionAr
   hipLaunchKernelGGL((cols_loader_kernel<D, GPV, kFused, kMode, kHeads>), grid, dim3(2 * kThreads), 0, \
                      stream, a.table, a.lengths, a.q, a.tsb, a.width, a.order, a.T, a.qsb,     \
                      a.qsh, a.G, a.hs, a.Hq, a.k, a.v, a.partials, a.lse, a.counters, a.out,   \
-                     a.maxima, a.Hkv, a.splits, a.scale, a.c)
+                     a.maxima, a.Hkv, a.splits, a.scale, a.c, a.wf)
   switch (gp) {
     case 1: PD_LAUNCH_LOADER(1); break;
     case 2: PD_LAUNCH_LOADER(2); break;
@@ -1302,6 +1429,10 @@ void launch_cols_loader(int gp, dim3 grid, hipStream_t stream, const PartitionAr
   }
 #undef PD_LAUNCH_LOADER
 }
+
+// Longest split (in tiles) that the matched protocol walks several of per
+// workgroup (partition_entry).
+constexpr int kWalkMaxSplitTiles = 5;
 
 int padded_group(int g) {
   int gp = 1;
@@ -1359,6 +1490,31 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
       case 257: launch_tile_d<128, true>(gp, grid, st, a); break;
       case 512: launch_tile_d<256, false>(gp, grid, st, a); break;
       default: launch_tile_d<256, true>(gp, grid, st, a); break;
+    }
+    return launch_status(what);
+  }
+  // Plans of short splits with more workgroups than CUs walk wf consecutive
+  // splits per workgroup (kMatchedWalk), so that one resident round of
+  // workgroups runs them; every split keeps its bits.  A workgroup's start
+  // (table, query and first tiles in flight) then runs once instead of wf
+  // times, but each split before the last is stored while the K / V stream
+  // runs, which costs a few microseconds when every CU streams.  Paired A/B
+  // at Hq 16 / Hkv 4 / D 256 (walk against one workgroup per split): splits
+  // of 2 to 5 tiles 1.2-19% faster (ctx 8192 x 2 sequences, 2064 x 8 and x 16,
+  // 32768, 8192 x 4); splits of 9 or 10 tiles 1-13% slower (4096 x 16,
+  // 8192 x 8, 16384 x 4, 32768 x 2, 65536), with one exception (2064 x 32,
+  // whose last splits are short).
+  const int cus = device_cu_count();
+  const int64_t wgs = int64_t(splits) * num_kv_heads * batch;
+  if (!fused && cus > 0 && splits > 1 && wgs > cus &&
+      tokens_per_split <= kWalkMaxSplitTiles * tile_tokens) {
+    a.wf = int(std::min<int64_t>((wgs + cus - 1) / cus, splits));
+    const dim3 wgrid((splits + a.wf - 1) / a.wf, num_kv_heads, batch);
+    a.order = batch_order(wgrid);
+    switch (head_dim) {
+      case 64: launch_cols_loader<64, false, kMatchedWalk>(gp, wgrid, st, a); break;
+      case 128: launch_cols_loader<128, false, kMatchedWalk>(gp, wgrid, st, a); break;
+      default: launch_cols_loader<256, false, kMatchedWalk>(gp, wgrid, st, a); break;
     }
     return launch_status(what);
   }
@@ -1540,8 +1696,12 @@ extern "C" int pd_matched_decode_noalloc(const void* q, int64_t q_stride_b, int6
 
 namespace {
 
-// ml_merge_kernel (up to 128 partitions) or ml_merge_loop_kernel over `rows`
-// (b, h) rows; arguments checked by the caller.
+// The m/l/acc merge over `rows` (b, h) rows, up to 128 partitions in one
+// wavefront per row and 64 E columns, more in one wavefront per row:
+// ml_merge_kernel / ml_merge_loop_kernel (the reference's order), or with
+// kOnline their online forms (pd_split_decode's order).  Arguments checked by
+// the caller.
+template <bool kOnline>
 void launch_ml_merge(const float* maxima, const float* denoms, const float* accums, uint16_t* o,
                      int64_t rows, int head_dim, int partitions, hipStream_t st) {
   if (partitions <= 128) {
@@ -1554,8 +1714,12 @@ void launch_ml_merge(const float* maxima, const float* denoms, const float* accu
     while (batch < partitions && batch < (E == 1 ? 48 : 16)) batch = batch < 32 ? 2 * batch : 48;
     const dim3 grid(unsigned(rows), head_dim / (64 * E));
 #define PD_LAUNCH_ML(EV, KB)                                                                   \
-  hipLaunchKernelGGL((ml_merge_kernel<EV, KB>), grid, dim3(64), 0, st, maxima, denoms, accums, \
-                     o, partitions, head_dim)
+  if (kOnline)                                                                                 \
+    hipLaunchKernelGGL((ml_online_merge_kernel<EV, KB>), grid, dim3(64), 0, st, maxima, denoms,  \
+                       accums, o, partitions, head_dim);                                       \
+  else                                                                                         \
+    hipLaunchKernelGGL((ml_merge_kernel<EV, KB>), grid, dim3(64), 0, st, maxima, denoms, accums, \
+                       o, partitions, head_dim)
     switch (E * 100 + batch) {
       case 104: PD_LAUNCH_ML(1, 4); break;
       case 108: PD_LAUNCH_ML(1, 8); break;
@@ -1574,16 +1738,28 @@ void launch_ml_merge(const float* maxima, const float* denoms, const float* accu
   }
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(ml_merge_loop_kernel<1>, dim3(rows), dim3(64), 0, st, maxima, denoms,
-                         accums, o, partitions);
+      if (kOnline)
+        hipLaunchKernelGGL(ml_online_merge_loop_kernel<1>, dim3(rows), dim3(64), 0, st, maxima,
+                           denoms, accums, o, partitions);
+      else
+        hipLaunchKernelGGL(ml_merge_loop_kernel<1>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                           accums, o, partitions);
       break;
     case 128:
-      hipLaunchKernelGGL(ml_merge_loop_kernel<2>, dim3(rows), dim3(64), 0, st, maxima, denoms,
-                         accums, o, partitions);
+      if (kOnline)
+        hipLaunchKernelGGL(ml_online_merge_loop_kernel<2>, dim3(rows), dim3(64), 0, st, maxima,
+                           denoms, accums, o, partitions);
+      else
+        hipLaunchKernelGGL(ml_merge_loop_kernel<2>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                           accums, o, partitions);
       break;
     default:
-      hipLaunchKernelGGL(ml_merge_loop_kernel<4>, dim3(rows), dim3(64), 0, st, maxima, denoms,
-                         accums, o, partitions);
+      if (kOnline)
+        hipLaunchKernelGGL(ml_online_merge_loop_kernel<4>, dim3(rows), dim3(64), 0, st, maxima,
+                           denoms, accums, o, partitions);
+      else
+        hipLaunchKernelGGL(ml_merge_loop_kernel<4>, dim3(rows), dim3(64), 0, st, maxima, denoms,
+                           accums, o, partitions);
       break;
   }
 }
@@ -1673,17 +1849,18 @@ int launch_online(const void* q, int64_t qsb, int64_t qsh, const void* k, const 
   // _split grid does (runtime.py:111-113).
   const bool per_part = kSplitMode && per_partition_grid(parts, ygrid, batch);
   const dim3 grid(per_part ? parts : 1, ygrid, batch);
+  a.wf = kSplitMode ? parts : 1;  // the walk covers every partition
   a.order = batch_order(grid);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (per_part) {
-    // One workgroup per partition; with an output, ml_merge_kernel merges
-    // them after (the walk's in-kernel merge has the same arithmetic).
+    // One workgroup per partition; with an output, ml_online_merge_kernel
+    // merges them after (the walk's in-kernel merge has the same arithmetic).
     a.out = nullptr;
     launch_online_mode<kSplitPart>(head_dim, heads, G, grid, st, a);
     if (int s = launch_status(what)) return s;
     if (out) {
-      launch_ml_merge(maxima, denoms, accums, static_cast<uint16_t*>(out), int64_t(batch) * num_heads,
-                      head_dim, parts, st);
+      launch_ml_merge<true>(maxima, denoms, accums, static_cast<uint16_t*>(out),
+                            int64_t(batch) * num_heads, head_dim, parts, st);
     }
   } else {
     launch_online_mode<kSplitMode ? kSplit : kBase>(head_dim, heads, G, grid, st, a);
@@ -1732,8 +1909,8 @@ extern "C" int pd_ml_merge(const float* maxima, const float* denoms, const float
     return pd::fail(PD_EINVAL, "invalid or missing preallocated split-K workspace");
   const int64_t rows = int64_t(batch) * num_heads;
   if (rows > 0x7fffffff) return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
-  launch_ml_merge(maxima, denoms, accums, static_cast<uint16_t*>(out), rows, head_dim, partitions,
-                  reinterpret_cast<hipStream_t>(stream));
+  launch_ml_merge<false>(maxima, denoms, accums, static_cast<uint16_t*>(out), rows, head_dim,
+                         partitions, reinterpret_cast<hipStream_t>(stream));
   return launch_status("pd_ml_merge");
 }
 

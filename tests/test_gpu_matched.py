@@ -355,3 +355,35 @@ def test_single_tile_and_multi_tile_kernels_agree_on_one_tile(dim, hq, hkv):
         out[tokens] = (partials, lse)
     assert torch.equal(out[tile][1].view(torch.int32), out[2 * tile][1].view(torch.int32))
     assert torch.equal(out[tile][0].view(torch.int32), out[2 * tile][0].view(torch.int32))
+
+
+@pytest.mark.parametrize("dim,hq,hkv,cap,splits", [(128, 32, 8, 2048, 8), (256, 16, 8, 1024, 8),
+                                                   (64, 16, 8, 4096, 8), (256, 32, 4, 3000, 12)])
+def test_walk_of_several_splits_per_workgroup(dim, hq, hkv, cap, splits):
+    """Plans with more (split, kv head, sequence) workgroups than CUs run one resident round
+    in which each workgroup walks several consecutive splits of its sequence.  Every split
+    must keep its bits: each row of such a batch (8 sequences, splits x kv heads x 8 > 256
+    workgroups) equals the same sequence run alone (one workgroup per split), partials, LSEs
+    and output bit for bit, from NaN workspaces; and the batch passes the oracle's gate."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    batch = 8
+    assert splits * hkv * batch > cus >= splits * hkv, "the batch must walk, one sequence not"
+    tile = 16384 // dim
+    part = -(-(-(-cap // tile)) // splits) * tile
+    lengths = [0, 1, part - 1, part, part + 1, 3 * part + tile // 2, cap - 1, cap]
+    case = make_case(lengths, hq, hkv, dim, seed=splits + dim, capacity=cap)
+    poison_tails(*case[1:3], case[3], case[4])
+    spec = DecodeSpec(batch, hq, hkv, dim, cap)
+    g, res, out = run(case, spec, num_splits=splits)
+    assert res.plan.splits == splits and res.plan.tokens_per_split == part
+    check_all(case, g, res, out, where=f"walk D{dim} {hq}/{hkv} {splits}x{part}")
+    q, k, v, table, lens = g
+    for i in range(batch):
+        alone = allocate_matched_resources(DecodeSpec(1, hq, hkv, dim, cap), "cuda",
+                                           num_splits=splits)
+        poison_workspace(alone)
+        one = matched_decode(q[i:i + 1], k, v, table[i:i + 1], lens[i:i + 1], resources=alone)
+        torch.cuda.synchronize()
+        assert torch.equal(one.view(torch.int16), out[i:i + 1].view(torch.int16)), f"row {i}"
+        assert torch.equal(alone.partials.view(torch.int32), res.partials[i:i + 1].view(torch.int32))
+        assert torch.equal(alone.lse.view(torch.int32), res.lse[i:i + 1].view(torch.int32))
