@@ -280,10 +280,11 @@ def bandwidth_sweep(torch, seed=64, calls=20):
     return result
 
 
-def context_sweep(torch, contexts=(8192, 32768, 65536, 131072)):
-    """D256 GQA 4:1 (Hq 16, Hkv 4), B=1 at longer contexts, planner plan.  At 131072
-    tokens the KV (537 MB) exceeds the 256 MB last-level cache, so the reads come
-    from HBM; the shorter ones are partly cache-resident across replays."""
+def context_sweep(torch, contexts=(8192, 16384, 32768, 49152, 65536, 131072)):
+    """D256 GQA 4:1 (Hq 16, Hkv 4), B=1 at longer contexts, planner plan.  The KV of one
+    call (33.6 MB at 8192 tokens, 537 MB at 131072) stays partly in the 256 MB last-level
+    cache across replays up to about 65536 tokens; ``hbm_*`` gives the same call with its
+    tables cycling over page sets of at least 1 GB in total, so that it reads HBM."""
     out = {}
     for ctx in contexts:
         case = matched_case(torch, 1, 16, 4, 256, ctx, [ctx], 11)
@@ -295,13 +296,18 @@ def context_sweep(torch, contexts=(8192, 32768, 65536, 131072)):
         nbytes = algorithmic_bytes([ctx], 1, 16, 4, 256)
         pbytes = algorithmic_bytes([ctx], 1, 16, 4, 256, with_output=False)
         p = case["plan"]
+        kv_bytes = 2 * ctx * 4 * 256 * 2
+        hbm_us, copies, _ = hbm_resident_rate(torch, case, copies=max(2, -(-1_070_000_000 // kv_bytes)))
         out[f"ctx_{ctx}"] = {"plan": f"{p.splits}x{p.tokens_per_split}",
                              "us_per_call": round(us, 2), "tbps": round(nbytes / us / 1e6, 3),
                              "pct_peak": round(100 * nbytes / us / 1e6 / PEAK_TBPS, 1),
                              "fused_us_per_call": round(fused_us, 2),
                              "fused_pct_peak": round(100 * nbytes / fused_us / 1e6 / PEAK_TBPS, 1),
                              "partition_us": round(part_us, 2),
-                             "partition_pct_peak": round(100 * pbytes / part_us / 1e6 / PEAK_TBPS, 1)}
+                             "partition_pct_peak": round(100 * pbytes / part_us / 1e6 / PEAK_TBPS, 1),
+                             "hbm_us_per_call": round(hbm_us, 2),
+                             "hbm_pct_peak": round(100 * nbytes / hbm_us / 1e6 / PEAK_TBPS, 1),
+                             "hbm_page_sets": copies}
         del case
         torch.cuda.empty_cache()
     return out
@@ -386,7 +392,7 @@ def small_batch_backends(torch, batches=(1, 8), seed=20261105):
     return out
 
 
-def batch_sweep_ctx2064(torch, batches=(8, 32)):
+def batch_sweep_ctx2064(torch, batches=(8, 16, 32)):
     """The headline shape (Hq 16, Hkv 4, D 256) at B sequences of 2064 tokens, planner plan:
     where the call's share of peak grows with the batch (hot cache)."""
     out = {}
@@ -540,7 +546,7 @@ def profile_launches(torch, which, calls=50):
     print(json.dumps({"profiled": which}))
 
 
-AB_WORKLOADS = ("headline", "partitions", "edge_d64", "edge_d256", "sweep")
+AB_WORKLOADS = ("headline", "partitions", "edge_d64", "edge_d256", "sweep", "shape")
 
 
 def ab_variants_paged(torch, q, k, v, table, lens, spec, backend, libraries):
@@ -615,7 +621,9 @@ def ab_report(torch, args):
       the rest U[1, 4096]; D 64 MHA 16/16, D 256 GQA 32/4) through --ab-backend
       (hip_base or hip_splitk);
     * sweep: the bandwidth-sweep batch (B=64, Hq 32 / Hkv 8 / D 128, lengths U[1, 32768],
-      pages over a 200 GB pool) through --ab-backend.
+      pages over a 200 GB pool) through --ab-backend;
+    * shape: the matched decode of --ab-shape B,Hq,Hkv,D,ctx (B sequences of ctx tokens),
+      planner plan.
     Outside headline the variants are current (this build) or NAME=PATH.  Every variant
     of a report uses the same workspace and output buffers (the placement of a workspace
     alone moves these times by a few percent), and each variant's output is copied right
@@ -672,7 +680,21 @@ def ab_report(torch, args):
         libraries = {item.split("=", 1)[0]: libraries.get(item.split("=", 1)[0])
                      for item in items}
         unrolls, replays = (4, 16), 5
-        if workload == "partitions":
+        if workload == "shape":
+            # --ab-shape B,Hq,Hkv,D,ctx: B sequences of ctx tokens (capacity ctx), planner plan.
+            b, hq, hkv, dim, cap = (int(x) for x in args.ab_shape.split(","))
+            from paged_decode.splitkv_plan import make_splitkv_plan
+            spec = DecodeSpec(b, hq, hkv, dim, cap)
+            plan = make_splitkv_plan(spec, torch.cuda.get_device_properties(0)
+                                     .multi_processor_count)
+            q, k, v, table, lens = make_inputs(torch, b, hq, hkv, dim, cap, [cap] * b, 7)
+            variants, outputs = ab_variants_matched(torch, q, k, v, table, lens, spec,
+                                                    plan.splits, plan.tokens_per_split,
+                                                    plan.lse_lanes, libraries)
+            unrolls, replays = (32, 128), 10
+            label = (f"matched decode B={b} Hq={hq} Hkv={hkv} D={dim} ctx {cap}, plan "
+                     f"{plan.splits}x{plan.tokens_per_split}")
+        elif workload == "partitions":
             part = args.ab_partition
             cap = max(2112, ctx)
             spec = DecodeSpec(batch, 16, 4, 256, cap)
@@ -783,6 +805,8 @@ def main():
     ap.add_argument("--ab-backend", default="hip_base",
                     choices=("hip_base", "hip_splitk", "matched"),
                     help="backend of the edge_d64 / edge_d256 / sweep A/B workloads")
+    ap.add_argument("--ab-shape", default="8,32,8,128,4096", metavar="B,Hq,Hkv,D,ctx",
+                    help="geometry of the shape A/B workload (matched decode, planner plan)")
     ap.add_argument("--ab-partition", type=int, default=1024,
                     help="partition tokens of the partitions A/B workload")
     ap.add_argument("--section", default=None, metavar="S1,S2,...",
