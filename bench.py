@@ -471,10 +471,14 @@ def profile_launches(torch, which, calls=50):
     calibrate: a 256 MiB device copy (known bytes: 256 MiB read + 256 MiB
     written), used to scale FETCH_SIZE / WRITE_SIZE.  headline: partition and
     merge at the headline shape.  sweep: partition and merge of the bandwidth sweep.
+    mid: partition and merge at D256 GQA 4:1, B=1, context 32768 (128 splits of 4 tiles,
+    walked two per workgroup).
     long: partition and merge at D256 GQA 4:1, B=1, context 131072 (KV from HBM).
     parts: the headline shape with 1024-token partitions (3 splits, 12 workgroups).
     edge: paged_decode's hip_base and hip_splitk on the edge-coverage batches (B=128,
     a quarter of the lengths 0, the rest U[1, 4096]; D 64 MHA 16/16, D 256 GQA 32/4).
+    small: paged_decode hip_base and hip_splitk at B=1 on the headline shape (the
+    small-batch chunks and their m/l/acc merge).
     decoder: the 24-layer random-init decoder, prompt 512, 16 greedy decode steps as
     hipGraph replays (the kernel mix of one decode step).
     """
@@ -510,6 +514,26 @@ def profile_launches(torch, which, calls=50):
             full()
         torch.cuda.synchronize()
         del case, full
+    if "mid" in which:
+        # 128 splits of 4 tiles: the partition walks two splits per workgroup.
+        case = matched_case(torch, 1, 16, 4, 256, 32768, [32768], 11)
+        for _ in range(calls):
+            case["partition"]()
+            case["merge"]()
+        torch.cuda.synchronize()
+        del case
+    if "small" in which:
+        # paged_decode at B=1 on the headline shape: one-workgroup chunks + m/l/acc merge.
+        from paged_decode.runtime import allocate_resources, paged_decode
+        from paged_decode.spec import DecodeSpec
+        q, k, v, table, lens = make_inputs(torch, 1, 16, 4, 256, 2112, [2064], 5)
+        for backend in ("hip_base", "hip_splitk"):
+            res = allocate_resources(DecodeSpec(1, 16, 4, 256, 2112), "cuda", backend)
+            for _ in range(calls):
+                paged_decode(q, k, v, table, lens, resources=res, backend=backend)
+            torch.cuda.synchronize()
+            del res
+        del q, k, v, table, lens
     if "long" in which:
         case = matched_case(torch, 1, 16, 4, 256, 131072, [131072], 11)
         for _ in range(10):
@@ -787,7 +811,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the extra measurements")
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU run")
-    ap.add_argument("--profile", default=None, metavar="headline,sweep,long,parts,edge,decoder",
+    ap.add_argument("--profile", default=None,
+                    metavar="headline,sweep,mid,long,parts,edge,small,decoder",
                     help="only make eager launches for rocprofv3 (calibration copy + cases)")
     ap.add_argument("--require-idle-gpu", action="store_true",
                     help="refuse to run (before any GPU work) if amd-smi lists other processes")
