@@ -77,6 +77,40 @@ def decode_metadata(block_tables, seq_lens, block_size=256, device="cuda"):
             torch.tensor(padded, dtype=torch.int32, device=device))
 
 
+class DecodeTimings:
+    """Per-step decode intervals of an engine, as the overlay's ModelRunner keeps them
+    when ``Config.record_decode_timings`` is set (engine/model_runner.py:203-211): a pair
+    of timing events around each decode step's model call (eager or graph replay) and
+    the step's batch.  Prefill steps, and every step while ``enabled`` is false, run
+    untimed.  ``intervals()`` reads them back in the form tools/benchmark_engine.py:66-67
+    reports, ``[{"milliseconds": ..., "batch": ...}]``; reading synchronizes on the last
+    event, so call it after the generation, not inside one."""
+
+    def __init__(self, enabled=True):
+        self.enabled = enabled
+        self.records = []
+
+    def run(self, step, batch, is_prefill=False):
+        """``step()`` (one model call), timed when it is a decode step and timing is on."""
+        if is_prefill or not self.enabled:
+            return step()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        result = step()
+        end.record()
+        self.records.append((start, end, int(batch)))
+        return result
+
+    def intervals(self):
+        if self.records:
+            self.records[-1][1].synchronize()
+        return [{"milliseconds": a.elapsed_time(b), "batch": n} for a, b, n in self.records]
+
+    def clear(self):
+        self.records.clear()
+
+
 def graph_batch_sizes(max_num_seqs):
     """Decode graph buckets of the engine: 1, 2, 4, 8, then every 16 up to the maximum
     (engine/model_runner.py:250-251)."""

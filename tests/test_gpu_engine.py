@@ -18,8 +18,8 @@ if not torch.cuda.is_available():
     pytest.skip("needs an MI355X GPU", allow_module_level=True)
 
 from gpu_cases import assert_close_dense
-from paged_decode.engine_attention import (Attention, decode_metadata, graph_batch_sizes,
-                                           reset_context, set_context)
+from paged_decode.engine_attention import (Attention, DecodeTimings, decode_metadata,
+                                           graph_batch_sizes, reset_context, set_context)
 from paged_decode.integration import configure_model
 
 pytestmark = pytest.mark.gpu
@@ -170,3 +170,40 @@ def test_captured_decode_buckets_equal_eager_steps(backend):
             assert torch.equal(layer.v_cache.view(torch.int16), after[i][1].view(torch.int16))
             assert_close_dense(eager[i][:, 0], dense(layer, step_inputs[i][0], eng.tables, eng.lens))
         eng.grow()
+
+
+def test_decode_timings_of_eager_steps_and_graph_replays():
+    """DecodeTimings records one interval per decode step, eager or replayed, with its
+    batch; prefill steps and disabled timing record nothing."""
+    eng = Engine("hip_splitk")
+    timings = DecodeTimings()
+    timings.run(lambda: eng.prefill([300, 17]), 2, is_prefill=True)
+    eng.grow()
+    slots, lens, tables = decode_metadata(eng.tables, eng.lens)
+    set_context(False, slot_mapping=slots, context_lens=lens, block_tables=tables)
+    inputs = [eng.qkv(layer, len(eng.lens)) for layer in eng.layers]
+    step = lambda: [layer(*x).clone() for layer, x in zip(eng.layers, inputs)]
+    eager = timings.run(step, len(eng.lens))
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.current_stream().wait_stream(stream)
+    # Layers of one geometry share a borrowed output buffer: each output is copied out.
+    outs = [torch.empty_like(e) for e in eager]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for dst, layer, x in zip(outs, eng.layers, inputs):
+            dst.copy_(layer(*x))
+    for _ in range(3):
+        timings.run(graph.replay, len(eng.lens))
+    timings.enabled = False
+    timings.run(graph.replay, len(eng.lens))
+    reset_context()
+    got = timings.intervals()
+    assert [g["batch"] for g in got] == [2, 2, 2, 2]
+    assert all(g["milliseconds"] > 0 for g in got)
+    for a, b in zip(eager, outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    timings.clear()
+    assert timings.intervals() == []

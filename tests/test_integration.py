@@ -92,3 +92,13 @@ def test_flash_attn_decode_raises_on_this_platform():
     k = torch.zeros((1, 2, 64), dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError, match="custom decode_backend"):
         layer(q, k, k)
+
+
+def test_decode_timings_skip_prefill_and_disabled_steps():
+    """Prefill steps and steps with timing off run untimed (no CUDA events needed)."""
+    from paged_decode.engine_attention import DecodeTimings
+    timings = DecodeTimings(enabled=False)
+    assert timings.run(lambda: 7, 4) == 7
+    timings.enabled = True
+    assert timings.run(lambda: 8, 4, is_prefill=True) == 8
+    assert timings.records == [] and timings.intervals() == []
