@@ -40,9 +40,13 @@ def noalloc_call(g, spec, plan, out):
 
 CASES = [
     # (lengths, Hq, Hkv, D, capacity, explicit splits): the benchmark's D256 GQA shape
-    # with four sequences, then a smaller one (fewer rows, fewer splits, D 128).
+    # with four sequences, then a smaller one (fewer rows, fewer splits, D 128), then
+    # eight sequences whose plan (12 splits of 3 tiles, 384 workgroups) the partition
+    # walks two splits per workgroup, against pd_matched_decode's one launch, which
+    # runs one workgroup per split.
     ([2064, 0, 1000, 1], 16, 4, 256, 2112, 0),
     ([257, 0], 8, 2, 128, 600, 0),
+    ([2064, 0, 1000, 2064, 1, 2064, 1500, 192], 16, 4, 256, 2112, 0),
 ]
 
 
