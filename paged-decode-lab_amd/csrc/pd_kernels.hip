@@ -4,22 +4,27 @@
 // Kernels
 //   cols_loader        one 512-thread workgroup per (split, kv head, sequence)
 //                      (per (kv head, sequence) for the base and fixed-split
-//                      protocols, which walk the whole context): QK^T on MFMA
-//                      (v_mfma_f32_16x16x32_bf16), FP32 online softmax over
-//                      16384/D-row tiles walked last-to-first, P through LDS
-//                      and PV on MFMA split across the four compute
-//                      wavefronts by output columns, while four loader
+//                      protocols, which walk the whole context, and per run
+//                      of consecutive short splits for the matched walk):
+//                      QK^T on MFMA (v_mfma_f32_16x16x32_bf16), FP32 online
+//                      softmax over 16384/D-row tiles walked last-to-first, P
+//                      through LDS and PV on MFMA split across the four
+//                      compute wavefronts by output columns, while four loader
 //                      wavefronts copy the K and V rows of the next tiles into
-//                      LDS (buffer_load ... lds).  Three protocols: matched
+//                      LDS (buffer_load ... lds) and store completed
+//                      partitions of the walks.  Three protocols: matched
 //                      (bf16 p, normalized FP32 partial + LSE), base (FP32 p,
 //                      whole context, bf16 out) and fixed split (FP32 p,
-//                      (m, l, acc) per partition).  D = 64, 128 and 256.
+//                      (m, l, acc) per partition, optionally merged in the
+//                      kernel).  D = 64, 128 and 256.
 //   matched_tile       the matched protocol for splits of exactly one tile,
 //                      with PV split across the wavefronts by output columns.
 //   lse_merge          one wavefront per (sequence, query head, 64 columns):
 //                      stable log-sum-exp merge of the split partials, bf16 out.
 //   ml_merge           one wavefront per (sequence, query head, 64 columns):
-//                      merge of the (m, l, acc) states.
+//                      merge of the (m, l, acc) states in the reference's
+//                      order; ml_online_merge the same in the fixed-split
+//                      walk's order (running maximum).
 //
 // Every kernel reads the sequence length and block table on the device and
 // never needs host-side knowledge of tensor contents, so launches are
