@@ -12,6 +12,11 @@ padding, sometimes a custom softmax scale, and one backend:
   whatever grid paged_decode picks (the small-batch chunks at these batches).
 Every output passes the oracle's one-ulp gate and the dense 2e-2 gate; matched
 LSEs match the oracle's.  Outputs and workspaces start NaN-poisoned.
+
+A second sweep draws batches of 8-12 sequences with an explicit split count whose
+workgroups outnumber the CUs in splits of 2 to 5 tiles, so that the partition walks
+several splits per workgroup: outputs and LSEs must equal the single-launch path's
+(one workgroup per split) bit for bit, and pass the oracle's gate.
 """
 import numpy as np
 import pytest
@@ -108,3 +113,70 @@ def test_random_case(index):
     for b, n in enumerate(c["lengths"]):
         if n == 0:
             assert torch.count_nonzero(out[b]) == 0, where
+
+
+WALK_CASES = 16
+
+
+def draw_walk(index):
+    """A batch and an explicit split count whose (split, kv head, sequence) workgroups
+    outnumber the CUs, in splits of 2 to 5 tiles: the partition walks several splits per
+    workgroup."""
+    from paged_decode.splitkv_plan import make_splitkv_plan
+    rng = np.random.default_rng(9000 + index)
+    dim = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([4, 8]))
+    group = int(rng.choice([1, 2, 4]))
+    batch = int(rng.integers(8, 13))
+    tile = 16384 // dim
+    tiles = int(rng.integers(2, 6))
+    splits = -(-257 // (hkv * batch)) + int(rng.integers(0, 3))
+    capacity = max(tile, splits * tiles * tile - int(rng.integers(0, tile)))
+    spec = DecodeSpec(batch, group * hkv, hkv, dim, capacity)
+    # Page rounding of the capacity can add a tile per split: take the first split
+    # count (from the drawn one up) whose splits hold 2 to 5 tiles.
+    while True:
+        plan = make_splitkv_plan(spec, 256, num_splits=splits)
+        if 2 * tile <= plan.tokens_per_split <= 5 * tile:
+            break
+        splits += 1
+    lengths = rng.integers(0, capacity + 1, size=batch)
+    for b in range(batch):
+        if rng.random() < 0.4:
+            lengths[b] = min(int(rng.choice(BOUNDARIES + (capacity,))), capacity)
+    scale = float(rng.uniform(0.02, 0.2)) if rng.random() < 0.25 else None
+    return dict(dim=dim, hq=group * hkv, hkv=hkv, batch=batch, capacity=capacity,
+                lengths=[int(x) for x in lengths], splits=splits, scale=scale, seed=index)
+
+
+@pytest.mark.parametrize("index", range(WALK_CASES))
+def test_random_walk_case(index):
+    """The matched walk (several splits per workgroup) on seeded batches: bit for bit the
+    single-launch path's output (one workgroup per split), and within the oracle's gate."""
+    c = draw_walk(index)
+    where = f"walk case {index}: {c}"
+    q, k, v, table, lens = make_case(c["lengths"], c["hq"], c["hkv"], c["dim"], seed=c["seed"],
+                                     capacity=c["capacity"])
+    poison_tails(k, v, table, lens)
+    case = (q, k, v, table, lens)
+    g = to_gpu(case)
+    spec = DecodeSpec(c["batch"], c["hq"], c["hkv"], c["dim"], c["capacity"])
+    res = allocate_matched_resources(spec, "cuda", num_splits=c["splits"])
+    plan = res.plan
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert plan.splits * c["hkv"] * c["batch"] > cus, where
+    assert 2 * plan.tile_tokens <= plan.tokens_per_split <= 5 * plan.tile_tokens, where
+    poison_workspace(res)
+    out = matched_decode(*g, resources=res, scale=c["scale"]).clone()
+    fused = allocate_matched_resources(spec, "cuda", num_splits=c["splits"], fused=True)
+    poison_workspace(fused)
+    single = matched_decode(*g, resources=fused, scale=c["scale"])
+    torch.cuda.synchronize()
+    assert torch.equal(single.view(torch.int16), out.view(torch.int16)), where
+    assert torch.equal(fused.lse.view(torch.int32), res.lse.view(torch.int32)), where
+    expected, _, lse_ref, bound, _, counts = OM.matched_decode_with_bounds(
+        *case, plan.splits, plan.tokens_per_split, plan.tile_tokens, plan.lse_lanes, c["scale"],
+        counts=True)
+    np.testing.assert_allclose(to_np(res.lse), lse_ref, atol=2e-5, rtol=1e-6, err_msg=where)
+    assert_within_one_ulp(out, expected, where, bound, counts)
+    assert_close_dense(out, torch_dense(*g, scale=c["scale"]), where)
