@@ -423,6 +423,60 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
         }
       }
     };
+    // kSplit holds up to kHold completed partitions in the loaders' registers
+    // and stores them together, when the hold is full and after the walk's last
+    // tile: stored one at a time in the middle of the K / V stream, each
+    // partition cost about 2.5 us of the walk at D = 256.  The partitions of a
+    // hold are consecutive, hfirst, hfirst - 1, ... (the walk runs backwards).
+    constexpr int kHold = kMode != kSplit ? 1 : kFbPasses == 1 ? 16 : kFbPasses == 2 ? 8 : 4;
+    u32x4_t hx[kHold][kFbPasses];
+    float hm[kHold], hl[kHold];
+    int held = 0, hfirst = 0;
+    auto store_held = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < kHold; ++j) {
+        if (j < held) {
+#pragma unroll
+          for (int i = 0; i < kFbPasses; ++i) {
+            const int f = (i * 256 + w * 64 + lane) * 4;
+            const int h = f / D;
+            if (h < Gs) {
+              const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + hfirst - j;
+              *reinterpret_cast<u32x4_t*>(partials + orow * D + f % D) = hx[j][i];
+            }
+          }
+          if (w == 0 && lane < Gs) {
+            const int64_t orow = (int64_t(b) * Hq + qb + lane) * splits + hfirst - j;
+            maxima[orow] = hm[j];
+            lse_out[orow] = hl[j];
+          }
+        }
+      }
+      held = 0;
+    };
+    auto hold = [&](int part) __attribute__((always_inline)) {
+      if (held == kHold) store_held();
+      if (held == 0) hfirst = part;
+      const float den = (__uint_as_float(fl[0]) + __uint_as_float(fl[1])) +
+                        (__uint_as_float(fl[2]) + __uint_as_float(fl[3]));
+#pragma unroll
+      for (int j = 0; j < kHold; ++j) {
+        if (j == held) {
+#pragma unroll
+          for (int i = 0; i < kFbPasses; ++i) hx[j][i] = fx[i];
+          hm[j] = __uint_as_float(fmx);
+          hl[j] = den;
+        }
+      }
+      ++held;
+    };
+    auto complete = [&](int part) __attribute__((always_inline)) {
+      if constexpr (kMode == kSplit) {
+        hold(part);
+      } else {
+        flush_store(part);
+      }
+    };
     for (int ti = count - 1; ti >= 0; --ti) {
       lds_barrier();  // B1(ti)
       // The partition that ended with tile ti + 1 is in LDS since B1(ti).
@@ -436,11 +490,12 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       }
       lds_barrier();  // B2(ti)
       if (ti >= 2) issue(ti - 2, true);
-      if (flushed) flush_store(p + (ti + 1) / tpp);
+      if (flushed) complete(p + (ti + 1) / tpp);
       if (kFlush && ti == 0) {
         lds_barrier();  // the last partition's flush
         flush_read();
-        flush_store(p);
+        complete(p);
+        if constexpr (kMode == kSplit) store_held();
       }
     }
     if constexpr (!kFlush) lds_barrier();  // epilogue
