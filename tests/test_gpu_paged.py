@@ -284,8 +284,27 @@ def test_fixed_split_grids_and_partition_sizes(dim, hq, hkv, tiles_per_partition
     part = tiles_per_partition * tile
     cap = 4 * part + 3 * tile
     lengths = [0, 1, tile, part - 1, part, part + 1, 2 * part + tile // 2, cap]
-    q, k, v, table, lens = make_case(lengths, hq, hkv, dim, seed=tiles_per_partition,
-                                     capacity=cap)
+    check_fixed_split_grids(dim, hq, hkv, part, lengths, cap, tiles_per_partition,
+                            f"D{dim} {hq}/{hkv} {tiles_per_partition}-tile partitions")
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 2, 1), (64, 4, 1), (128, 8, 2), (128, 8, 1),
+                                         (128, 16, 1), (256, 8, 1), (256, 16, 1), (256, 40, 2)])
+def test_fixed_split_walk_of_more_partitions_than_a_hold(dim, hq, hkv):
+    """The walk holds up to 16, 8 or 4 completed partitions in the loaders' registers (by
+    the one, two or four 16-byte stores each loader lane makes per partition) and stores a
+    full hold before taking the next one; with one-tile partitions and up to 37 of them
+    per sequence, the holds fill and are stored two to nine times in one walk.  The same
+    checks as above."""
+    tile = 16384 // dim
+    cap = 37 * tile
+    lengths = [cap, cap - 1, 16 * tile + 1, 8 * tile, 4 * tile + 3, 1, 0, 33 * tile]
+    check_fixed_split_grids(dim, hq, hkv, tile, lengths, cap, 37,
+                            f"D{dim} {hq}/{hkv} 37 one-tile partitions")
+
+
+def check_fixed_split_grids(dim, hq, hkv, part, lengths, cap, seed, label):
+    q, k, v, table, lens = make_case(lengths, hq, hkv, dim, seed=seed, capacity=cap)
     poison_tails(k, v, table, lens)
     case = (q, k, v, table, lens)
     g = to_gpu(case)
@@ -307,16 +326,14 @@ def test_fixed_split_grids_and_partition_sizes(dim, hq, hkv, tiles_per_partition
         "pd_split_decode: the walk and one workgroup per partition differ"
     torch.cuda.synchronize()
     m_ref, l_ref, a_ref = OS.split_partitions(*case, parts, part_size=part)
-    assert_within_one_ulp(decoded[0], OS.ml_merge(m_ref, l_ref, a_ref),
-                          f"pd_split_decode D{dim} {hq}/{hkv} {tiles_per_partition}-tile partitions")
+    assert_within_one_ulp(decoded[0], OS.ml_merge(m_ref, l_ref, a_ref), f"pd_split_decode {label}")
     np.testing.assert_array_equal(np.isinf(to_np(maxima)), np.isinf(m_ref))
     live = np.isfinite(m_ref)
     np.testing.assert_allclose(to_np(maxima)[live], m_ref[live], rtol=1e-6, atol=1e-6)
     np.testing.assert_allclose(to_np(denoms), l_ref, rtol=3e-5, atol=1e-6)
     np.testing.assert_allclose(to_np(accums), a_ref, rtol=3e-5, atol=3e-5)
-    assert_within_one_ulp(out, OS.ml_merge(m_ref, l_ref, a_ref),
-                          f"D{dim} {hq}/{hkv} {tiles_per_partition}-tile partitions")
-    assert torch.count_nonzero(out[0]) == 0
+    assert_within_one_ulp(out, OS.ml_merge(m_ref, l_ref, a_ref), label)
+    assert torch.count_nonzero(out[lengths.index(0)]) == 0
 
 
 @pytest.mark.parametrize("grid", GRIDS)
