@@ -602,34 +602,58 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
             __builtin_bit_cast(bf16x8_t, kr[g * C::kCH + ch]), qf[ch], s[g], 0, 0, 0);
     }
     mfma_result_barrier(s);
-    if constexpr (!kMatchedArith) {
-      // Scores in the reference's units: dot(q, k) * SCALE (kernels.py:30).
-#pragma unroll
-      for (int g = 0; g < C::kNG; ++g)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s[g][r] *= scale;
-    }
+    // kv-head groups: row R = 16 g + 4 qg + r of a wavefront's rows holds kv
+    // head R % H, so query head qh (kv head e) scores live rows only at
+    // r = e + H i, i < kLive; every other score of the lane would be -inf
+    // (probability exactly 0) and is not formed.  x[g][i] is the lane's live
+    // score at r = e + H i (-inf past the end), in the reference's units;
+    // padding query lanes (qh >= H G) take the last head's rows.
+    constexpr int kLive = kHeads > 1 ? 4 / kHeads : 1;
+    const int e = kHeads > 1 ? min(qh / G, kHeads - 1) : 0;
+    float x[kHeads > 1 ? C::kNG : 1][kLive];
     if constexpr (kHeads > 1) {
-      // Rows of the other kv heads (R % H = r % H), and tokens past the end;
-      // padding query lanes (qh >= H G) take the last head's rows.
-      const int e = min(qh / G, kHeads - 1);
 #pragma unroll
-      for (int g = 0; g < C::kNG; ++g)
+      for (int g = 0; g < C::kNG; ++g) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (r % kHeads != e || (w * C::kTW + 16 * g + 4 * qg + r) / kHeads >= nvalid)
-            s[g][r] = -INFINITY;
-    } else if (nvalid < TILE) {
+        for (int i = 0; i < kLive; ++i) {
+          float v;
+          if constexpr (kHeads == 4) {
+            v = e == 0 ? s[g][0] : e == 1 ? s[g][1] : e == 2 ? s[g][2] : s[g][3];
+          } else {
+            v = e == 0 ? s[g][2 * i] : s[g][2 * i + 1];
+          }
+          // Scores in the reference's units: dot(q, k) * SCALE (kernels.py:30).
+          v *= scale;
+          const int tok = (w * C::kTW + 16 * g + 4 * qg + e + kHeads * i) / kHeads;
+          x[g][i] = tok >= nvalid ? -INFINITY : v;
+        }
+      }
+    } else {
+      if constexpr (!kMatchedArith) {
+        // Scores in the reference's units: dot(q, k) * SCALE (kernels.py:30).
 #pragma unroll
-      for (int g = 0; g < C::kNG; ++g)
+        for (int g = 0; g < C::kNG; ++g)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (w * C::kTW + 16 * g + 4 * qg + r >= nvalid) s[g][r] = -INFINITY;
+          for (int r = 0; r < 4; ++r) s[g][r] *= scale;
+      }
+      if (nvalid < TILE) {
+#pragma unroll
+        for (int g = 0; g < C::kNG; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (w * C::kTW + 16 * g + 4 * qg + r >= nvalid) s[g][r] = -INFINITY;
+      }
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < C::kNG; ++g)
-      mx = fmaxf(fmaxf(mx, fmaxf(s[g][0], s[g][1])), fmaxf(s[g][2], s[g][3]));
+    for (int g = 0; g < C::kNG; ++g) {
+      if constexpr (kHeads > 1) {
+#pragma unroll
+        for (int i = 0; i < kLive; ++i) mx = fmaxf(mx, x[g][i]);
+      } else {
+        mx = fmaxf(fmaxf(mx, fmaxf(s[g][0], s[g][1])), fmaxf(s[g][2], s[g][3]));
+      }
+    }
     mx = max_rows(mx);
     float (*wm)[16] = sm.wmax[ti & 1];
     if (lane < 16) wm[w][lane] = mx;
@@ -664,6 +688,38 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     float psum = 0.f;
 #pragma unroll
     for (int g = 0; g < C::kNG; ++g) {
+      if constexpr (kHeads > 1) {
+        // The live probabilities in row order, as three bf16 terms each, at
+        // positions r = e + H i of the lane's four rows (zero elsewhere).
+        const int pofs = qh * P::kPitch + (w * C::kTW + 16 * g + 4 * qg) * 2;
+        uint32_t t3[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
+#pragma unroll
+        for (int i = 0; i < kLive; ++i) {
+          const float pr = exp_fast(x[g][i] - mn);
+          psum += pr;
+          const uint32_t hi = pack_bf16(pr, 0.f);
+          const float r0 = pr - bf16_lo(hi);
+          const uint32_t mid = pack_bf16(r0, 0.f);
+          const uint32_t lo = pack_bf16(r0 - bf16_lo(mid), 0.f);
+          const uint32_t terms[3] = {lo, mid, hi};
+          const int pos = e + kHeads * i;  // 0..3
+#pragma unroll
+          for (int t = 0; t < 3; ++t) {
+            const uint32_t word = (pos & 1) ? terms[t] << 16 : terms[t];
+            if constexpr (kHeads == 4) {
+              t3[t][0] = pos < 2 ? word : 0u;
+              t3[t][1] = pos < 2 ? 0u : word;
+            } else {
+              t3[t][i] = word;
+            }
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+          *reinterpret_cast<u32x2_t*>(ps[t] + pofs) =
+              u32x2_t{qh < Gs ? t3[t][0] : 0u, qh < Gs ? t3[t][1] : 0u};
+        continue;
+      }
       float pr[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
