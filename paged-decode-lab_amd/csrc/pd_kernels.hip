@@ -288,10 +288,11 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   // wavefronts: the compute wavefronts leave its acc in `fb` (query head h at
   // fb[h * kFbPitch + c]), its maxima in `fm` and their denominator shares in
   // sm.lsum, and the loaders read them back and store them with 16-byte
-  // stores after issuing their next K copies.  A compute wavefront that
-  // stored them itself stood still for about 1-2 us per partition (its stores
-  // wait behind the loaders' copies), which every wavefront then waited for
-  // at the next barrier.
+  // stores after issuing their next K copies (kSplit holds them in registers
+  // and stores several together, below).  A compute wavefront that stored
+  // them itself stood still for about 1-2 us per partition (its stores wait
+  // behind the loaders' copies), which every wavefront then waited for at
+  // the next barrier.
   // kWalk: several partitions per workgroup, [p, p_end) (all of the
   // sequence's for kSplit, whose launch passes wf = splits).
   constexpr bool kWalk = kMode == kSplit || kMode == kMatchedWalk;
