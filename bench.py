@@ -624,7 +624,13 @@ def ab_variants_matched(torch, q, k, v, table, lens, spec, splits, part, lanes, 
             _native.partition(q, k, v, table, lens, partials, lse, spec.num_kv_heads, splits,
                               part, 16384 // spec.head_dim, scale, library=library)
             _native.lse_merge(partials, lse, out, lanes, library=library)
-        calls[name] = call
+
+        def decode():
+            # pd_matched_decode without counters: one launch for a plan of one split
+            _native.matched_decode(q, k, v, table, lens, partials, lse, None, out,
+                                   spec.num_kv_heads, splits, part, 16384 // spec.head_dim,
+                                   scale)
+        calls[name] = decode if name == "decode" else call
     return calls, {name: out for name in libraries}
 
 
@@ -648,7 +654,9 @@ def ab_report(torch, args):
       pages over a 200 GB pool) through --ab-backend;
     * shape: the matched decode of --ab-shape B,Hq,Hkv,D,ctx (B sequences of ctx tokens),
       planner plan.
-    Outside headline the variants are current (this build) or NAME=PATH.  Every variant
+    Outside headline the variants are current (this build) or NAME=PATH, and for shape and
+    partitions also decode (pd_matched_decode without counters, this build: the
+    partition alone for a plan of one split).  Every variant
     of a report uses the same workspace and output buffers (the placement of a workspace
     alone moves these times by a few percent), and each variant's output is copied right
     after its own call for the bit-for-bit comparison."""
@@ -698,9 +706,11 @@ def ab_report(torch, args):
                  f"{plan.splits}x{plan.tokens_per_split}")
     else:
         for item in items:
-            if "=" not in item and item != "current":
+            if "=" not in item and item not in ("current", "decode"):
                 raise SystemExit(f"unknown A/B variant {item!r} for workload {workload}: "
-                                 "current or NAME=PATH")
+                                 "current, decode (shape and partitions) or NAME=PATH")
+            if item == "decode" and workload not in ("shape", "partitions"):
+                raise SystemExit("the decode variant is for the shape and partitions workloads")
         libraries = {item.split("=", 1)[0]: libraries.get(item.split("=", 1)[0])
                      for item in items}
         unrolls, replays = (4, 16), 5

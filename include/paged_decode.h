@@ -39,7 +39,7 @@ enum pd_status { PD_OK = 0, PD_EINVAL = 1, PD_ELAUNCH = 2 };
 
 #define PD_PAGE_SIZE 256      /* spec.py:6 */
 #define PD_PARTITION_SIZE 1024 /* spec.py:7 */
-#define PD_ABI_VERSION 6
+#define PD_ABI_VERSION 7
 
 /* Split-KV plan; field meanings follow SplitKVPlan (splitkv_plan.py:15-23). */
 typedef struct pd_plan {
@@ -105,22 +105,28 @@ int pd_lse_merge(const float* partials, const float* lse, void* out,
 /* int32 counters per (sequence, kv head) in pd_matched_decode's `counters`. */
 #define PD_FUSED_COUNTERS_PER_GROUP 128
 
-/* Matched split-KV decode in one launch: the partition of pd_partition plus
- * the LSE merge of pd_lse_merge (bit-identical to pd_partition followed by
- * pd_lse_merge).  Replaces the two launches of matched_decode
- * (matched_splitkv.py:142-149).  With splits of one tile (tokens_per_split ==
- * tile_tokens) the merge of each GQA group is shared by the last wavefront to
- * finish each quarter of the head_dim columns; otherwise the last workgroup of
- * each (sequence, kv head) merges the whole group.  `counters` is int32
- * [batch * num_kv_heads * PD_FUSED_COUNTERS_PER_GROUP] (four counters per
- * group, each on a 128-byte line), all zero before the first call; every completed
- * call leaves it all zero again, so the launch can be replayed from a graph
- * without a reset.  Calls that share `counters` must not run concurrently.
+/* Matched split-KV decode: the partition of pd_partition plus the LSE merge of
+ * pd_lse_merge, bit-identical to pd_partition followed by pd_lse_merge.
+ * Replaces the two launches of matched_decode (matched_splitkv.py:142-149).
  * Writes partials, lse and out bf16 [batch, num_heads, head_dim].  The merge
  * sums with the plan's lse_lanes, min(next_pow2(splits), 32 if
  * head_dim % 128 == 0 else 16).
- * The partials are published with device-scope stores and read with
- * device-scope loads, so the merge may run on any XCD. */
+ * With `counters` (non-NULL) it is one fused launch.  With splits of one tile
+ * (tokens_per_split == tile_tokens) the merge of each GQA group is shared by
+ * the last wavefront to finish each quarter of the head_dim columns;
+ * otherwise the last workgroup of each (sequence, kv head) merges the whole
+ * group.  `counters` is int32 [batch * num_kv_heads *
+ * PD_FUSED_COUNTERS_PER_GROUP] (four counters per group, each on a 128-byte
+ * line), all zero before the first call; every completed call leaves it all
+ * zero again, so the launch can be replayed from a graph without a reset.
+ * Calls that share `counters` must not run concurrently.  The partials are
+ * published with device-scope stores and read with device-scope loads, so the
+ * merge may run on any XCD.
+ * With counters NULL it runs the partition and the merge as two launches,
+ * except for a plan of one split of more than one tile (splits == 1,
+ * tokens_per_split > tile_tokens): the merge of one split weighs it by exactly
+ * 1, so the partition writes out = bf16(partial) itself (-0 as +0, 0 for an
+ * empty sequence) and nothing else is launched. */
 int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                       const void* k, const void* v,
                       const int32_t* table, int64_t table_stride_b, int32_t table_width,

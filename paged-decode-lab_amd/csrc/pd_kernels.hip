@@ -511,8 +511,9 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     for (int pp = p; pp < p_end; ++pp)
       write_empty_partition<D, kEmptyMode>(tid, b, Hq, qb, Gs, splits, pp, partials, lse_out,
                                            out, maxima);
-    // The walk's merged output of an empty sequence is 0 (no live partition).
-    if (kMode == kSplit && out != nullptr)
+    // The walk's merged output of an empty sequence is 0 (no live partition),
+    // and so is the directly written output of a one-split matched plan.
+    if ((kMode == kSplit || kMode == kMatched) && out != nullptr)
       write_empty_partition<D, kBase>(tid, b, Hq, qb, Gs, splits, 0, partials, lse_out, out,
                                       maxima);
     return;
@@ -861,6 +862,17 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 #pragma unroll
         for (int j = 0; j < P::kNBW; ++j) partials[orow * D + col + 16 * j] = acc[j][r] * inv;
         if (w == 0 && qh == 0) lse_out[orow] = lv;
+        if (out != nullptr) {
+          // A plan of one split (out is passed only then): its LSE merge
+          // (matched_splitkv.py:101-127) weighs the split by
+          // exp(lse - (ln(exp(lse - lse)) + lse)) = exp2(0) = 1 exactly, so
+          // it writes bf16(fma(1, partial, +0)), which is bf16(partial + 0)
+          // (-0 becomes +0); an empty split (lse -inf) weighs 0 and gives 0.
+          uint16_t* dst = out + (int64_t(b) * Hq + qb + h) * D + col;
+#pragma unroll
+          for (int j = 0; j < P::kNBW; ++j)
+            dst[16 * j] = uint16_t(bf16_bits(den > 0.f ? acc[j][r] * inv + 0.f : 0.f));
+        }
       }
     }
   }
@@ -1559,6 +1571,12 @@ int padded_group(int g) {
 
 // Validation and dispatch shared by pd_partition (fused = false) and
 // pd_matched_decode (fused = true).
+// A matched plan of one split longer than a tile: the partition kernel
+// (cols_loader_kernel) writes the output itself and no merge runs.
+bool one_split_direct(int32_t splits, int32_t tokens_per_split, int32_t tile_tokens) {
+  return splits == 1 && tokens_per_split != tile_tokens;
+}
+
 int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, int64_t qsh,
                     const void* k, const void* v, const int32_t* table, int64_t tsb,
                     int32_t width, const int32_t* lengths, float* partials, float* lse,
@@ -1589,6 +1607,9 @@ int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, in
     return pd::fail(PD_EINVAL, "grid dimension exceeds device limits");
   if (tsb < 0 || tsb >= (int64_t(1) << 31))
     return pd::fail(PD_EINVAL, "block table row stride must be in [0, 2^31)");
+  // Without the fused merge, `out` is written only by a plan of one split of
+  // more than one tile (its merge is the identity, one_split_direct).
+  if (!fused && !one_split_direct(splits, tokens_per_split, tile_tokens)) out = nullptr;
   PartitionArgs a{static_cast<const uint16_t*>(q), int(qsb), int(qsh),
                   static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), table,
                   int(tsb), width, lengths, partials, lse,
@@ -1663,6 +1684,12 @@ extern "C" int pd_partition(const void* q, int64_t q_stride_b, int64_t q_stride_
                          tile_tokens, scale, stream);
 }
 
+namespace {
+int merge_entry(const char* what, const float* partials, const float* lse, void* out,
+                int32_t batch, int32_t num_heads, int32_t head_dim, int32_t splits,
+                int32_t lse_lanes, pd_stream_t stream);
+}  // namespace
+
 extern "C" int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                  const void* k, const void* v, const int32_t* table,
                                  int64_t table_stride_b, int32_t table_width,
@@ -1671,11 +1698,23 @@ extern "C" int pd_matched_decode(const void* q, int64_t q_stride_b, int64_t q_st
                                  int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                  int32_t head_dim, int32_t splits, int32_t tokens_per_split,
                                  int32_t tile_tokens, double scale, pd_stream_t stream) {
-  return partition_entry("pd_matched_decode", true, q, q_stride_b, q_stride_h, k, v, table,
-                         table_stride_b, table_width, lengths, partials, lse, counters, out,
-                         batch,
-                         num_heads, num_kv_heads, head_dim, splits, tokens_per_split,
-                         tile_tokens, scale, stream);
+  if (counters != nullptr)
+    return partition_entry("pd_matched_decode", true, q, q_stride_b, q_stride_h, k, v, table,
+                           table_stride_b, table_width, lengths, partials, lse, counters, out,
+                           batch, num_heads, num_kv_heads, head_dim, splits, tokens_per_split,
+                           tile_tokens, scale, stream);
+  // Without counters: the partition and the LSE merge as two launches, or the
+  // partition alone, writing the output, for a plan of one split.
+  pd::clear_error();
+  if (!out) return pd::fail(PD_EINVAL, "invalid matched workspace");
+  if (int st = partition_entry("pd_matched_decode", false, q, q_stride_b, q_stride_h, k, v,
+                               table, table_stride_b, table_width, lengths, partials, lse,
+                               nullptr, out, batch, num_heads, num_kv_heads, head_dim, splits,
+                               tokens_per_split, tile_tokens, scale, stream))
+    return st;
+  if (one_split_direct(splits, tokens_per_split, tile_tokens)) return PD_OK;
+  return merge_entry("pd_matched_decode", partials, lse, out, batch, num_heads, head_dim,
+                     splits, plan_lse_lanes(splits, head_dim), stream);
 }
 
 namespace {
@@ -1804,9 +1843,10 @@ extern "C" int pd_matched_decode_noalloc(const void* q, int64_t q_stride_b, int6
   auto* lse = reinterpret_cast<float*>(base + lse_offset);
   if (int st = partition_entry("pd_matched_decode_noalloc", false, q, q_stride_b, q_stride_h, k,
                                v, table, table_stride_b, table_width, lengths, partials, lse,
-                               nullptr, nullptr, batch, num_heads, num_kv_heads, head_dim,
+                               nullptr, out, batch, num_heads, num_kv_heads, head_dim,
                                splits, tokens_per_split, tile_tokens, scale, stream))
     return st;
+  if (one_split_direct(splits, tokens_per_split, tile_tokens)) return PD_OK;
   return merge_entry("pd_matched_decode_noalloc", partials, lse, out, batch, num_heads,
                      head_dim, splits, plan_lse_lanes(splits, head_dim), stream);
 }

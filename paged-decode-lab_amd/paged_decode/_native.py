@@ -125,13 +125,16 @@ def partition(q, k, v, tables, lengths, partials, lse, num_kv_heads, splits, tok
 
 def matched_decode(q, k, v, tables, lengths, partials, lse, counters, out, num_kv_heads, splits,
                    tokens_per_split, tile_tokens, scale, library=None):
+    """pd_matched_decode: the fused launch with ``counters``; without (None) the partition
+    and the LSE merge, or the partition alone for a plan of one multi-tile split."""
     b, h, d = q.shape
     L = library or lib()
     check(L.pd_matched_decode(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
                               v.data_ptr(), tables.data_ptr(), tables.stride(0),
                               tables.shape[1], lengths.data_ptr(), partials.data_ptr(),
                               lse.data_ptr(),
-                              counters.data_ptr(), out.data_ptr(), b, h, num_kv_heads, d,
+                              None if counters is None else counters.data_ptr(),
+                              out.data_ptr(), b, h, num_kv_heads, d,
                               splits, tokens_per_split, tile_tokens, scale,
                               stream_handle(q.device)), L)
 

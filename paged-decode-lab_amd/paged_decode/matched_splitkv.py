@@ -83,13 +83,10 @@ def matched_decode(q, k, v, tables, lengths, *, resources, scale=None):
     _validate(q, k, v, tables, lengths, resources, "hip_base", scale)
     _check_matched(q, tables, resources, scale)
     spec, plan = resources.spec, resources.plan
-    if resources.counters is not None:
-        _native.matched_decode(q, k, v, tables, lengths, resources.partials, resources.lse,
-                               resources.counters, resources.out, spec.num_kv_heads, plan.splits,
-                               plan.tokens_per_split, plan.tile_tokens, scale)
-        return resources.out
-    _native.partition(q, k, v, tables, lengths, resources.partials, resources.lse,
-                      spec.num_kv_heads, plan.splits, plan.tokens_per_split, plan.tile_tokens,
-                      scale)
-    _native.lse_merge(resources.partials, resources.lse, resources.out, plan.lse_lanes)
+    # With counters the fused launch; without, the partition then the LSE merge
+    # (matched_splitkv.py:147-149), or the partition alone for a plan of one split of
+    # several tiles, whose merge is the identity (the same bits).
+    _native.matched_decode(q, k, v, tables, lengths, resources.partials, resources.lse,
+                           resources.counters, resources.out, spec.num_kv_heads, plan.splits,
+                           plan.tokens_per_split, plan.tile_tokens, scale)
     return resources.out

@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert names == sorted(_native.SIGNATURES), names
     for name in names:
         assert getattr(lib, name) is not None
-    assert lib.pd_abi_version() == 6
+    assert lib.pd_abi_version() == 7
 
 
 def test_error_reporting_and_validation_without_launching():

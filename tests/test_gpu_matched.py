@@ -63,6 +63,41 @@ def test_d256_gqa_single_sequence(ctx, cap):
           f"{frac:.2e} of outputs one ulp off")
 
 
+@pytest.mark.parametrize("lengths,hq,hkv,dim,cap", [
+    ([2064, 0, 1000, 1, 64, 65], 16, 4, 256, 2112),
+    ([4096, 0, 300, 2049], 32, 8, 128, 4096),
+    ([1000, 0, 1, 257, 256], 16, 16, 64, 1024),
+    ([700, 0, 33], 8, 1, 128, 768),
+])
+def test_one_split_plan_writes_its_output_in_the_partition(lengths, hq, hkv, dim, cap):
+    """A plan of one split of several tiles needs no merge launch: the LSE merge weighs
+    that split by exactly 1, so matched_decode (pd_matched_decode without counters) lets
+    the partition write bf16(partial) itself.  Output, partials and LSEs must equal
+    pd_partition + pd_lse_merge's bit for bit (NaN-poisoned buffers; zero-length rows
+    exactly 0), and the output the oracle's at one ulp."""
+    case = make_case(lengths, hq, hkv, dim, seed=len(lengths) + dim, capacity=cap)
+    poison_tails(*case[1:])
+    spec = DecodeSpec(len(lengths), hq, hkv, dim, cap)
+    g, res, out = run(case, spec, num_splits=1)
+    plan = res.plan
+    assert plan.splits == 1 and plan.tokens_per_split > plan.tile_tokens
+    partials = torch.full_like(res.partials, float("nan"))
+    lse = torch.full_like(res.lse, float("nan"))
+    two = torch.full_like(out, float("nan"))
+    _native.partition(*g, partials, lse, hkv, 1, plan.tokens_per_split, plan.tile_tokens,
+                      dim ** -0.5)
+    _native.lse_merge(partials, lse, two, plan.lse_lanes)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), two.view(torch.int16)), \
+        "one-split output differs from pd_partition + pd_lse_merge"
+    assert torch.equal(res.partials.view(torch.int32), partials.view(torch.int32))
+    assert torch.equal(res.lse.view(torch.int32), lse.view(torch.int32))
+    for i, n in enumerate(lengths):
+        if n == 0:
+            assert torch.count_nonzero(out[i].view(torch.int16)) == 0
+    check_all(case, g, res, out, where=f"one split D{dim} {hq}/{hkv}")
+
+
 def test_d256_fixed_1024_token_partitions():
     """Same kernels with 1024-token partitions (the fixed-partition geometry)."""
     case = make_case([2064], 16, 4, 256, seed=20261105, capacity=2112)

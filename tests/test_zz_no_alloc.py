@@ -43,10 +43,13 @@ CASES = [
     # with four sequences, then a smaller one (fewer rows, fewer splits, D 128), then
     # eight sequences whose plan (12 splits of 3 tiles, 384 workgroups) the partition
     # walks two splits per workgroup, against pd_matched_decode's one launch, which
-    # runs one workgroup per split.
+    # runs one workgroup per split; last, one split of 33 tiles, whose output the
+    # allocation-free partition writes itself.
     ([2064, 0, 1000, 1], 16, 4, 256, 2112, 0),
     ([257, 0], 8, 2, 128, 600, 0),
     ([2064, 0, 1000, 2064, 1, 2064, 1500, 192], 16, 4, 256, 2112, 0),
+    # a plan of one split of 33 tiles: the partition writes the output, no merge runs
+    ([2064, 0, 700], 16, 4, 256, 2112, 1),
 ]
 
 
