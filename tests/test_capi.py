@@ -125,3 +125,14 @@ def test_noalloc_rejects_workspaces_past_its_static_scratch():
     status = lib.pd_matched_decode_noalloc(null, 0, 0, null, null, null, 0, 128, null, null,
                                            64, 32, 8, 256, 32, 1024, 64, 0.0625, null)
     assert status == _native.PD_EINVAL and b"static scratch" in lib.pd_last_error()
+
+
+def test_matched_decode_without_counters_needs_an_output():
+    # Without counters pd_matched_decode runs the partition and the merge (or, for a plan
+    # of one split, the partition alone writing the output): a NULL output is refused
+    # before any device call.
+    lib = _native.lib()
+    null = ctypes.c_void_p(0)
+    status = lib.pd_matched_decode(null, 0, 0, null, null, null, 0, 9, null, null, null, null,
+                                   null, 1, 16, 4, 256, 1, 2304, 64, 0.0625, null)
+    assert status == _native.PD_EINVAL and b"invalid matched workspace" in lib.pd_last_error()
