@@ -883,8 +883,10 @@ def main():
     torch.cuda.synchronize()
     us = graph_time_us(torch, case["full"], args.steps)
     fused_us = graph_time_us(torch, case["fused"], args.steps)
-    part_us = graph_time_us(torch, case["partition"], args.steps)
-    merge_us = graph_time_us(torch, case["merge"], args.steps)
+    # The partition and merge alone (the roofline's launch duration): median of five
+    # timings, as the reference protocol takes, so that one slow replay does not set it.
+    part_us = sorted(graph_time_us(torch, case["partition"], args.steps) for _ in range(5))[2]
+    merge_us = sorted(graph_time_us(torch, case["merge"], args.steps) for _ in range(5))[2]
     progress(f"headline: {us:.3f} us/call, partition {part_us:.3f}, merge {merge_us:.3f}, "
              f"fused {fused_us:.3f}")
     nbytes = algorithmic_bytes([ctx], 1, 16, 4, 256)
