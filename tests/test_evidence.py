@@ -63,3 +63,16 @@ def test_bench_ab_refuses_unknown_variants_before_any_gpu_work():
                          timeout=300, cwd=root)
     assert res.returncode != 0
     assert "unknown A/B variant 'bogus'" in res.stderr
+
+
+def test_bench_ab_decode_variant_belongs_to_the_matched_workloads():
+    """The decode variant (pd_matched_decode without counters) is a matched-decode call:
+    a paged-backend workload refuses it before any GPU work."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--ab", "decode",
+                          "--ab-workload", "edge_d64"], capture_output=True, text=True,
+                         timeout=300, cwd=root)
+    assert res.returncode != 0
+    assert "decode variant is for the shape and partitions workloads" in res.stderr
