@@ -1602,14 +1602,15 @@ int padded_group(int g) {
   return gp;
 }
 
-// Validation and dispatch shared by pd_partition (fused = false) and
-// pd_matched_decode (fused = true).
 // A matched plan of one split longer than a tile: the partition kernel
 // (cols_loader_kernel) writes the output itself and no merge runs.
 bool one_split_direct(int32_t splits, int32_t tokens_per_split, int32_t tile_tokens) {
   return splits == 1 && tokens_per_split != tile_tokens;
 }
 
+// Validation and dispatch shared by pd_partition (fused = false) and
+// pd_matched_decode (fused = true, or fused = false with an output for a plan
+// of one split).
 int partition_entry(const char* what, bool fused, const void* q, int64_t qsb, int64_t qsh,
                     const void* k, const void* v, const int32_t* table, int64_t tsb,
                     int32_t width, const int32_t* lengths, float* partials, float* lse,
