@@ -584,6 +584,15 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 #pragma unroll
   for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
   float m_own = -INFINITY;  // running max of head qh
+  // The lane's kv head in a group of kHeads (e), as bit masks for the score
+  // select, and the scale in a register of its own (a kernel argument the
+  // compiler would otherwise fetch again in every tile).
+  const int e = kHeads > 1 ? min(qh / G, kHeads - 1) : 0;
+  uint32_t emask[kHeads > 1 ? kHeads : 1];
+#pragma unroll
+  for (int r = 0; r < (kHeads > 1 ? kHeads : 1); ++r) emask[r] = r == e ? 0xffffffffu : 0u;
+  float scale_v = scale;
+  asm volatile("" : "+v"(scale_v));
   float l_own = 0.f;        // this lane's share of head qh's denominator
   // The walk with an output (out != nullptr) also merges the partitions as it
   // completes them, with ml_online_merge_kernel's arithmetic (ml_step): running
@@ -642,21 +651,20 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     // score at r = e + H i (-inf past the end), in the reference's units;
     // padding query lanes (qh >= H G) take the last head's rows.
     constexpr int kLive = kHeads > 1 ? 4 / kHeads : 1;
-    const int e = kHeads > 1 ? min(qh / G, kHeads - 1) : 0;
     float x[kHeads > 1 ? C::kNG : 1][kLive];
     if constexpr (kHeads > 1) {
 #pragma unroll
       for (int g = 0; g < C::kNG; ++g) {
 #pragma unroll
         for (int i = 0; i < kLive; ++i) {
-          float v;
-          if constexpr (kHeads == 4) {
-            v = e == 0 ? s[g][0] : e == 1 ? s[g][1] : e == 2 ? s[g][2] : s[g][3];
-          } else {
-            v = e == 0 ? s[g][2 * i] : s[g][2 * i + 1];
-          }
+          // s[g][e + H i] by bit masks (a select on the lane's e became branches)
+          uint32_t vb = 0;
+#pragma unroll
+          for (int r = i * kHeads; r < i * kHeads + kHeads; ++r)
+            vb |= __float_as_uint(s[g][r]) & emask[r - i * kHeads];
+          float v = __uint_as_float(vb);
           // Scores in the reference's units: dot(q, k) * SCALE (kernels.py:30).
-          v *= scale;
+          v *= scale_v;
           const int tok = (w * C::kTW + 16 * g + 4 * qg + e + kHeads * i) / kHeads;
           x[g][i] = tok >= nvalid ? -INFINITY : v;
         }
@@ -667,7 +675,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
 #pragma unroll
         for (int g = 0; g < C::kNG; ++g)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) s[g][r] *= scale;
+          for (int r = 0; r < 4; ++r) s[g][r] *= scale_v;
       }
       if (nvalid < TILE) {
 #pragma unroll
