@@ -108,7 +108,14 @@ def validate_metadata(table, lengths, num_pages, max_context_len):
                                      num_pages, max_context_len))
 
 
+# torch's raw lookup of the current stream returns the handle without building a Stream
+# object (a few microseconds of host time per launch); current_stream is the fallback.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device):
+    if _raw_stream is not None and device.index is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -66,13 +66,13 @@ def _check_matched(q, tables, resources, scale):
     shape = (spec.max_batch, spec.num_heads, plan.splits)
     for tensor, geometry in ((resources.lse, shape),
                              (resources.partials, (*shape, spec.head_dim))):
-        if (tensor.shape != geometry or tensor.device != q.device
+        if (tensor.shape != geometry or tensor.get_device() != q.get_device()
                 or tensor.dtype != torch.float32 or not tensor.is_contiguous()):
             raise ValueError("invalid matched workspace")
     counters = resources.counters
     if counters is not None and (
             counters.shape != (spec.max_batch * spec.num_kv_heads * COUNTERS_PER_GROUP,)
-            or counters.device != q.device
+            or counters.get_device() != q.get_device()
             or counters.dtype != torch.int32 or not counters.is_contiguous()):
         raise ValueError("invalid matched workspace")
 

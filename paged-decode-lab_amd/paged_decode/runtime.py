@@ -48,6 +48,8 @@ class Resources:
     chunk_accums: torch.Tensor | None = None
     sm_count: int = 0
     _chunk_plans: dict = field(default_factory=dict, repr=False, compare=False)
+    # Shaped views of the chunk workspace by (batch, chunks), made once per shape.
+    _chunk_views: dict = field(default_factory=dict, repr=False, compare=False)
 
 
 def _device_cus(device):
@@ -140,8 +142,10 @@ def _validate(q, k, v, tables, lengths, resources, backend, scale):
     if backend not in ("hip_base", "hip_splitk"):
         raise ValueError("unknown custom backend")
     spec = resources.spec
-    tensors = (q, k, v, tables, lengths, resources.out)
-    if not all(t.is_cuda and t.device == q.device for t in tensors):
+    # get_device() is the CUDA index, -1 on the CPU (no torch.device objects built).
+    device = q.get_device()
+    if device < 0 or not (k.get_device() == v.get_device() == tables.get_device()
+                          == lengths.get_device() == resources.out.get_device() == device):
         raise ValueError("all tensors must be on the same CUDA device")
     if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("custom decode supports BF16 Q/K/V only")
@@ -176,7 +180,7 @@ def _validate(q, k, v, tables, lengths, resources, backend, scale):
         shape = (spec.max_batch, spec.num_heads, spec.partitions)
         for tensor, expected in ((resources.maxima, shape), (resources.denoms, shape),
                                  (resources.accums, (*shape, spec.head_dim))):
-            if (tensor is None or tensor.shape != expected or tensor.device != q.device
+            if (tensor is None or tensor.shape != expected or tensor.get_device() != device
                     or tensor.dtype != torch.float32 or not tensor.is_contiguous()):
                 raise ValueError("invalid or missing preallocated split-K workspace")
 
@@ -199,11 +203,15 @@ def paged_decode(q, k, v, tables, lengths, *, resources, backend="hip_base", sca
     chunked = _chunk_plan(resources, b, tables.shape[1])
     if chunked is not None:
         chunks, tokens = chunked
-        rows = b * spec.num_heads * chunks
-        shape = (b, spec.num_heads, chunks)
-        maxima = resources.chunk_maxima[:rows].view(shape)
-        denoms = resources.chunk_denoms[:rows].view(shape)
-        accums = resources.chunk_accums[:rows * spec.head_dim].view(*shape, spec.head_dim)
+        views = resources._chunk_views.get((b, chunks))
+        if views is None:
+            rows = b * spec.num_heads * chunks
+            shape = (b, spec.num_heads, chunks)
+            views = (resources.chunk_maxima[:rows].view(shape),
+                     resources.chunk_denoms[:rows].view(shape),
+                     resources.chunk_accums[:rows * spec.head_dim].view(*shape, spec.head_dim))
+            resources._chunk_views[(b, chunks)] = views
+        maxima, denoms, accums = views
         _native.split_fixed(q, k, v, tables, lengths, maxima, denoms, accums, spec.num_kv_heads,
                             chunks, tokens, scale)
         _native.ml_merge(maxima, denoms, accums, resources.out, b)
