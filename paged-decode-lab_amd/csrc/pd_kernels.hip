@@ -884,6 +884,12 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       }
     }
   }
+  // No K read is in flight here (tile 0 issues none), but the compiler does
+  // not know that the inline-asm reads are asynchronous: its control-flow graph
+  // has an exit edge right after read_k, where it would reuse their registers
+  // with no wait.  This wait (free: nothing is outstanding) makes every path
+  // to such a reuse pass a wait for the reads.
+  lds_wait(kr);
 
   if constexpr (kWalk) {
     // Partitions past the sequence's last token are empty.
