@@ -541,10 +541,19 @@ struct Matched {
 // between the two halves by their own address (bit 0), so the swizzle spreads
 // the rows of one half over its 4 pairs of pieces.  (A swizzle by r mod 4
 // alone left a 2-way conflict on every read.)
-template <int D>
+//
+// kRows (D = 64 only): the reads of P V by rows (each compute wavefront
+// multiplying its own rows by all 64 columns) take rows 4c .. 4c + 3 of a
+// 16-row group in lanes 16c .. 16c + 15 of each 32-lane half, so rows 0-7 of
+// a group share a clock instead of rows 0-3 and 8-11: bit 2 of the row picks
+// the pair instead of bit 3.
+template <int D, bool kRows = false>
 __device__ __forceinline__ int vswz(int row) {
+  static_assert(!kRows || D == 64, "row-wise P V swizzle at D = 64 only");
   if constexpr (D >= 128)
     return 2 * (row & 3) + 8 * ((row >> 3) & 1);
+  else if constexpr (kRows)
+    return 2 * (((row >> 1) & 1) | (((row >> 2) & 1) << 1));
   else
     return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1));
 }
@@ -559,21 +568,21 @@ __device__ __forceinline__ int tile_row_elems(int R, int RS) {
 
 // Source byte offset (tile-relative) of the 16 bytes that DMA copy i of
 // wavefront w places at LDS position 16 * (64 i + lane) of its rows.
-template <int D, int GP, int H = 1>
+template <int D, int GP, int H = 1, bool kRows = false>
 __device__ __forceinline__ int v_copy_offset(int i, int lane, int w, int RS) {
   using C = Matched<D, GP>;
   const int slot = 64 * i + lane;
   const int row = slot / C::kPieces, pos = slot % C::kPieces;
-  return (tile_row_elems<D, H>(w * C::kTW + row, RS) + 8 * (pos ^ vswz<D>(row))) * 2;
+  return (tile_row_elems<D, H>(w * C::kTW + row, RS) + 8 * (pos ^ vswz<D, kRows>(row))) * 2;
 }
 
 // Byte offset within a V row of this lane's 8 bytes of a transposed read of
 // the 16 columns from col0 (a multiple of 16): lane l % 4 = b reads columns
 // col0 + 4b .. +3 of a row whose index within its 16-row group is `row`.
-template <int D>
+template <int D, bool kRows = false>
 __device__ __forceinline__ int v_read_offset(int col0, int lane, int row) {
   const int b = lane & 3;
-  return 16 * (((col0 >> 3) + (b >> 1)) ^ vswz<D>(row)) + 8 * (b & 1);
+  return 16 * (((col0 >> 3) + (b >> 1)) ^ vswz<D, kRows>(row)) + 8 * (b & 1);
 }
 
 // K rows staged in LDS by loader wavefronts (cols_loader_kernel): row r of a

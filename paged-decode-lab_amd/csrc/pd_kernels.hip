@@ -155,9 +155,9 @@ __device__ __forceinline__ void for_each_step(F&& f, std::integer_sequence<int, 
 // padding query heads (qh >= Gs) are neither written (by the caller) nor read:
 // their lanes take zeros, which frees LDS bandwidth for the three bf16 terms
 // at D = 256 (paired A/B on the edge-coverage batches at D 256 GQA 8:1: 1.8%
-// and 2.2% faster); at D 64 and 128 the eight and four k-steps' masked reads
-// cost more than they save, and for the matched protocol's one term they
-// changed nothing (+0.1 to +0.4%).
+// and 2.2% faster); at D 128 (and at D 64, before P V by rows there) the
+// four and eight k-steps' masked reads cost more than they save, and for the
+// matched protocol's one term they changed nothing (+0.1 to +0.4%).
 template <int D, int kTerms>
 inline constexpr bool kSkipPadRows = D == 256 && kTerms == 3;
 
@@ -172,22 +172,8 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<D>::kNBW],
   // slot: wavefront part u / kTW, row u % kTW (u + 4 stays in the same part).
   const int u = 8 * qg + (qh >> 2);
   const uint32_t vb = lds_address(slot) + (u / C::kTW) * C::kSlot + (u % C::kTW) * C::kPitch;
-  // kChains (D = 64, one 16-column block per wavefront): the tile's products
-  // go to six independent accumulators (bf16 term t and k-step parity e at
-  // (2t + e) kNBW + j) and are added to acc after the tile as
-  // acc + ((hi + mid) + lo), instead of one chain of 24 dependent MFMAs
-  // (paired A/B on the edge-coverage batches at D 64: 1.4% faster for both
-  // backends; at D 128, with two blocks, it changed nothing).  The sums read
-  // the MFMA results only after mfma_result_barrier: without it this compiler
-  // let them read the first register of a result before its MFMA had written
-  // it on one path (one-tile sequences of the kv-head pairs).
-  constexpr bool kChains = kTerms == 3 && P::kNBW == 1;
-  constexpr int kCh = kChains ? 6 * P::kNBW : 1;
-  floatx4_t ch[kCh];
-  if constexpr (kChains) {
-#pragma unroll
-    for (int i = 0; i < kCh; ++i) ch[i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-  }
+  // D = 64 with three terms multiplies by rows instead (pv_tile_rows).
+  static_assert(!(D == 64 && kTerms == 3), "pv_tile_rows");
   auto pv_step = [&](auto KS) __attribute__((always_inline)) {
     constexpr int ks = decltype(KS)::value;
     bf16x8_t a[kTerms];
@@ -239,30 +225,72 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<D>::kNBW],
           bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo[j])[0], __builtin_bit_cast(u32x2_t, lo[j])[1],
                             __builtin_bit_cast(u32x2_t, hi[j])[0], __builtin_bit_cast(u32x2_t, hi[j])[1]});
 #pragma unroll
-      for (int t = 0; t < kTerms; ++t) {
-        if constexpr (kChains) {
-          const int base = t * 2 * P::kNBW + (ks & 1) * P::kNBW;
-          ch[base + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], bv, ch[base + j], 0, 0, 0);
-        } else {
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], bv, acc[j], 0, 0, 0);
-        }
-      }
+      for (int t = 0; t < kTerms; ++t)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], bv, acc[j], 0, 0, 0);
     }
   };
   for_each_step(pv_step, std::make_integer_sequence<int, P::kKS>{});
-  if constexpr (kChains) {
-    mfma_result_barrier(ch);
+}
+
+// P V by rows (D = 64, three bf16 terms): compute wavefront w multiplies the
+// probabilities of its own 64 tile rows, still in registers, by all 64 V
+// columns, into acc[j] = O_w[head 4qg + r][16j + qh]; the four wavefronts'
+// O_w are summed at the partition's end.  pa[s][t] holds bf16 term t (lo,
+// mid, hi) of the lane's probabilities of head qh at rows 16g + 4qg + 0..3 of
+// its rows for g = 2s (words 0-1) and 2s + 1 (words 2-3), two per word, where
+// the scores left them: the A operand of 32-row k-step s (k = 8qg + e <-> row
+// 16(2s) + 4qg + e for e < 4, 16(2s + 1) + 4qg + e - 4 above), and the B
+// operand is read transposed in the same k order: rows 4qg .. 4qg + 3 and
+// 16 + 4qg .. 16 + 4qg + 3 of the k-step (V pieces swizzled by
+// vswz<64, true>).  vo[j] is the lane's byte offset for columns 16j ..
+// 16j + 15 within its wavefront's rows (v_rows_offsets).  No P goes through
+// LDS: at D = 64 the P tile is 16 x 256 and every wavefront read all of it in
+// pv_tile_cols.
+template <int GP>
+__device__ __forceinline__ void pv_tile_rows(floatx4_t (&acc)[4], const u32x4_t (&pa)[2][3],
+                                             const char* slot, int w, const uint32_t (&vo)[4]) {
+  using C = Matched<64, GP>;
+  static_assert(C::kNG == 4 && C::kTW == 64, "D = 64 geometry");
+  const uint32_t vb = lds_address(slot) + w * C::kSlot;
+  auto step = [&](auto S) __attribute__((always_inline)) {
+    constexpr int s = decltype(S)::value;
+    constexpr int kLo = 32 * s * C::kPitch, kHi = kLo + 16 * C::kPitch;
+    short4_t lo[4], hi[4];
 #pragma unroll
-    for (int j = 0; j < P::kNBW; ++j)
+    for (int j = 0; j < 4; ++j) {
+      lo[j] = lds_read_tr_at<kLo>(vb + vo[j]);
+      hi[j] = lds_read_tr_at<kHi>(vb + vo[j]);
+    }
+    lds_settle(lo, hi);
+    bf16x8_t a[3];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        // ps terms 2, 1, 0 are hi, mid, lo
-        const float hi = ch[4 * P::kNBW + j][r] + ch[5 * P::kNBW + j][r];
-        const float mid = ch[2 * P::kNBW + j][r] + ch[3 * P::kNBW + j][r];
-        const float lo = ch[0 * P::kNBW + j][r] + ch[1 * P::kNBW + j][r];
-        acc[j][r] += (hi + mid) + lo;
-      }
-  }
+    for (int t = 0; t < 3; ++t) a[t] = __builtin_bit_cast(bf16x8_t, pa[s][t]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8_t bv = __builtin_bit_cast(
+          bf16x8_t, u32x4_t{__builtin_bit_cast(u32x2_t, lo[j])[0], __builtin_bit_cast(u32x2_t, lo[j])[1],
+                            __builtin_bit_cast(u32x2_t, hi[j])[0], __builtin_bit_cast(u32x2_t, hi[j])[1]});
+#pragma unroll
+      for (int t = 0; t < 3; ++t)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], bv, acc[j], 0, 0, 0);
+    }
+  };
+  for_each_step(step, std::make_integer_sequence<int, 2>{});
+  // The rescale of the next tile reads acc behind a branch (the compiler's
+  // wait states there have been too few before).
+  mfma_result_barrier(acc);
+}
+
+// The lane's byte offsets for pv_tile_rows: row 4qg + qh / 4 of a k-step's
+// first 16 (the transposed read's source row of lane 4c + b of its 16-lane
+// group is row c of the group's block), columns 16j + 4(qh % 4) .. + 3.
+template <int GP>
+__device__ __forceinline__ void v_rows_offsets(uint32_t (&vo)[4], int lane) {
+  const int qh = lane & 15, qg = lane >> 4;
+  const int row = 4 * qg + (qh >> 2);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    vo[j] = uint32_t(row * Matched<64, GP>::kPitch + v_read_offset<64, true>(16 * j, lane, row));
 }
 
 // --------------------------------------- multi-tile partition, loader waves
@@ -273,7 +301,13 @@ __device__ __forceinline__ void pv_tile_cols(floatx4_t (&acc)[TileP<D>::kNBW],
 // probabilities (three bf16 terms for the base and fixed-split protocols) to
 // LDS, and compute wavefront w multiplies the whole tile's P by V columns
 // [w D/4, (w + 1) D/4) (pv_tile_cols).  The accumulator takes D/16 VGPRs, and
-// O needs no cross-wave reduction at the end.  At D = 64, kHeads = H = 2 or 4
+// O needs no cross-wave reduction at the end.  At D = 64 in the base and
+// fixed-split protocols (three bf16 terms: a 16 x 256 P tile that every
+// wavefront would read whole) each wavefront instead multiplies its own rows'
+// P, kept in registers, by all 64 columns (pv_tile_rows), and the four
+// wavefronts' O are summed where a partition ends (kRowsPV: the paired A/B on
+// the edge-coverage batches at D 64 measured x0.963 for hip_base and x0.967
+// for hip_splitk, another fp32 summation order).  At D = 64, kHeads = H = 2 or 4
 // serves H adjacent kv heads (base and fixed-split protocols): row R of a
 // tile is token R / H of kv head H kh + R % H, a token's H rows one contiguous
 // read of 128 H bytes; query head e G + g scores only the rows of its own kv
@@ -333,6 +367,8 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   constexpr int TILE = C::kTile;        // tile rows: TILE / kHeads tokens of kHeads kv heads
   constexpr int TTOK = TILE / kHeads;   // tokens per tile
   constexpr int kTerms = kMatchedArith ? 1 : 3;
+  // D = 64 with three terms: P V by rows (pv_tile_rows), P kept in registers.
+  constexpr bool kRowsPV = D == 64 && kTerms == 3;
   constexpr int kStage = TILE * D * 2;  // bytes of one K or V stage
   constexpr int kCopies = C::kDma;      // 1 KiB copies per loader, tensor and tile
   constexpr int kPieces = D / 8;        // 16-byte pieces per K row
@@ -341,7 +377,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   __shared__ MatchedShared<D, GP> sm;
   __shared__ __attribute__((aligned(16))) char ks[2][kStage];
   __shared__ __attribute__((aligned(16))) char vs[2][kStage];
-  __shared__ __attribute__((aligned(16))) char ps[kTerms][16 * P::kPitch];
+  __shared__ __attribute__((aligned(16))) char ps[kRowsPV ? 1 : kTerms][kRowsPV ? 16 : 16 * P::kPitch];
   __shared__ __attribute__((aligned(16))) int slens[kMaxOrderedBatch + 4];
 
   // The fixed-split protocol writes the (m, l, acc) of each T-token partition
@@ -365,7 +401,10 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   constexpr bool kFlush = kMode == kSplit || kMode == kSplitPart || kMode == kMatchedWalk;
   constexpr int kFbPitch = D + 4;                 // floats per head row of fb
   constexpr int kFbPasses = GP * D >= 1024 ? GP * D / 1024 : 1;  // 16-byte stores per loader lane
-  __shared__ __attribute__((aligned(16))) float fb[kFlush ? GP * kFbPitch : 4];
+  // kRowsPV: one copy of fb per compute wavefront (its O_w), summed by the readers
+  // as (w0 + w1) + (w2 + w3); the base protocol's epilogue uses them too.
+  constexpr int kFbCopies = kRowsPV ? 4 : 1;
+  __shared__ __attribute__((aligned(16))) float fb[kFlush || kRowsPV ? kFbCopies * GP * kFbPitch : 4];
   __shared__ float fm[16];
   constexpr int kEmptyMode = kMatchedArith ? kMatched : (kFlush ? kSplit : kMode);  // write_empty_partition's
   const int p = kWalk ? int(blockIdx.x) * wf : int(blockIdx.x);
@@ -402,7 +441,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       const int pos = 64 * (kCopies * w + i) + lane;
       const int row = pos / kPieces;
       koff[i] = (tile_row_elems<D, kHeads>(row, int(RS)) + 8 * ((pos % kPieces) ^ kswz<D>(row))) * 2;
-      voff[i] = v_copy_offset<D, GP, kHeads>(i, lane, w, int(RS));
+      voff[i] = v_copy_offset<D, GP, kHeads, kRowsPV>(i, lane, w, int(RS));
     }
     pw.settle();
     auto issue = [&](int ti, bool is_k) __attribute__((always_inline)) {
@@ -429,7 +468,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     // read would count the copies in flight) and stored after the next K
     // copies are issued.  In-order completion then lets the next wait for K
     // cover the stores too.
-    u32x4_t fx[kFbPasses];
+    u32x4_t fx[kFbPasses * kFbCopies];  // pass i, copy c at fx[i * kFbCopies + c]
     u32x4_t fd[kMatchedArith ? kFbPasses : 1];  // denominator shares of the pass's head
     uint32_t fmx = 0, fl[4] = {0, 0, 0, 0};
     auto flush_read = [&]() __attribute__((always_inline)) {
@@ -437,8 +476,11 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       for (int i = 0; i < kFbPasses; ++i) {
         const int f = (i * 256 + w * 64 + lane) * 4;
         const int h = min(f / D, GP - 1);  // rows past GP are never stored
-        fx[i] = lds_read16_at(lds_address(reinterpret_cast<const char*>(fb)) +
-                              uint32_t(h * kFbPitch + f % D) * 4);
+#pragma unroll
+        for (int c = 0; c < kFbCopies; ++c)
+          fx[i * kFbCopies + c] =
+              lds_read16_at(lds_address(reinterpret_cast<const char*>(fb)) +
+                            uint32_t(c * GP * kFbPitch + h * kFbPitch + f % D) * 4);
         if constexpr (kMatchedArith) {
           const int hh = h & 15;
 #pragma unroll
@@ -456,6 +498,19 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       lds_wait(fx);
       if constexpr (kMatchedArith) lds_wait(fd);
       asm volatile("" : "+v"(fmx), "+v"(fl[0]), "+v"(fl[1]), "+v"(fl[2]), "+v"(fl[3]));
+      if constexpr (kRowsPV) {
+        // The partition's accumulators: the four compute wavefronts' rows.
+#pragma unroll
+        for (int i = 0; i < kFbPasses; ++i) {
+          u32x4_t sum;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const auto x = [&](int c) { return __uint_as_float(fx[i * kFbCopies + c][e]); };
+            sum[e] = __float_as_uint((x(0) + x(1)) + (x(2) + x(3)));
+          }
+          fx[i] = sum;
+        }
+      }
     };
     auto flush_store = [&](int part) __attribute__((always_inline)) {
 #pragma unroll
@@ -612,9 +667,22 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     for (int i = 0; i < C::kNG * C::kCH; ++i) kr[i] = lds_read16_at(kaddr[i] + stage);
   };
 
-  floatx4_t acc[P::kNBW];  // O[head 4*qg + r][64w + 16j + qh]
+  // O[head 4*qg + r][64w + 16j + qh] over the tile's rows; with kRowsPV,
+  // O_w[head 4*qg + r][16j + qh] over this wavefront's rows only.
+  constexpr int kAccB = kRowsPV ? 4 : P::kNBW;
+  floatx4_t acc[kAccB];
 #pragma unroll
-  for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < kAccB; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  u32x4_t pa[kRowsPV ? C::kNG / 2 : 1][3];  // kRowsPV: the tile's P terms (pv_tile_rows)
+  uint32_t vo[4] = {0u, 0u, 0u, 0u};
+  if constexpr (kRowsPV) v_rows_offsets<GP>(vo, lane);
+  // kRowsPV: O of head h, column col, as (O_0 + O_1) + (O_2 + O_3) from the
+  // wavefronts' copies in fb (the loaders' flush_read sums the same way).
+  auto rows_sum = [&](int h, int col) __attribute__((always_inline)) {
+    const float* x = fb + h * kFbPitch + col;
+    constexpr int kCopy = GP * kFbPitch;
+    return (x[0] + x[kCopy]) + (x[2 * kCopy] + x[3 * kCopy]);
+  };
   float m4[4];             // running max of heads 4*qg + r
 #pragma unroll
   for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
@@ -658,6 +726,11 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
       const int h = 4 * qg + r;
       const float den = (sm.lsum[0][h] + sm.lsum[1][h]) + (sm.lsum[2][h] + sm.lsum[3][h]);
       if (mS[r].live) mT[r] = fmaf(den, mS[r].b, mT[r] * mS[r].a);
+      // kRowsPV: the partition's accumulators are in fb only after this barrier too.
+      if constexpr (kRowsPV) {
+        if (mS[r].live && h < Gs)
+          mO[0][r] = fmaf(rows_sum(h, w * P::kCols + qh), mS[r].b, mO[0][r] * mS[r].a);
+      }
     }
   };
 
@@ -790,10 +863,18 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
             }
           }
         }
+        if constexpr (kRowsPV) {
 #pragma unroll
-        for (int t = 0; t < 3; ++t)
-          *reinterpret_cast<u32x2_t*>(ps[t] + pofs) =
-              u32x2_t{qh < Gs ? t3[t][0] : 0u, qh < Gs ? t3[t][1] : 0u};
+          for (int t = 0; t < 3; ++t) {
+            pa[g >> 1][t][2 * (g & 1)] = qh < Gs ? t3[t][0] : 0u;
+            pa[g >> 1][t][2 * (g & 1) + 1] = qh < Gs ? t3[t][1] : 0u;
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < 3; ++t)
+            *reinterpret_cast<u32x2_t*>(ps[t] + pofs) =
+                u32x2_t{qh < Gs ? t3[t][0] : 0u, qh < Gs ? t3[t][1] : 0u};
+        }
         continue;
       }
       float pr[4];
@@ -820,7 +901,13 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
           t3[1][h2] = qh < Gs ? mid : 0u;
           t3[2][h2] = qh < Gs ? hi : 0u;
         }
-        if (!kSkipPadRows<D, kTerms> || qh < Gs) {
+        if constexpr (kRowsPV) {
+#pragma unroll
+          for (int t = 0; t < 3; ++t) {
+            pa[g >> 1][t][2 * (g & 1)] = t3[t][0];
+            pa[g >> 1][t][2 * (g & 1) + 1] = t3[t][1];
+          }
+        } else if (!kSkipPadRows<D, kTerms> || qh < Gs) {
 #pragma unroll
           for (int t = 0; t < 3; ++t)
             *reinterpret_cast<u32x2_t*>(ps[t] + pofs) = u32x2_t{t3[t][0], t3[t][1]};
@@ -830,12 +917,15 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     l_own = l_own * a_own + psum;
     if (ti != count - 1 && __builtin_amdgcn_ballot_w64(moved)) {
 #pragma unroll
-      for (int j = 0; j < P::kNBW; ++j)
+      for (int j = 0; j < kAccB; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] *= alpha[r];
     }
     lds_barrier();  // B2(ti): P rows written, V(ti) and K(ti - 1) in LDS
-    pv_tile_cols<D, GP, kTerms>(acc, ps, vs[ti & 1], lane, w, Gs);
+    if constexpr (kRowsPV)
+      pv_tile_rows<GP>(acc, pa, vs[ti & 1], w, vo);
+    else
+      pv_tile_cols<D, GP, kTerms>(acc, ps, vs[ti & 1], lane, w, Gs);
     if (ti > 0) read_k(ti - 1);
 
     if constexpr (kFlush) {
@@ -852,16 +942,18 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
         for (int r = 0; r < 4; ++r) {
           const int h = 4 * qg + r;
           if (h >= Gs) break;
-          float* row = fb + h * kFbPitch + w * P::kCols + qh;
+          // kRowsPV: this wavefront's O_w, all columns, into its copy of fb.
+          float* row = fb + (kRowsPV ? w * GP * kFbPitch : w * P::kCols) + h * kFbPitch + qh;
 #pragma unroll
-          for (int j = 0; j < P::kNBW; ++j) row[16 * j] = acc[j][r];
+          for (int j = 0; j < kAccB; ++j) row[16 * j] = acc[j][r];
           if (w == 0 && qh == 0) fm[h] = m4[r];
         }
         if (merge_out) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             mS[r] = ml_step(m4[r], mM[r]);
-            if (mS[r].live) {
+            // kRowsPV: merged after the next barrier (merge_denominators).
+            if (!kRowsPV && mS[r].live) {
 #pragma unroll
               for (int j = 0; j < P::kNBW; ++j) mO[j][r] = fmaf(acc[j][r], mS[r].b, mO[j][r] * mS[r].a);
             }
@@ -876,7 +968,7 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
           if (merge_out) merge_denominators();
         }
 #pragma unroll
-        for (int j = 0; j < P::kNBW; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < kAccB; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int r = 0; r < 4; ++r) m4[r] = -INFINITY;
         m_own = -INFINITY;
@@ -911,9 +1003,20 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
   }
   if constexpr (kFlush) return;  // partition p was written by the flush after its first tile
 
-  // ---- epilogue: denominators over the waves; O needs no reduction
+  // ---- epilogue: denominators over the waves; O needs no reduction (with
+  // kRowsPV, the sum of the wavefronts' copies in fb)
   const float l = sum_rows(l_own);
   if (lane < 16) sm.lsum[w][lane] = l;
+  if constexpr (kRowsPV) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * qg + r;
+      if (h >= Gs) break;
+      float* row = fb + w * GP * kFbPitch + h * kFbPitch + qh;
+#pragma unroll
+      for (int j = 0; j < kAccB; ++j) row[16 * j] = acc[j][r];
+    }
+  }
   lds_barrier();
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -925,8 +1028,13 @@ cols_loader_kernel(const int32_t* __restrict__ table, const int32_t* __restrict_
     if constexpr (kMode == kBase) {
       // acc / denom, 0 for an empty sequence (kernels.py:40).
       uint16_t* dst = out + (int64_t(b) * Hq + qb + h) * D + col;
+      if constexpr (kRowsPV) {
+        static_assert(P::kNBW == 1, "one 16-column block per wavefront at D = 64");
+        dst[0] = uint16_t(bf16_bits(rows_sum(h, col) / safe));
+      } else {
 #pragma unroll
-      for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = uint16_t(bf16_bits(acc[j][r] / safe));
+        for (int j = 0; j < P::kNBW; ++j) dst[16 * j] = uint16_t(bf16_bits(acc[j][r] / safe));
+      }
     } else {
       const int64_t orow = (int64_t(b) * Hq + qb + h) * splits + p;
       const float inv = rcp_fast(safe);

@@ -172,6 +172,56 @@ def test_v_rows_swizzle_round_trips_and_transposed_reads_are_conflict_free(dim):
                     assert len(chunks) == 32, (step, second, col0, half)
 
 
+def vswz_rows(row):
+    """vswz<64, true>: the V swizzle of the D 64 kernels that multiply P V by rows."""
+    return 2 * (((row >> 1) & 1) | (((row >> 2) & 1) << 1))
+
+
+def rows_read_row(lane, step, second):
+    """Row of its wavefront's 64 that `lane` reads in a transposed read of the row-wise
+    P V (pv_tile_rows): rows 4(L/16) + (L%16)/4 (+16 in the second read) of k-step
+    `step`, in the k order of the probabilities left in the score registers."""
+    return 32 * step + 4 * (lane >> 4) + ((lane & 15) >> 2) + (16 if second else 0)
+
+
+def _rows_chunks(swizzle, read):
+    """8-byte LDS chunks (mod 256 bytes) per half-wavefront read of the row-wise P V,
+    after checking that every read finds the logical columns it asks for."""
+    pitch, rows = 128, 64
+    stored = {(r, p ^ swizzle(r)): p for r in range(rows) for p in range(8)}
+    assert len(stored) == rows * 8
+    out = []
+    for step in range(2):
+        for second in (False, True):
+            for col0 in range(0, 64, 16):
+                for half in (0, 32):
+                    chunks = set()
+                    for lane in range(half, half + 32):
+                        row = read(lane, step, second)
+                        b = lane & 3
+                        pos = ((col0 >> 3) + (b >> 1)) ^ swizzle(row)
+                        assert stored[(row, pos)] == (col0 + 4 * b) // 8
+                        chunks.add(((row * pitch + 16 * pos + 8 * (b & 1)) % 256) // 8)
+                    out.append(len(chunks))
+    return out
+
+
+def test_row_wise_v_swizzle_is_conflict_free_where_the_column_swizzle_is_not():
+    """The row-wise reads put rows 0-7 of a 16-row group in one half-wavefront (the
+    column-split reads put rows 0-3 and 8-11 there): with bit 2 of the row in the
+    swizzle every half-wavefront read hits 32 distinct 8-byte chunks of the 256 bytes
+    the LDS serves per clock; the column swizzle (bit 3) would give 2-way conflicts."""
+    assert set(_rows_chunks(vswz_rows, rows_read_row)) == {32}
+    assert set(_rows_chunks(lambda r: vswz(64, r), rows_read_row)) == {16}
+    # The operand k order: lane (qg, qh) supplies k = 8 qg + e for rows 4 qg + e
+    # (e < 4) and 16 + 4 qg + e - 4, which is where the scores of 16-row groups 2s and
+    # 2s + 1 left that lane's probabilities (rows 16 g + 4 qg + r).
+    for lane in range(64):
+        qg, c = lane >> 4, (lane & 15) >> 2
+        assert rows_read_row(lane, 0, False) == 16 * 0 + 4 * qg + c
+        assert rows_read_row(lane, 1, True) == 16 * 3 + 4 * qg + c
+
+
 def kswz(dim, row):
     return row & 15 if dim >= 128 else (row >> 1) & 7
 
